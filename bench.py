@@ -1,0 +1,243 @@
+"""Benchmark: full v1 Bi-Real binary UNet forward, 32x32x120 patches, batch 1024.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024] [--no-cpu]
+
+One step = one batched forward of `--batch` synthetic patches (seeded blob at
+base 16, x ~ N(0,1)) with the input already resident in HBM; K steps are
+timed between device synchronisations.  Prints ONE JSON line on stdout:
+
+  value         patches/s over the K timed steps
+  roofline      the dominant kernel (the order-exact real first conv): FP32
+                FMA work per launch / its mean hipEvent-measured duration
+                against the published FP32 vector peak
+  bconv         the 17 binary convs: binary-op/s (2 per bit-MAC, border taps
+                counted) against the VALU-popcount roofline
+  fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
+                32x32, batch 1024 (the benchmark's fused-kernel config)
+  cpu_baseline  the reference C CLI (oracle/_ref/bnn_infer, built from the
+                reference sources) timed on this host: median of reps of one
+                patch, like csrc/main.c:55-61; falls back to the checker
+                (kind "port") where the reference build is absent
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import subprocess
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+# MI355X published peaks
+PEAK_FP32_FLOPS = 157.3e12          # vector FP32 (with packed math)
+PEAK_HBM = 8.0e12
+
+
+def valu_binop_peak() -> float:
+    # 256 CU x 64 lanes x 2.4 GHz 32-bit lane-ops; v_bitop3 + v_bcnt per 32
+    # bit-MACs = 16 bit-MACs per lane-op = 32 binary ops per lane-op
+    return 256 * 64 * 2.4e9 * 16 * 2
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(blob_path: str, budget_s: float) -> dict:
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    from oracle.oracle import REF_CLI
+    env = dict(os.environ, OMP_NUM_THREADS=str(cores))
+    if os.path.exists(REF_CLI):
+        # calibrate with a short run, then size the sample to the budget
+        def run(reps):
+            with tempfile.TemporaryDirectory() as td:
+                r = subprocess.run([REF_CLI, blob_path, "rand", os.path.join(td, "o.bin"), "32", "32", str(reps)],
+                                   capture_output=True, text=True, env=env, timeout=600)
+            if r.returncode != 0:
+                raise RuntimeError(r.stderr)
+            m = re.search(r"# forward\s*:\s*([\d.]+) ms", r.stderr)
+            return float(m.group(1))
+        t1 = run(3)
+        reps = max(5, min(2000, int(budget_s * 1000.0 / max(t1, 1e-3))))
+        med = run(reps)
+        return {"value": round(1000.0 / med, 2), "unit": "patches/s", "cores": cores, "kind": "reference",
+                "sample": f"reference bnn_infer (csrc/main.c) built from its sources, one 32x32x120 patch, "
+                          f"median of {reps} reps = {med:.3f} ms/patch, OMP_NUM_THREADS={cores}"}
+    import numpy as np
+    from bnns_to_c_amd import synth
+    from oracle.oracle import Oracle
+    model = Oracle().parse(open(blob_path, "rb").read())
+    x = synth.make_input(7, 1)
+    t0 = time.perf_counter()
+    model.forward_batch(x, parallel=False)
+    t1 = time.perf_counter() - t0
+    n = max(4, min(4096, int(budget_s / max(t1, 1e-4))))
+    x = synth.make_input(7, n)
+    t0 = time.perf_counter()
+    model.forward_batch(x, parallel=False)
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "patches/s", "cores": cores, "kind": "port",
+            "sample": f"CPU restatement (oracle/), {n} patches of 32x32x120 in sequence, "
+                      f"OMP_NUM_THREADS={cores}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1024)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the patch batch shards with no exchange "
+              "(see DESIGN.md), and this build runs on one GPU; use --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from bnns_to_c_amd import blob, engine, synth
+
+    N, H, W = args.batch, 32, 32
+    b = synth.make_blob(seed=0, base=16)
+    td = tempfile.mkdtemp()
+    blob_path = os.path.join(td, "bench.blob")
+    blob.write(b, blob_path)
+    eng = engine.Engine(blob_path)
+    x = torch.from_numpy(synth.make_input(1, N)).cuda()
+    y = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step():
+        eng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1)
+    ms_per_step = ev_ms / args.steps
+    value = N * args.steps / (ev_ms / 1e3)
+    log(f"forward: {ms_per_step:.4f} ms/step (events), wall {wall * 1e3 / args.steps:.4f} ms/step, "
+        f"{value:,.0f} patches/s")
+
+    # per-kernel times: the same forward with an event pair around every kernel
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    engine.prof_enable(False)
+    recs = engine.prof_records()
+    agg = {}
+    for lab, op, ms, work in recs:
+        a = agg.setdefault(lab, [op, 0.0, 0, work])
+        a[1] += ms
+        a[2] += 1
+    kernels = []
+    for lab, (op, ms, cnt, work) in agg.items():
+        mean = ms / cnt
+        if op == "conv_real":
+            rate = 2 * work / (mean / 1e3)
+            kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "tflops": round(rate / 1e12, 3),
+                            "frac": round(rate / PEAK_FP32_FLOPS, 4)})
+        else:
+            rate = 2 * work / (mean / 1e3)
+            kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "tbinops": round(rate / 1e12, 2),
+                            "frac": round(rate / valu_binop_peak(), 4)})
+    for k in kernels:
+        log(f"  {k['label']:10s} {k['op']:10s} {k['ms']*1e3:9.1f} us  frac {k['frac']:.3f}")
+    real = next(k for k in kernels if k["op"] == "conv_real")
+    real_work = agg[real["label"]][3]
+    real_flops = 2 * real_work
+    achieved = real_flops / (real["ms"] / 1e3)
+    bin_ms = sum(k["ms"] for k in kernels if k["op"] != "conv_real")
+    bin_work = sum(agg[k["label"]][3] for k in kernels if k["op"] != "conv_real")
+    bin_rate = 2 * bin_work / (bin_ms / 1e3)
+
+    # fused bconv + fold + 2x2 max-pool, 128->128 at 32x32, batch 1024
+    C = 128
+    a = synth.make_bits(30, N, H, W, C)
+    w = synth.make_signs(31, C, C)
+    L = engine.ConvLayer(blob.pack_kidx(w), C, C, synth.make_thresholds(32, C, 288),
+                         synth.make_thresholds(33, C, 288))
+    da = torch.from_numpy(a).cuda()
+    act = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
+    engine.pack_act_device(da.data_ptr(), act.data_ptr(), N, C, H, W, sp)
+    del da
+    skip = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
+    down = torch.empty((N, H // 2, W // 2, C // 32), dtype=torch.int32, device="cuda")
+    reps = 20
+    for _ in range(3):
+        L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pool_ms = e0.elapsed_time(e1) / reps
+    pool_bitmacs = N * C * H * W * C * 9
+    pool_rate = 2 * pool_bitmacs / (pool_ms / 1e3)
+    log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, "
+        f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
+    L.close()
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(blob_path, args.cpu_budget)
+        log(f"cpu baseline: {cpu}")
+    eng.close()
+
+    out = {
+        "metric": "patches/s full UNet @32x32x120 b1024; bconv binary-op/s as % of roofline",
+        "value": round(value, 1),
+        "unit": "patches/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 first conv + xnor-popcount (u32) binary convs",
+        "data": "synthetic: seeded random blob (base 16, Bernoulli sign weights, U[-fan_in/4,fan_in/4] "
+                "ge/lt thresholds) and x ~ N(0,1) patches, resident in HBM",
+        "config": {"workload": "v1 Bi-Real binary UNet forward (nearest upsampler), 32x32x120 patches",
+                   "batch": N, "H": H, "W": W, "n_bands": 120, "n_classes": 3, "base_channels": 16},
+        "roofline": {"bound": "valu", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32 FMA)",
+                     "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": None,
+                     "algorithmic": f"{real_flops:.4g} FLOP/launch = 2 x 17,694,720 MAC x {N} patches"},
+        "bconv": {"kernels": 17, "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
+                  "frac": round(bin_rate / valu_binop_peak(), 4), "ms": round(bin_ms, 5),
+                  "unit": "binary-op/s (2 per bit-MAC, border taps counted)"},
+        "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
+                       "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
+                       "frac": round(pool_rate / valu_binop_peak(), 4)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

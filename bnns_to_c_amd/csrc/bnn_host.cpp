@@ -1,0 +1,990 @@
+// bnn_host.cpp - libbnn_hip.so host side: blob v1 parsing, device model,
+// the batched forward, the debug/profiling paths and the C ABI.
+//
+// Blob layout and record order: python/bnn2c/blob.py:36-114,159-200 read the
+// way csrc/bnn_model.c:27-96 reads it (same checks, plus version == 1 and
+// upsampler == 0, which the reference reads but never checks).  The forward
+// follows csrc/bnn_model.c:150-253 stage for stage; every stage runs as one
+// kernel on the model's HIP stream over a batch of N independent patches.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "bnn_kernels.h"
+#include "bnn_model.h"
+#include "bnn_prof.h"
+
+using namespace bnn;
+
+// ------------------------------------------------------------------ errors
+namespace {
+thread_local std::string g_err;
+
+int set_err(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                  \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return set_err(BNN_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                     __LINE__);                                                        \
+  } while (0)
+
+[[noreturn]] void die() {
+  fprintf(stderr, "%s\n", g_err.c_str());
+  exit(1);
+}
+
+// ------------------------------------------------------------ blob reader
+struct Reader {
+  std::vector<uint8_t> buf;
+  size_t off = 0;
+  bool bad = false;
+
+  bool fail(const char* what) {
+    if (!bad) set_err(BNN_EBLOB, "%s", what);
+    bad = true;
+    return false;
+  }
+  bool raw(void* dst, size_t n) {
+    if (bad) return false;
+    if (n > buf.size() - off) return fail("short read");
+    memcpy(dst, buf.data() + off, n);
+    off += n;
+    return true;
+  }
+  int i32() {
+    int v = 0;
+    raw(&v, 4);
+    return v;
+  }
+  // allocate count*elem bytes after checking they are present in the blob
+  template <class T>
+  T* arr(long long count) {
+    if (bad) return nullptr;
+    if (count < 0) { fail("negative record dimension"); return nullptr; }
+    const long double need = (long double)count * sizeof(T);
+    if (need > (long double)(buf.size() - off)) { fail("short read"); return nullptr; }
+    T* p = (T*)malloc(count ? (size_t)count * sizeof(T) : 1);
+    if (!p) { fail("out of memory"); return nullptr; }
+    raw(p, (size_t)count * sizeof(T));
+    return p;
+  }
+};
+
+constexpr int TAG_BIN = 1, TAG_REAL = 2, TAG_ACT = 3, TAG_HEAD = 4;
+
+void read_conv(Reader& r, Conv* c) {
+  memset(c, 0, sizeof *c);
+  c->tag = r.i32();
+  c->Cout = r.i32(); c->Cin = r.i32(); c->kh = r.i32(); c->kw = r.i32();
+  c->pad = r.i32(); c->stride = r.i32();
+  if (r.bad) return;
+  if (c->tag == TAG_BIN) {
+    c->nwords = r.i32();
+    c->packed = r.arr<uint64_t>((long long)c->Cout * c->nwords);
+  } else if (c->tag == TAG_REAL) {
+    if (c->Cout < 0 || c->Cin < 0 || c->kh < 0 || c->kw < 0) { r.fail("negative record dimension"); return; }
+    c->wsign = r.arr<int8_t>((long long)c->Cout * c->Cin * c->kh * c->kw);
+    c->alpha = r.arr<float>(c->Cout);
+  } else {
+    char m[64];
+    snprintf(m, sizeof m, "bad conv tag %d", c->tag);
+    r.fail(m);
+  }
+}
+
+void read_act(Reader& r, Act* a) {
+  memset(a, 0, sizeof *a);
+  const int tag = r.i32();
+  if (!r.bad && tag != TAG_ACT) {
+    char m[64];
+    snprintf(m, sizeof m, "bad act tag %d", tag);
+    r.fail(m);
+    return;
+  }
+  a->kind = r.i32();
+  a->C = r.i32();
+  if (r.bad) return;
+  if (a->C < 0) { r.fail("negative record dimension"); return; }
+  if ((long double)a->C * 16 > (long double)(r.buf.size() - r.off)) { r.fail("short read"); return; }
+  if (a->kind == 0) {  // any other kind is the real fold (csrc/bnn_model.c:114-124)
+    a->type = r.arr<int32_t>(a->C); a->t = r.arr<int32_t>(a->C);
+    a->lo = r.arr<int32_t>(a->C); a->hi = r.arr<int32_t>(a->C);
+  } else {
+    a->A = r.arr<float>(a->C); a->B = r.arr<float>(a->C);
+    a->slope = r.arr<float>(a->C); a->rsign = r.arr<float>(a->C);
+  }
+}
+
+void free_conv(Conv* c) { free(c->packed); free(c->wsign); free(c->alpha); }
+void free_act(Act* a) {
+  free(a->type); free(a->t); free(a->lo); free(a->hi);
+  free(a->A); free(a->B); free(a->slope); free(a->rsign);
+}
+void free_host(Model* m) {
+  for (int i = 0; i < 4; ++i) {
+    free_conv(&m->enc_conv1[i]); free_conv(&m->enc_conv2[i]);
+    free_act(&m->enc_act1[i]); free_act(&m->enc_act2_skip[i]); free_act(&m->enc_act2_down[i]);
+    free_conv(&m->dec_conv1[i]); free_conv(&m->dec_conv2[i]);
+    free_act(&m->dec_act1[i]); free_act(&m->dec_act2[i]);
+  }
+  free_conv(&m->bott_conv1); free_conv(&m->bott_conv2);
+  free_act(&m->bott_act1); free_act(&m->bott_act2);
+  free(m->head_W); free(m->head_bias);
+}
+
+int parse_blob(const char* path, Model** out) {
+  *out = nullptr;
+  FILE* f = fopen(path, "rb");
+  if (!f) return set_err(BNN_EBLOB, "cannot open %s", path);
+  Reader r;
+  uint8_t chunk[1 << 16];
+  size_t got;
+  while ((got = fread(chunk, 1, sizeof chunk, f)) > 0) r.buf.insert(r.buf.end(), chunk, chunk + got);
+  fclose(f);
+  if (r.buf.size() < 4) return set_err(BNN_EBLOB, "short read");
+  if (memcmp(r.buf.data(), "BNNC", 4) != 0) return set_err(BNN_EBLOB, "bad magic");
+  r.off = 4;
+  Model* m = (Model*)calloc(1, sizeof(Model));
+  if (!m) return set_err(BNN_EBLOB, "out of memory");
+  m->version = r.i32(); m->base_channels = r.i32();
+  m->n_bands = r.i32(); m->n_classes = r.i32(); m->upsampler = r.i32();
+  if (!r.bad && m->version != 1) {
+    char msg[64];
+    snprintf(msg, sizeof msg, "unsupported blob version %d", m->version);
+    r.fail(msg);
+  }
+  if (!r.bad && m->upsampler != 0) {
+    char msg[64];
+    snprintf(msg, sizeof msg, "unsupported upsampler %d (v1 engine runs nearest only)", m->upsampler);
+    r.fail(msg);
+  }
+  for (int i = 0; i < 4; ++i) {
+    read_conv(r, &m->enc_conv1[i]); read_act(r, &m->enc_act1[i]);
+    read_conv(r, &m->enc_conv2[i]); read_act(r, &m->enc_act2_skip[i]);
+    read_act(r, &m->enc_act2_down[i]);
+  }
+  read_conv(r, &m->bott_conv1); read_act(r, &m->bott_act1);
+  read_conv(r, &m->bott_conv2); read_act(r, &m->bott_act2);
+  for (int i = 0; i < 4; ++i) {
+    read_conv(r, &m->dec_conv1[i]); read_act(r, &m->dec_act1[i]);
+    read_conv(r, &m->dec_conv2[i]); read_act(r, &m->dec_act2[i]);
+  }
+  const int tag = r.i32();
+  if (!r.bad && tag != TAG_HEAD) {
+    char msg[64];
+    snprintf(msg, sizeof msg, "bad head tag %d", tag);
+    r.fail(msg);
+  }
+  m->head_Cout = r.i32(); m->head_Cin = r.i32();
+  m->head_W = r.arr<float>((long long)m->head_Cout * m->head_Cin);
+  m->head_bias = r.arr<float>(m->head_Cout);
+  if (!r.bad && r.off != r.buf.size()) r.fail("trailing bytes in blob");
+  if (r.bad) {
+    free_host(m);
+    free(m);
+    return BNN_EBLOB;
+  }
+  *out = m;
+  return BNN_OK;
+}
+
+// The chain the forward assumes; the reference trusts the blob instead.
+bool conv_ok(const Conv& c, int tag, int cin) {
+  return c.tag == tag && c.Cin == cin && c.Cout > 0 && c.kh == 3 && c.kw == 3 && c.pad == 1 &&
+         c.stride == 1 && (tag != TAG_BIN || c.nwords == (cin * 9 + 63) / 64);
+}
+bool act_ok(const Act& a, bool real, int c) { return a.C == c && (real ? a.kind != 0 : a.kind == 0); }
+
+int validate(const Model* m) {
+  if (m->n_bands <= 0 || m->n_classes <= 0) return set_err(BNN_EBLOB, "bad n_bands/n_classes");
+  int c = m->n_bands, skipc[4];
+  for (int i = 0; i < 4; ++i) {
+    const Conv &c1 = m->enc_conv1[i], &c2 = m->enc_conv2[i];
+    if (!conv_ok(c1, i == 0 ? TAG_REAL : TAG_BIN, c)) return set_err(BNN_EBLOB, "enc%d.conv1 does not chain", i + 1);
+    if (!act_ok(m->enc_act1[i], i == 0, c1.Cout)) return set_err(BNN_EBLOB, "enc%d.act1 does not chain", i + 1);
+    if (!conv_ok(c2, TAG_BIN, c1.Cout)) return set_err(BNN_EBLOB, "enc%d.conv2 does not chain", i + 1);
+    if (!act_ok(m->enc_act2_skip[i], false, c2.Cout) || !act_ok(m->enc_act2_down[i], false, c2.Cout))
+      return set_err(BNN_EBLOB, "enc%d.act2 does not chain", i + 1);
+    skipc[i] = c = c2.Cout;
+  }
+  if (!conv_ok(m->bott_conv1, TAG_BIN, c) || !act_ok(m->bott_act1, false, m->bott_conv1.Cout))
+    return set_err(BNN_EBLOB, "bottleneck.conv1 does not chain");
+  c = m->bott_conv1.Cout;
+  if (!conv_ok(m->bott_conv2, TAG_BIN, c) || !act_ok(m->bott_act2, false, m->bott_conv2.Cout))
+    return set_err(BNN_EBLOB, "bottleneck.conv2 does not chain");
+  c = m->bott_conv2.Cout;
+  for (int i = 0; i < 4; ++i) {
+    const Conv &c1 = m->dec_conv1[i], &c2 = m->dec_conv2[i];
+    if (!conv_ok(c1, TAG_BIN, skipc[3 - i] + c) || !act_ok(m->dec_act1[i], false, c1.Cout))
+      return set_err(BNN_EBLOB, "dec%d.conv1 does not chain", 4 - i);
+    if (!conv_ok(c2, TAG_BIN, c1.Cout) || !act_ok(m->dec_act2[i], false, c2.Cout))
+      return set_err(BNN_EBLOB, "dec%d.conv2 does not chain", 4 - i);
+    c = c2.Cout;
+  }
+  if (m->head_Cin != c || m->head_Cout != m->n_classes) return set_err(BNN_EBLOB, "head does not chain");
+  if (c > 32) return set_err(BNN_EBLOB, "head input width %d > 32 is not supported by the fused head", c);
+  return BNN_OK;
+}
+
+// --------------------------------------------------------- host repacking
+inline int words(int c) { return (c + 31) >> 5; }
+inline int pad32(int c) { return (c + 31) & ~31; }
+
+// kidx sign bits (bit k = ci*9 + t) -> [cw0+cw1][coutp][9] uint32 with channel
+// ci placed at word ci>>5 of the first segment (ci < cs) or at word
+// cw0 + ((ci-cs)>>5) of the second (the upsampled half of a concat).
+std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int taps, int cs) {
+  const int nw = (cin * taps + 63) / 64;
+  const int cw0 = words(cs ? cs : cin), cw1 = cs ? words(cin - cs) : 0;
+  const int coutp = pad32(cout);
+  std::vector<uint32_t> wt((size_t)(cw0 + cw1) * coutp * taps, 0u);
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci) {
+      int w, b;
+      if (!cs || ci < cs) { w = ci >> 5; b = ci & 31; }
+      else { w = cw0 + ((ci - cs) >> 5); b = (ci - cs) & 31; }
+      for (int t = 0; t < taps; ++t) {
+        const int k = ci * taps + t;
+        if ((kbits[(size_t)co * nw + (k >> 6)] >> (k & 63)) & 1ull)
+          wt[((size_t)w * coutp + co) * taps + t] |= 1u << b;
+      }
+    }
+  return wt;
+}
+
+struct FoldHost {
+  std::vector<int32_t> lo;
+  std::vector<uint32_t> wid, inv;
+};
+
+FoldHost canon_fold(const Act& a, int coutp) {
+  FoldHost f;
+  f.lo.assign(coutp, 0);
+  f.wid.assign(coutp, 0);
+  f.inv.assign(coutp / 32, 0);
+  std::vector<uint8_t> inv(coutp, 0);
+  bnn_fold_canon(a.type, a.t, a.lo, a.hi, a.C, f.lo.data(), f.wid.data(), inv.data());
+  for (int c = 0; c < a.C; ++c)
+    if (inv[c]) f.inv[c >> 5] |= 1u << (c & 31);
+  return f;
+}
+
+// ------------------------------------------------------------ device model
+struct DevBconv {
+  int cin = 0, cout = 0, cs = 0, cw0 = 0, cw1 = 0;
+  uint32_t* wt = nullptr;
+  FoldDev f1{}, f2{};
+};
+
+struct Workspace {
+  int N = 0, H = 0, W = 0;
+  uint8_t* base = nullptr;
+  uint32_t *a1 = nullptr, *skip[4] = {}, *down[4] = {}, *h[4] = {}, *b1 = nullptr, *b2 = nullptr;
+  uint32_t *d1[4] = {}, *d2[4] = {};
+};
+
+}  // namespace
+
+struct BnnDevice {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+  int rcin = 0, rcout = 0, rCO = 16, rchunks = 1;
+  float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
+  DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
+  float *hw = nullptr, *hb = nullptr;
+  int ncls = 0;
+  Workspace ws;
+  float* stage_in = nullptr;
+  size_t stage_in_cap = 0;
+  float* stage_out = nullptr;
+  size_t stage_out_cap = 0;
+};
+
+struct BnnConvLayer {
+  BnnDevice dev;   // owns the allocations
+  DevBconv L;
+};
+
+namespace {
+
+template <class T>
+int dev_upload(BnnDevice* D, T** dst, const T* src, size_t n) {
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, n ? n * sizeof(T) : 4));
+  D->allocs.push_back(p);
+  if (n) HIP_TRY(hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice));
+  *dst = (T*)p;
+  return BNN_OK;
+}
+
+int upload_fold(BnnDevice* D, FoldDev* fd, const Act& a, int coutp) {
+  FoldHost f = canon_fold(a, coutp);
+  int32_t* lo;
+  uint32_t *wid, *inv;
+  int rc;
+  if ((rc = dev_upload(D, &lo, f.lo.data(), f.lo.size()))) return rc;
+  if ((rc = dev_upload(D, &wid, f.wid.data(), f.wid.size()))) return rc;
+  if ((rc = dev_upload(D, &inv, f.inv.data(), f.inv.size()))) return rc;
+  fd->lo = lo; fd->wid = wid; fd->inv = inv;
+  return BNN_OK;
+}
+
+int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1, const Act* a2) {
+  L->cin = c.Cin; L->cout = c.Cout; L->cs = cs;
+  L->cw0 = words(cs ? cs : c.Cin);
+  L->cw1 = cs ? words(c.Cin - cs) : 0;
+  std::vector<uint32_t> wt = repack_bin(c.packed, c.Cin, c.Cout, 9, cs);
+  int rc;
+  if ((rc = dev_upload(D, &L->wt, wt.data(), wt.size()))) return rc;
+  const int coutp = pad32(c.Cout);
+  if (a1 && (rc = upload_fold(D, &L->f1, *a1, coutp))) return rc;
+  if (a2 && (rc = upload_fold(D, &L->f2, *a2, coutp))) return rc;
+  return BNN_OK;
+}
+
+// real conv weights [chunk][ky][kx][cin][CO] as +-1.0f, folds padded to chunk*CO
+int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
+  D->rcin = c.Cin;
+  D->rcout = c.Cout;
+  D->rCO = c.Cout > 16 ? 32 : 16;
+  D->rchunks = (c.Cout + D->rCO - 1) / D->rCO;
+  const int CO = D->rCO, tot = D->rchunks * CO;
+  std::vector<float> w((size_t)D->rchunks * 9 * c.Cin * CO, 0.0f);
+  for (int co = 0; co < c.Cout; ++co)
+    for (int ci = 0; ci < c.Cin; ++ci)
+      for (int t = 0; t < 9; ++t)
+        w[(((size_t)(co / CO) * 9 + t) * c.Cin + ci) * CO + co % CO] =
+            (float)c.wsign[((size_t)co * c.Cin + ci) * 9 + t];
+  auto padv = [&](const float* src) {
+    std::vector<float> v(tot, 0.0f);
+    std::copy(src, src + c.Cout, v.begin());
+    return v;
+  };
+  int rc;
+  if ((rc = dev_upload(D, &D->rw, w.data(), w.size()))) return rc;
+  std::vector<float> v;
+  v = padv(c.alpha); if ((rc = dev_upload(D, &D->ralpha, v.data(), v.size()))) return rc;
+  v = padv(a.A); if ((rc = dev_upload(D, &D->rA, v.data(), v.size()))) return rc;
+  v = padv(a.B); if ((rc = dev_upload(D, &D->rB, v.data(), v.size()))) return rc;
+  v = padv(a.slope); if ((rc = dev_upload(D, &D->rslope, v.data(), v.size()))) return rc;
+  v = padv(a.rsign); if ((rc = dev_upload(D, &D->rrsign, v.data(), v.size()))) return rc;
+  return BNN_OK;
+}
+
+void release(BnnDevice* D) {
+  if (!D) return;
+  if (D->stream) hipStreamSynchronize(D->stream);
+  for (void* p : D->allocs) hipFree(p);
+  D->allocs.clear();
+  if (D->ws.base) hipFree(D->ws.base);
+  if (D->stage_in) hipFree(D->stage_in);
+  if (D->stage_out) hipFree(D->stage_out);
+  if (D->stream) hipStreamDestroy(D->stream);
+  D->stream = nullptr;
+}
+
+int build_device(Model* m) {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return set_err(BNN_EHIP, "no HIP device visible: libbnn_hip runs the forward on the GPU only");
+  BnnDevice* D = new BnnDevice();
+  m->dev = D;
+  HIP_TRY(hipGetDevice(&D->device));
+  HIP_TRY(hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking));
+  int rc;
+  if ((rc = upload_real(D, m->enc_conv1[0], m->enc_act1[0]))) return rc;
+  if ((rc = upload_bconv(D, &D->e2[0], m->enc_conv2[0], 0, &m->enc_act2_skip[0], &m->enc_act2_down[0]))) return rc;
+  for (int i = 1; i < 4; ++i) {
+    if ((rc = upload_bconv(D, &D->e1[i], m->enc_conv1[i], 0, &m->enc_act1[i], nullptr))) return rc;
+    if ((rc = upload_bconv(D, &D->e2[i], m->enc_conv2[i], 0, &m->enc_act2_skip[i], &m->enc_act2_down[i]))) return rc;
+  }
+  if ((rc = upload_bconv(D, &D->b1, m->bott_conv1, 0, &m->bott_act1, nullptr))) return rc;
+  if ((rc = upload_bconv(D, &D->b2, m->bott_conv2, 0, &m->bott_act2, nullptr))) return rc;
+  for (int i = 0; i < 4; ++i) {
+    const int cs = m->enc_conv2[3 - i].Cout;
+    if ((rc = upload_bconv(D, &D->d1[i], m->dec_conv1[i], cs, &m->dec_act1[i], nullptr))) return rc;
+    if ((rc = upload_bconv(D, &D->d2[i], m->dec_conv2[i], 0, &m->dec_act2[i], nullptr))) return rc;
+  }
+  D->ncls = m->head_Cout;
+  if ((rc = dev_upload(D, &D->hw, m->head_W, (size_t)m->head_Cout * m->head_Cin))) return rc;
+  if ((rc = dev_upload(D, &D->hb, m->head_bias, (size_t)m->head_Cout))) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  return BNN_OK;
+}
+
+// per-level spatial dims: level 0 = input, 1..4 after each pool
+void level_dims(int H, int W, int* hs, int* wsz) {
+  hs[0] = H; wsz[0] = W;
+  for (int l = 1; l <= 4; ++l) { hs[l] = hs[l - 1] / 2; wsz[l] = wsz[l - 1] / 2; }
+}
+
+int ensure_ws(const Model* m, BnnDevice* D, int N, int H, int W) {
+  Workspace& w = D->ws;
+  if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
+  // a forward may still be in flight on a caller's stream
+  if (w.base) { HIP_TRY(hipDeviceSynchronize()); hipFree(w.base); w.base = nullptr; }
+  int hs[5], ws[5];
+  level_dims(H, W, hs, ws);
+  std::vector<std::pair<uint32_t**, size_t>> plan;
+  auto add = [&](uint32_t** p, int lvl, int c) { plan.push_back({p, (size_t)N * hs[lvl] * ws[lvl] * words(c)}); };
+  add(&w.a1, 0, m->enc_conv1[0].Cout);
+  for (int i = 0; i < 4; ++i) {
+    if (i) add(&w.h[i], i, m->enc_conv1[i].Cout);
+    add(&w.skip[i], i, m->enc_conv2[i].Cout);
+    add(&w.down[i], i + 1, m->enc_conv2[i].Cout);
+  }
+  add(&w.b1, 4, m->bott_conv1.Cout);
+  add(&w.b2, 4, m->bott_conv2.Cout);
+  for (int i = 0; i < 4; ++i) {
+    add(&w.d1[i], 3 - i, m->dec_conv1[i].Cout);
+    add(&w.d2[i], 3 - i, m->dec_conv2[i].Cout);
+  }
+  size_t total = 0;
+  for (auto& e : plan) total += (e.second * 4 + 255) & ~(size_t)255;
+  HIP_TRY(hipMalloc((void**)&w.base, total));
+  size_t off = 0;
+  for (auto& e : plan) {
+    *e.first = (uint32_t*)(w.base + off);
+    off += (e.second * 4 + 255) & ~(size_t)255;
+  }
+  w.N = N; w.H = H; w.W = W;
+  return BNN_OK;
+}
+
+// ------------------------------------------------------------ profiling
+struct ProfRec {
+  std::string label, optype;
+  double oe, taps, sec;
+};
+std::vector<ProfRec> g_prof;
+bool g_prof_on = false;
+
+// work-item shape: pool epilogue needs 2x2 blocks, the head one pixel; the
+// channel group shrinks until the launch has ~4 waves per SIMD
+void pick_shape(int epi, int N, int H, int W, int cout, int* mt, int* cog) {
+  *mt = (epi == EPI_POOL) ? 2 : 1;
+  if (epi == EPI_HEAD) { *cog = cout <= 16 ? 16 : 32; return; }
+  const long tiles = (long)N * ((H + *mt - 1) / *mt) * ((W + *mt - 1) / *mt);
+  int c = *mt == 2 ? 16 : 32;
+  auto waves = [&](int g) { return ((tiles + 63) / 64) * (long)((cout + g - 1) / g); };
+  while (c > 8 && waves(c) < 4096) c /= 2;
+  *cog = c;
+}
+
+struct Dumps {
+  bool on = false;
+  float* conv1 = nullptr;
+  int32_t* P[32] = {};
+  int32_t* P2[4] = {};
+};
+
+struct Op {
+  const char* label;
+  const char* optype;
+  double oe, taps;
+};
+
+// Enqueue the whole forward for N patches.  Each stage is one kernel; with
+// profiling on, an event pair brackets every kernel.
+int enqueue_forward(const Model* m, BnnDevice* D, const float* d_in, int N, int H, int W, float* d_logits,
+                    hipStream_t s, Dumps* dmp, std::vector<Op>* ops, std::vector<hipEvent_t>* evs) {
+  Workspace& w = D->ws;
+  int hs[5], wsz[5];
+  level_dims(H, W, hs, wsz);
+  auto mark = [&](const char* label, const char* optype, double oe, double taps) -> int {
+    if (!evs) return BNN_OK;
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    HIP_TRY(hipEventRecord(e, s));
+    evs->push_back(e);
+    if (label) ops->push_back({label, optype, oe, taps});
+    return BNN_OK;
+  };
+  const bool dump = dmp && dmp->on;
+  int pi = 0;  // index into dmp->P
+  int rc;
+  if ((rc = mark(nullptr, nullptr, 0, 0))) return rc;
+
+  // enc1.conv1: real conv + real fold -> a1 bits
+  for (int ch = 0; ch < D->rchunks; ++ch) {
+    RealArgs ra{};
+    ra.x = d_in;
+    ra.w = D->rw + (size_t)ch * 9 * D->rcin * D->rCO;
+    ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
+    ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
+    ra.CO = D->rCO;
+    ra.co0 = ch * D->rCO;
+    ra.out = w.a1;
+    ra.f32 = dump ? dmp->conv1 : nullptr;
+    HIP_TRY(launch_real(ra, s));
+  }
+  if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
+
+  auto bconv = [&](const DevBconv& L, int epi, const uint32_t* in0, const uint32_t* in1, int lvl, int lvl1,
+                   uint32_t* out, uint32_t* out2, float* logits, const char* label) -> int {
+    BconvArgs a{};
+    a.in0 = in0; a.in1 = in1; a.cw0 = L.cw0; a.cw1 = L.cw1;
+    a.N = N; a.H = hs[lvl]; a.W = wsz[lvl]; a.cin = L.cin; a.cout = L.cout;
+    if (in1) {
+      a.h1 = hs[lvl1]; a.w1 = wsz[lvl1];
+      const int uH = 2 * a.h1, uW = 2 * a.w1;
+      a.oh = a.H > uH ? (a.H - uH) / 2 : 0;
+      a.ow = a.W > uW ? (a.W - uW) / 2 : 0;
+      a.uh = std::min(uH, a.H);
+      a.uw = std::min(uW, a.W);
+    }
+    a.wt = L.wt; a.f1 = L.f1; a.f2 = L.f2;
+    a.out = out; a.out2 = out2; a.cwo = words(L.cout);
+    a.logits = logits; a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
+    if (dump) {
+      a.P = dmp->P[pi++];
+      if (epi == EPI_POOL) a.P2 = dmp->P2[lvl];
+    }
+    int mt, cog;
+    pick_shape(epi, N, a.H, a.W, L.cout, &mt, &cog);
+    HIP_TRY(launch_bconv(a, epi, mt, cog, dump, s));
+    const char* ot = epi == EPI_POOL ? "bconv_pool" : epi == EPI_HEAD ? "bconv_head" : "bconv";
+    return mark(label, ot, (double)N * L.cout * a.H * a.W, (double)L.cin * 9);
+  };
+
+  static const char* enc_c1[4] = {"", "enc2.c1", "enc3.c1", "enc4.c1"};
+  static const char* enc_c2[4] = {"enc1.c2", "enc2.c2", "enc3.c2", "enc4.c2"};
+  static const char* dec_c1[4] = {"dec4.c1", "dec3.c1", "dec2.c1", "dec1.c1"};
+  static const char* dec_c2[4] = {"dec4.c2", "dec3.c2", "dec2.c2", "dec1.c2"};
+  const uint32_t* x = w.a1;
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t* hin = x;
+    if (i) {
+      if ((rc = bconv(D->e1[i], EPI_FOLD, x, nullptr, i, 0, w.h[i], nullptr, nullptr, enc_c1[i]))) return rc;
+      hin = w.h[i];
+    }
+    if ((rc = bconv(D->e2[i], EPI_POOL, hin, nullptr, i, 0, w.skip[i], w.down[i], nullptr, enc_c2[i]))) return rc;
+    x = w.down[i];
+  }
+  if ((rc = bconv(D->b1, EPI_FOLD, x, nullptr, 4, 0, w.b1, nullptr, nullptr, "bott.c1"))) return rc;
+  if ((rc = bconv(D->b2, EPI_FOLD, w.b1, nullptr, 4, 0, w.b2, nullptr, nullptr, "bott.c2"))) return rc;
+  x = w.b2;
+  int xl = 4;
+  for (int i = 0; i < 4; ++i) {
+    const int lvl = 3 - i;
+    if ((rc = bconv(D->d1[i], EPI_FOLD, w.skip[lvl], x, lvl, xl, w.d1[i], nullptr, nullptr, dec_c1[i]))) return rc;
+    if (i < 3) {
+      if ((rc = bconv(D->d2[i], EPI_FOLD, w.d1[i], nullptr, lvl, 0, w.d2[i], nullptr, nullptr, dec_c2[i]))) return rc;
+    } else {
+      if ((rc = bconv(D->d2[i], EPI_HEAD, w.d1[i], nullptr, lvl, 0, dump ? w.d2[i] : nullptr, nullptr, d_logits,
+                      dec_c2[i])))
+        return rc;
+    }
+    x = w.d2[i];
+    xl = lvl;
+  }
+  return BNN_OK;
+}
+
+int check_shape(const Model* m, int N, int H, int W) {
+  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+  if (N < 0) return set_err(BNN_EARG, "negative batch");
+  if (H < 16 || W < 16)
+    return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
+  if ((size_t)N * m->n_bands * H * W * 4 >= 0xffffffffull)
+    return set_err(BNN_EARG, "batch too large for one launch (%zu input bytes >= 4 GiB)",
+                   (size_t)N * m->n_bands * H * W * 4);
+  return BNN_OK;
+}
+
+int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+               Dumps* dmp) {
+  int rc;
+  if ((rc = check_shape(m, N, H, W))) return rc;
+  if (N == 0) return BNN_OK;
+  BnnDevice* D = m->dev;
+  if (!s) s = D->stream;
+  if ((rc = ensure_ws(m, D, N, H, W))) return rc;
+  if (!g_prof_on) return enqueue_forward(m, D, d_in, N, H, W, d_logits, s, dmp, nullptr, nullptr);
+  std::vector<Op> ops;
+  std::vector<hipEvent_t> evs;
+  rc = enqueue_forward(m, D, d_in, N, H, W, d_logits, s, dmp, &ops, &evs);
+  if (!rc && !evs.empty()) {
+    HIP_TRY(hipEventSynchronize(evs.back()));
+    for (size_t i = 0; i + 1 < evs.size() && i < ops.size(); ++i) {
+      float ms = 0;
+      HIP_TRY(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
+      prof_add(ops[i].label, ops[i].optype, ops[i].oe, ops[i].taps, ms * 1e-3);
+    }
+  }
+  for (hipEvent_t e : evs) hipEventDestroy(e);
+  return rc;
+}
+
+int grow(float** p, size_t* cap, size_t bytes) {
+  if (*cap >= bytes) return BNN_OK;
+  if (*p) { HIP_TRY(hipDeviceSynchronize()); hipFree(*p); }
+  *p = nullptr;
+  *cap = 0;
+  HIP_TRY(hipMalloc((void**)p, bytes));
+  *cap = bytes;
+  return BNN_OK;
+}
+
+int run_host(const Model* m, const float* input, int N, int H, int W, float* logits, Dumps* dmp) {
+  int rc;
+  if ((rc = check_shape(m, N, H, W))) return rc;
+  if (N == 0) return BNN_OK;
+  BnnDevice* D = m->dev;
+  const size_t ib = (size_t)N * m->n_bands * H * W * 4, ob = (size_t)N * m->n_classes * H * W * 4;
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, ib))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, ob))) return rc;
+  HIP_TRY(hipMemcpyAsync(D->stage_in, input, ib, hipMemcpyHostToDevice, D->stream));
+  if ((rc = run_device(m, D->stage_in, N, H, W, D->stage_out, D->stream, dmp))) return rc;
+  HIP_TRY(hipMemcpyAsync(logits, D->stage_out, ob, hipMemcpyDeviceToHost, D->stream));
+  HIP_TRY(hipStreamSynchronize(D->stream));
+  return BNN_OK;
+}
+
+}  // namespace
+
+// =================================================================== C ABI
+extern "C" {
+
+const char* bnn_last_error(void) { return g_err.c_str(); }
+
+int bnn_blob_check(const char* path) {
+  Model* m = nullptr;
+  int rc = parse_blob(path, &m);
+  if (rc) return rc;
+  rc = validate(m);
+  free_host(m);
+  free(m);
+  return rc;
+}
+
+void bnn_free(Model* m) {
+  if (!m) return;
+  if (m->dev) {
+    release(m->dev);
+    delete m->dev;
+    m->dev = nullptr;
+  }
+  free_host(m);
+  free(m);
+}
+
+int bnn_load_status(const char* path, Model** out) {
+  *out = nullptr;
+  Model* m = nullptr;
+  int rc = parse_blob(path, &m);
+  if (rc) return rc;
+  if ((rc = validate(m)) || (rc = build_device(m))) {
+    const std::string keep = g_err;
+    bnn_free(m);
+    g_err = keep;
+    return rc;
+  }
+  *out = m;
+  return BNN_OK;
+}
+
+Model* bnn_load(const char* path) {
+  Model* m = nullptr;
+  if (bnn_load_status(path, &m)) die();
+  return m;
+}
+
+int bnn_forward_batch(const Model* m, const float* input, int N, int H, int W, float* logits) {
+  return run_host(m, input, N, H, W, logits, nullptr);
+}
+
+void bnn_forward(const Model* m, const float* input, int H, int W, float* logits) {
+  prof_reset();
+  if (bnn_forward_batch(m, input, 1, H, W, logits)) die();
+}
+
+int bnn_forward_device(const Model* m, const float* d_input, int N, int H, int W, float* d_logits,
+                       void* stream) {
+  return run_device(m, d_input, N, H, W, d_logits, (hipStream_t)stream, nullptr);
+}
+
+void* bnn_stream(const Model* m) { return (m && m->dev) ? (void*)m->dev->stream : nullptr; }
+
+int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, float* logits, bnn_stage_cb cb,
+                      void* ctx) {
+  int rc;
+  if ((rc = check_shape(m, N, H, W))) return rc;
+  if (N == 0) return BNN_OK;
+  BnnDevice* D = m->dev;
+  int hs[5], ws[5];
+  level_dims(H, W, hs, ws);
+  // P dumps in launch order, with the (c, level) of each
+  struct PInfo { const char* name; int c, lvl; };
+  std::vector<PInfo> pinfo;
+  pinfo.push_back({"enc1.conv2.P", m->enc_conv2[0].Cout, 0});
+  static const char* encn[4][2] = {{"", "enc1.conv2.P"}, {"enc2.conv1.P", "enc2.conv2.P"},
+                                   {"enc3.conv1.P", "enc3.conv2.P"}, {"enc4.conv1.P", "enc4.conv2.P"}};
+  for (int i = 1; i < 4; ++i) {
+    pinfo.push_back({encn[i][0], m->enc_conv1[i].Cout, i});
+    pinfo.push_back({encn[i][1], m->enc_conv2[i].Cout, i});
+  }
+  pinfo.push_back({"bott.conv1.P", m->bott_conv1.Cout, 4});
+  pinfo.push_back({"bott.conv2.P", m->bott_conv2.Cout, 4});
+  static const char* decn[4][2] = {{"dec4.conv1.P", "dec4.conv2.P"}, {"dec3.conv1.P", "dec3.conv2.P"},
+                                   {"dec2.conv1.P", "dec2.conv2.P"}, {"dec1.conv1.P", "dec1.conv2.P"}};
+  for (int i = 0; i < 4; ++i) {
+    pinfo.push_back({decn[i][0], m->dec_conv1[i].Cout, 3 - i});
+    pinfo.push_back({decn[i][1], m->dec_conv2[i].Cout, 3 - i});
+  }
+  Dumps d;
+  d.on = true;
+  std::vector<void*> tmp;
+  auto alloc = [&](size_t bytes) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) return nullptr;
+    tmp.push_back(p);
+    return p;
+  };
+  auto cleanup = [&]() { for (void* p : tmp) hipFree(p); };
+  d.conv1 = (float*)alloc((size_t)N * m->enc_conv1[0].Cout * H * W * 4);
+  for (size_t i = 0; i < pinfo.size(); ++i)
+    d.P[i] = (int32_t*)alloc((size_t)N * pinfo[i].c * hs[pinfo[i].lvl] * ws[pinfo[i].lvl] * 4);
+  for (int i = 0; i < 4; ++i) d.P2[i] = (int32_t*)alloc((size_t)N * m->enc_conv2[i].Cout * hs[i + 1] * ws[i + 1] * 4);
+  for (void* p : tmp)
+    if (!p) { cleanup(); return set_err(BNN_EHIP, "hipMalloc failed for debug dumps"); }
+  if ((rc = run_host(m, input, N, H, W, logits, &d))) { cleanup(); return rc; }
+  if (cb) {
+    const Workspace& w = D->ws;
+    auto emit_f = [&](const char* name, const void* dptr, int dtype, int c, int lvl) -> int {
+      const size_t n = (size_t)N * c * hs[lvl] * ws[lvl];
+      std::vector<uint8_t> h(n * 4);
+      HIP_TRY(hipMemcpy(h.data(), dptr, n * 4, hipMemcpyDeviceToHost));
+      cb(ctx, name, dtype, N, c, hs[lvl], ws[lvl], h.data());
+      return BNN_OK;
+    };
+    // packed bits [N][h][w][cw] -> int8 +-1 [N][c][h][w]
+    auto emit_b = [&](const char* name, const uint32_t* dptr, int c, int lvl) -> int {
+      const int hh = hs[lvl], ww = ws[lvl], cw = words(c);
+      const size_t np = (size_t)N * hh * ww;
+      std::vector<uint32_t> pk(np * cw);
+      HIP_TRY(hipMemcpy(pk.data(), dptr, pk.size() * 4, hipMemcpyDeviceToHost));
+      std::vector<int8_t> out((size_t)N * c * hh * ww);
+      for (int n = 0; n < N; ++n)
+        for (int ch = 0; ch < c; ++ch)
+          for (int p = 0; p < hh * ww; ++p) {
+            const uint32_t word = pk[((size_t)n * hh * ww + p) * cw + (ch >> 5)];
+            out[((size_t)n * c + ch) * hh * ww + p] = ((word >> (ch & 31)) & 1u) ? 1 : -1;
+          }
+      cb(ctx, name, 0, N, c, hh, ww, out.data());
+      return BNN_OK;
+    };
+    char nm[48];
+    int pi = 0;
+    if ((rc = emit_f("enc1.conv1", d.conv1, 2, m->enc_conv1[0].Cout, 0))) goto done;
+    if ((rc = emit_b("enc1.act1", w.a1, m->enc_conv1[0].Cout, 0))) goto done;
+    for (int i = 0; i < 4; ++i) {
+      if (i) {
+        if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, i))) goto done;
+        ++pi;
+        snprintf(nm, sizeof nm, "enc%d.act1", i + 1);
+        if ((rc = emit_b(nm, w.h[i], m->enc_conv1[i].Cout, i))) goto done;
+      }
+      if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, i))) goto done;
+      ++pi;
+      snprintf(nm, sizeof nm, "enc%d.act2_skip", i + 1);
+      if ((rc = emit_b(nm, w.skip[i], m->enc_conv2[i].Cout, i))) goto done;
+      snprintf(nm, sizeof nm, "enc%d.pool.P", i + 1);
+      if ((rc = emit_f(nm, d.P2[i], 1, m->enc_conv2[i].Cout, i + 1))) goto done;
+      snprintf(nm, sizeof nm, "enc%d.act2_down", i + 1);
+      if ((rc = emit_b(nm, w.down[i], m->enc_conv2[i].Cout, i + 1))) goto done;
+    }
+    if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, 4))) goto done;
+    ++pi;
+    if ((rc = emit_b("bott.act1", w.b1, m->bott_conv1.Cout, 4))) goto done;
+    if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, 4))) goto done;
+    ++pi;
+    if ((rc = emit_b("bott.act2", w.b2, m->bott_conv2.Cout, 4))) goto done;
+    for (int i = 0; i < 4; ++i) {
+      const int lvl = 3 - i;
+      if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, lvl))) goto done;
+      ++pi;
+      snprintf(nm, sizeof nm, "dec%d.act1", 4 - i);
+      if ((rc = emit_b(nm, w.d1[i], m->dec_conv1[i].Cout, lvl))) goto done;
+      if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, lvl))) goto done;
+      ++pi;
+      snprintf(nm, sizeof nm, "dec%d.act2", 4 - i);
+      if ((rc = emit_b(nm, w.d2[i], m->dec_conv2[i].Cout, lvl))) goto done;
+    }
+    cb(ctx, "logits", 2, N, m->n_classes, H, W, logits);
+  }
+done:
+  cleanup();
+  return rc;
+}
+
+// ----------------------------------------------------------- profiler API
+double prof_now(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + (double)t.tv_nsec * 1e-9;
+}
+void prof_reset(void) { g_prof.clear(); }
+void prof_add(const char* label, const char* optype, double out_elems, double taps, double sec) {
+  if (g_prof.size() >= 65536) return;
+  g_prof.push_back({label ? label : "?", optype ? optype : "?", out_elems, taps, sec});
+}
+void prof_report(FILE* o) {
+  if (g_prof.empty()) return;
+  double tot = 0;
+  for (auto& r : g_prof) tot += r.sec;
+  auto work = [](const ProfRec& r) { return r.oe * (r.taps > 0 ? r.taps : 1.0); };
+  fprintf(o, "\n# per-op (execution order, GPU kernel time)\n");
+  fprintf(o, "%-14s %-10s %12s %12s %10s %7s\n", "layer", "op", "out_elems", "work", "ms", "%");
+  for (auto& r : g_prof)
+    fprintf(o, "%-14s %-10s %12.0f %12.4g %10.4f %6.2f\n", r.label.c_str(), r.optype.c_str(), r.oe, work(r),
+            r.sec * 1e3, tot > 0 ? 100.0 * r.sec / tot : 0.0);
+  fprintf(o, "\n# roll-up by op type\n");
+  fprintf(o, "%-10s %6s %12s %10s %7s\n", "op", "calls", "work", "ms", "%");
+  std::vector<std::string> seen;
+  for (auto& r : g_prof)
+    if (std::find(seen.begin(), seen.end(), r.optype) == seen.end()) seen.push_back(r.optype);
+  for (auto& t : seen) {
+    double s = 0, w = 0;
+    int c = 0;
+    for (auto& r : g_prof)
+      if (r.optype == t) { s += r.sec; w += work(r); ++c; }
+    fprintf(o, "%-10s %6d %12.4g %10.4f %6.2f\n", t.c_str(), c, w, s * 1e3, tot > 0 ? 100.0 * s / tot : 0.0);
+  }
+  fprintf(o, "# total per-op: %.4f ms\n", tot * 1e3);
+}
+void bnn_prof_enable(int on) { g_prof_on = on != 0; }
+int bnn_prof_count(void) { return (int)g_prof.size(); }
+int bnn_prof_get(int i, char* label, int label_len, char* optype, int optype_len, double* ms, double* work) {
+  if (i < 0 || i >= (int)g_prof.size()) return set_err(BNN_EARG, "profile index out of range");
+  const ProfRec& r = g_prof[i];
+  if (label && label_len > 0) snprintf(label, label_len, "%s", r.label.c_str());
+  if (optype && optype_len > 0) snprintf(optype, optype_len, "%s", r.optype.c_str());
+  if (ms) *ms = r.sec * 1e3;
+  if (work) *work = r.oe * (r.taps > 0 ? r.taps : 1.0);
+  return BNN_OK;
+}
+
+// ------------------------------------------------------------ fold canon
+void bnn_fold_canon(const int32_t* type, const int32_t* t, const int32_t* lo, const int32_t* hi, int C,
+                    int32_t* out_lo, uint32_t* out_wid, uint8_t* out_inv) {
+  // |P| <= Cin*9 < 2^30, so clamping thresholds to +-2^30 changes no decision
+  // and keeps P - lo free of overflow.
+  const int32_t L = 1 << 30;
+  auto cl = [&](int32_t v) { return v < -L ? -L : (v > L ? L : v); };
+  for (int c = 0; c < C; ++c) {
+    int32_t l = 0;
+    uint32_t w = 0;
+    uint8_t inv = 0;
+    switch (type[c]) {
+      case 0: inv = t[c] > 0; break;                                  // constant
+      case 1: l = cl(t[c]); w = 0x80000000u; break;                   // P >= t
+      case 2: l = cl(t[c]); w = 0x80000000u; inv = 1; break;          // P <  t
+      case 3:                                                         // lo <= P < hi
+      case 4: {                                                       // P < lo || P >= hi
+        const int32_t a = cl(lo[c]), b = cl(hi[c]);
+        if (a < b) { l = a; w = (uint32_t)(b - a); }
+        inv = type[c] == 4;
+        break;
+      }
+      default: break;                                                 // -1 everywhere
+    }
+    out_lo[c] = l;
+    out_wid[c] = w;
+    out_inv[c] = inv;
+  }
+}
+
+// ------------------------------------------------------- isolated layers
+BnnConvLayer* bnn_layer_create(const uint64_t* packed_w, int Cin, int Cout, const int32_t* type1,
+                               const int32_t* t1, const int32_t* lo1, const int32_t* hi1, const int32_t* type2,
+                               const int32_t* t2, const int32_t* lo2, const int32_t* hi2) {
+  if (Cin <= 0 || Cout <= 0 || !packed_w) { set_err(BNN_EARG, "bad layer shape"); return nullptr; }
+  BnnConvLayer* Lr = new BnnConvLayer();
+  BnnDevice* D = &Lr->dev;
+  auto fail = [&]() -> BnnConvLayer* { release(D); delete Lr; return nullptr; };
+  if (hipGetDevice(&D->device) != hipSuccess) { set_err(BNN_EHIP, "no HIP device"); return fail(); }
+  if (hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking) != hipSuccess) {
+    set_err(BNN_EHIP, "hipStreamCreate failed");
+    return fail();
+  }
+  Conv c{};
+  c.tag = TAG_BIN; c.Cin = Cin; c.Cout = Cout; c.kh = c.kw = 3; c.pad = c.stride = 1;
+  c.nwords = (Cin * 9 + 63) / 64;
+  c.packed = const_cast<uint64_t*>(packed_w);
+  Act a1{}, a2{};
+  a1.C = a2.C = Cout;
+  a1.type = const_cast<int32_t*>(type1); a1.t = const_cast<int32_t*>(t1);
+  a1.lo = const_cast<int32_t*>(lo1); a1.hi = const_cast<int32_t*>(hi1);
+  a2.type = const_cast<int32_t*>(type2); a2.t = const_cast<int32_t*>(t2);
+  a2.lo = const_cast<int32_t*>(lo2); a2.hi = const_cast<int32_t*>(hi2);
+  if (upload_bconv(D, &Lr->L, c, 0, type1 ? &a1 : nullptr, type2 ? &a2 : nullptr)) return fail();
+  return Lr;
+}
+
+void bnn_layer_free(BnnConvLayer* L) {
+  if (!L) return;
+  release(&L->dev);
+  delete L;
+}
+
+static int layer_args(const BnnConvLayer* L, const uint32_t* d_act, int N, int H, int W, BconvArgs* a) {
+  if (!L) return set_err(BNN_EARG, "null layer");
+  if (N < 0 || H <= 0 || W <= 0) return set_err(BNN_EARG, "bad shape");
+  *a = BconvArgs{};
+  a->in0 = d_act; a->cw0 = L->L.cw0; a->N = N; a->H = H; a->W = W;
+  a->cin = L->L.cin; a->cout = L->L.cout; a->wt = L->L.wt; a->f1 = L->L.f1; a->f2 = L->L.f2;
+  a->cwo = words(L->L.cout);
+  return BNN_OK;
+}
+
+int bnn_layer_P_device(const BnnConvLayer* L, const uint32_t* d_act, int N, int H, int W, int32_t* d_P,
+                       void* stream) {
+  BconvArgs a;
+  int rc;
+  if ((rc = layer_args(L, d_act, N, H, W, &a))) return rc;
+  a.P = d_P;
+  int mt, cog;
+  pick_shape(EPI_P, N, H, W, a.cout, &mt, &cog);
+  HIP_TRY(launch_bconv(a, EPI_P, mt, cog, false, stream ? (hipStream_t)stream : L->dev.stream));
+  return BNN_OK;
+}
+
+int bnn_layer_fold_pool_device(const BnnConvLayer* L, const uint32_t* d_act, int N, int H, int W,
+                               uint32_t* d_skip, uint32_t* d_down, void* stream) {
+  BconvArgs a;
+  int rc;
+  if ((rc = layer_args(L, d_act, N, H, W, &a))) return rc;
+  if (!L->L.f1.lo || !L->L.f2.lo) return set_err(BNN_EARG, "layer was created without both rules");
+  if (H < 2 || W < 2) return set_err(BNN_EARG, "pool needs H, W >= 2");
+  a.out = d_skip; a.out2 = d_down;
+  int mt, cog;
+  pick_shape(EPI_POOL, N, H, W, a.cout, &mt, &cog);
+  HIP_TRY(launch_bconv(a, EPI_POOL, mt, cog, false, stream ? (hipStream_t)stream : L->dev.stream));
+  return BNN_OK;
+}
+
+int bnn_pack_act_device(const int8_t* d_a, uint32_t* d_out, int N, int C, int H, int W, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(launch_pack_act(d_a, d_out, N, C, H, W, s));
+  return BNN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+// bnn_infer - command-line driver, a drop-in for the reference's csrc/bnn_infer
+// (csrc/main.c:1-80): same arguments, same "rand" input, same stderr report.
+//
+//   bnn_infer weights.blob input.bin|rand output.bin [H W [reps]]
+//     input.bin : n_bands*H*W float32, [band,row,col]; "rand" = srand(1234)
+//                 uniform [-1,1] (csrc/main.c:39-41)
+//     output.bin: n_classes*H*W float32, [class,row,col]
+//     reps      : run the forward reps times, report median/min/max
+//
+// The forward runs on the GPU.  BNN_PROFILE=1 in the environment adds the
+// per-kernel table (the reference needs a separate `make profile` build).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+#include <algorithm>
+
+#include "bnn_model.h"
+#include "bnn_prof.h"
+
+int main(int argc, char** argv) {
+  if (argc < 4) {
+    fprintf(stderr, "usage: %s weights.blob input.bin|rand output.bin [H W [reps]]\n", argv[0]);
+    return 1;
+  }
+  const int H = argc > 4 ? atoi(argv[4]) : 32;
+  const int W = argc > 5 ? atoi(argv[5]) : 32;
+  int reps = argc > 6 ? atoi(argv[6]) : 1;
+  if (reps < 1) reps = 1;
+  const char* pe = getenv("BNN_PROFILE");
+  const bool profile = pe && *pe && strcmp(pe, "0") != 0;
+
+  const double t0 = prof_now();
+  Model* m = bnn_load(argv[1]);
+  const double t_load = prof_now() - t0;
+
+  const long n_in = (long)m->n_bands * H * W;
+  std::vector<float> input(n_in);
+  if (strcmp(argv[2], "rand") == 0) {
+    srand(1234);
+    for (long i = 0; i < n_in; ++i) input[i] = (float)rand() / RAND_MAX * 2.0f - 1.0f;
+  } else {
+    FILE* fi = fopen(argv[2], "rb");
+    if (!fi || fread(input.data(), sizeof(float), n_in, fi) != (size_t)n_in) {
+      fprintf(stderr, "bad input file\n");
+      return 1;
+    }
+    fclose(fi);
+  }
+
+  const long n_out = (long)m->n_classes * H * W;
+  std::vector<float> logits(n_out);
+  std::vector<double> ts(reps);
+  for (int r = 0; r < reps; ++r) {
+    if (profile) bnn_prof_enable(r == reps - 1);  // per-op rows of the last rep
+    const double f0 = prof_now();
+    bnn_forward(m, input.data(), H, W, logits.data());
+    ts[r] = (prof_now() - f0) * 1e3;
+  }
+  std::sort(ts.begin(), ts.end());
+  const double med = ts[reps / 2], tmin = ts[0], tmax = ts[reps - 1];
+
+  const double w0 = prof_now();
+  FILE* fo = fopen(argv[3], "wb");
+  if (!fo) {
+    fprintf(stderr, "cannot open %s\n", argv[3]);
+    return 1;
+  }
+  fwrite(logits.data(), sizeof(float), n_out, fo);
+  fclose(fo);
+  const double t_write = (prof_now() - w0) * 1e3;
+
+  fprintf(stderr, "# H=%d W=%d bands=%d classes=%d reps=%d\n", H, W, m->n_bands, m->n_classes, reps);
+  fprintf(stderr, "# blob load : %9.3f ms\n", t_load * 1e3);
+  fprintf(stderr, "# forward   : %9.3f ms  (median; min %.3f, max %.3f)\n", med, tmin, tmax);
+  fprintf(stderr, "# out write : %9.3f ms\n", t_write);
+  prof_report(stderr);
+  bnn_free(m);
+  return 0;
+}

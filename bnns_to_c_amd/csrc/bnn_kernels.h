@@ -1,0 +1,98 @@
+// bnn_kernels.h - device-side argument blocks and launchers (internal).
+//
+// HBM layouts used by every kernel here:
+//   real input      float  [N][Cin][H][W]       (per patch [band,row,col], csrc/main.c:3)
+//   binary act      uint32 [N][H][W][CW]        bit (c & 31) of word (c >> 5) = (a_c > 0),
+//                                               CW = ceil(C/32); unused high bits are 0
+//   binary weights  uint32 [CW][Cout][9]        same channel->bit map as the activations
+//                                               they meet, per 3x3 tap t = ky*3+kx
+//   real weights    float  [3 ky][3 kx][Cin][CO] +-1.0, CO = padded output width
+//   logits          float  [N][ncls][H][W]
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bnn {
+
+enum Epi : int {
+  EPI_FOLD = 0,  // integer rule on P -> packed bits
+  EPI_POOL = 1,  // rule on P (skip) + 2x2 max of P -> second rule (down)
+  EPI_HEAD = 2,  // rule on P -> +-1 -> fp32 1x1 head -> logits
+  EPI_P = 3,     // raw int32 P [N][Cout][H][W]
+};
+
+// One canonical interval per channel: bit = ((uint32)(P - lo) < wid) ^ inv.
+// Covers every integer rule type (csrc/bnn_fold.c:37-60).
+struct FoldDev {
+  const int32_t* lo;
+  const uint32_t* wid;
+  const uint32_t* inv;  // bit c & 31 of word c >> 5
+};
+
+struct BconvArgs {
+  const uint32_t* in0;  // plain input, or the skip half of a concat
+  const uint32_t* in1;  // low-res tensor upsampled 2x nearest (concat), or null
+  int cw0, cw1;         // words per pixel of in0 / in1
+  int h1, w1;           // in1 spatial dims
+  int oh, ow;           // F.pad before-offsets of the upsample inside H x W
+  int uh, uw;           // rows/cols of H x W the upsample covers (from oh/ow)
+  int N, H, W;
+  int cin, cout;        // true channel counts
+  const uint32_t* wt;   // [cw0+cw1][cout][9]
+  FoldDev f1, f2;
+  uint32_t* out;        // bits [N][H][W][cwo]  (EPI_FOLD/POOL)
+  uint32_t* out2;       // pooled bits [N][H/2][W/2][cwo] (EPI_POOL)
+  int cwo;
+  int32_t* P;           // EPI_P output, or the P dump of a fused epilogue
+  int32_t* P2;          // pooled-P dump (EPI_POOL)
+  float* logits;        // EPI_HEAD
+  const float* hw;      // head W [ncls][cout]
+  const float* hb;      // head bias [ncls]
+  int ncls;
+};
+
+struct RealArgs {
+  const float* x;
+  const float* w;       // [9][cin][CO]
+  const float* alpha;
+  const float* A;
+  const float* B;
+  const float* slope;
+  const float* rsign;
+  int N, H, W, cin, cout;
+  int CO;               // output channels per launch in the weight layout (16 or 32)
+  int co0;              // first output channel handled by this launch
+  uint32_t* out;        // bits [N][H][W][1]; may be null
+  float* f32;           // conv output [N][cout][H][W]; may be null
+};
+
+// Launchers return hipSuccess or the first launch error.  mt = micro-tile
+// side (1 or 2), cog = output channels per work-item (8/16/32).
+hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
+                        hipStream_t s);
+hipError_t launch_real(const RealArgs& a, hipStream_t s);
+
+// Simple kernels behind the reference's batch-1 kernel ABI.
+hipError_t launch_pack_act(const int8_t* a, uint32_t* out, int N, int C, int H, int W,
+                           hipStream_t s);
+hipError_t launch_bconv_generic(const uint32_t* act, const uint32_t* wt, int32_t* P,
+                                int cin, int H, int W, int cout, int kh, int kw,
+                                int pad, int stride, hipStream_t s);
+hipError_t launch_bconv_naive(const int8_t* a, const int8_t* w, int32_t* P, int cin,
+                              int H, int W, int cout, int kh, int kw, int pad,
+                              int stride, hipStream_t s);
+hipError_t launch_real_generic(const float* x, const float* w, const float* alpha,
+                               float* out, int cin, int H, int W, int cout, int kh,
+                               int kw, int pad, int stride, hipStream_t s);
+hipError_t launch_maxpool(const int32_t* P, int32_t* out, int C, int H, int W, int k,
+                          int stride, hipStream_t s);
+hipError_t launch_fold_int(const int32_t* P, int8_t* out, int C, int HW,
+                           const int32_t* type, const int32_t* t, const int32_t* lo,
+                           const int32_t* hi, hipStream_t s);
+hipError_t launch_fold_real(const float* x, int8_t* out, int C, int HW, const float* A,
+                            const float* B, const float* slope, const float* rsign,
+                            hipStream_t s);
+hipError_t launch_head(const float* a, const float* W, const float* b, float* out,
+                       int cin, int HW, int cout, hipStream_t s);
+
+}  // namespace bnn

@@ -1,0 +1,647 @@
+// bnn_kernels.hip - gfx950 kernels for the v1 Bi-Real binary UNet forward.
+//
+// Binary conv (csrc/bnn_conv.c:23-36): per output pixel and channel
+//     P = sum over in-image taps of a*w = N_valid - 2 * popcount((a XOR w) & valid)
+// with N_valid = (#in-image taps) * Cin.  Activations and weights are packed
+// along channels (bit = sign > 0), so each 32-bit word of a tap costs one
+// v_bitop3_b32 ((a ^ w) & valid) and one v_bcnt_u32_b32 (popcount + acc).
+// Zero high bits in both operands contribute nothing, so channel tails and
+// the word-aligned [skip ; upsampled] concat need no extra masking.  A work
+// item is one output pixel (MT=1) or a 2x2 block (MT=2, used by the pool
+// epilogue); the COG output channels of its group are wave-uniform, so the
+// weights arrive through scalar loads and feed the VALU as SGPR operands.
+// P never leaves registers: the integer rule, the 2x2 max-pool, the second
+// rule and the fp32 head run in the epilogue.
+//
+// Real-input first conv (csrc/bnn_conv_realin.c:66-116) is order-exact: for
+// each output, taps in row-major order, s = x*w summed over ci from 0 in
+// sequence, acc += s, out = alpha * acc.  Every product is x * (+-1), which
+// is exact, so one fused multiply-add per term rounds exactly like the
+// reference's multiply-then-add.  Out-of-image taps are computed on a clamped
+// (in-image) address and discarded by a select before acc += s; skipping a
+// tap and adding the +0 it would sum to are the same, since s and acc never
+// hold -0.
+#include "bnn_kernels.h"
+
+namespace bnn {
+namespace {
+
+constexpr int kBlock = 256;
+
+// gfx9 buffer descriptor word 3 for raw dword access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint32_t ld_u32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0);
+}
+
+// ------------------------------------------------------------------------
+// real-input conv + real fold
+// ------------------------------------------------------------------------
+template <int CO>
+__device__ __forceinline__ void fma_terms(float (&s)[3][CO], const float (&xv)[3],
+                                          const float* __restrict__ wr, int cin, int ci) {
+#pragma unroll
+  for (int kx = 0; kx < 3; ++kx) {
+    const float* wk = wr + ((size_t)kx * cin + ci) * CO;
+#pragma unroll
+    for (int c = 0; c < CO; ++c) s[kx][c] = __fmaf_rn(xv[kx], wk[c], s[kx][c]);
+  }
+}
+
+template <int CO>
+__global__ __launch_bounds__(kBlock) void k_real_conv(const RealArgs a, uint32_t xbytes) {
+  const int HW = a.H * a.W;
+  const long total = (long)a.N * HW;
+  long p = (long)blockIdx.x * kBlock + threadIdx.x;
+  const bool active = p < total;
+  if (!active) p = total - 1;
+  const int n = (int)(p / HW);
+  const int r = (int)(p - (long)n * HW);
+  const int y = r / a.W, x = r - y * a.W;
+  const uint32_t plane0 = (uint32_t)n * (uint32_t)a.cin * (uint32_t)HW;
+  const uint32_t pstride = (uint32_t)HW * 4u;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
+
+  float acc[CO];
+#pragma unroll
+  for (int c = 0; c < CO; ++c) acc[c] = 0.0f;
+
+#pragma unroll 1
+  for (int ky = 0; ky < 3; ++ky) {
+    const int iy = y + ky - 1;
+    const bool rowok = iy >= 0 && iy < a.H;
+    uint32_t off[3];
+    bool ok[3];
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx) {
+      const int ix = x + kx - 1;
+      ok[kx] = rowok && ix >= 0 && ix < a.W;
+      off[kx] = (plane0 + (ok[kx] ? (uint32_t)(iy * a.W + ix) : (uint32_t)r)) * 4u;
+    }
+    float s[3][CO];
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+      for (int c = 0; c < CO; ++c) s[kx][c] = 0.0f;
+    const float* wr = a.w + (size_t)ky * 3 * a.cin * CO;
+    // two register sets: the loads for term ci+1 are in flight while ci is summed
+    float xa[3], xb[3];
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx) xa[kx] = ld_f32(rs, off[kx], 0);
+    int ci = 0;
+#pragma unroll 1
+    for (; ci + 2 <= a.cin; ci += 2) {
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) xb[kx] = ld_f32(rs, off[kx], (uint32_t)(ci + 1) * pstride);
+      fma_terms<CO>(s, xa, wr, a.cin, ci);
+      const int cn = ci + 2 < a.cin ? ci + 2 : ci + 1;
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) xa[kx] = ld_f32(rs, off[kx], (uint32_t)cn * pstride);
+      fma_terms<CO>(s, xb, wr, a.cin, ci + 1);
+    }
+    if (ci < a.cin) fma_terms<CO>(s, xa, wr, a.cin, ci);
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+      for (int c = 0; c < CO; ++c) {
+        const float t = __fadd_rn(acc[c], s[kx][c]);
+        acc[c] = ok[kx] ? t : acc[c];
+      }
+  }
+  if (!active) return;
+  const int nco = a.cout - a.co0 < CO ? a.cout - a.co0 : CO;
+  if (a.f32) {
+#pragma unroll
+    for (int c = 0; c < CO; ++c)
+      if (c < nco)
+        a.f32[((size_t)n * a.cout + a.co0 + c) * HW + r] = __fmul_rn(a.alpha[a.co0 + c], acc[c]);
+  }
+  if (a.out) {
+    // real fold (csrc/bnn_fold.c:62-77): z = fma(A, x, B); z<0 -> slope*z;
+    // r = z + rsign; bit = r > 0.  The reference build fuses A*x+B only.
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < CO; ++c) {
+      const int co = a.co0 + c;
+      const float o = __fmul_rn(a.alpha[co], acc[c]);
+      float z = __fmaf_rn(a.A[co], o, a.B[co]);
+      if (z < 0.0f) z = __fmul_rn(a.slope[co], z);
+      const float rr = __fadd_rn(z, a.rsign[co]);
+      word |= (rr > 0.0f && c < nco) ? (1u << c) : 0u;
+    }
+    const int cwo = (a.cout + 31) >> 5;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out) + ((size_t)p * cwo) * 4 + (a.co0 >> 3);
+    if (CO == 32) *reinterpret_cast<uint32_t*>(dst) = word;
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+  }
+}
+
+// ------------------------------------------------------------------------
+// binary conv with fused epilogues
+// ------------------------------------------------------------------------
+template <int MT, int COG>
+struct Acc {
+  uint32_t d[MT * MT][COG];
+};
+
+// D[p][j] += sum over taps popcount((a ^ w) & m) for one 32-channel word.
+template <int MT, int COG>
+__device__ __forceinline__ void accumulate(Acc<MT, COG>& D, const uint32_t (&av)[MT + 2][MT + 2],
+                                           const uint32_t (&m)[MT + 2][MT + 2],
+                                           const uint32_t* __restrict__ wrow) {
+#pragma unroll
+  for (int j = 0; j < COG; ++j) {
+    uint32_t w9[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) w9[t] = wrow[j * 9 + t];
+#pragma unroll
+    for (int py = 0; py < MT; ++py)
+#pragma unroll
+      for (int px = 0; px < MT; ++px) {
+        uint32_t d = D.d[py * MT + px][j];
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+          for (int kx = 0; kx < 3; ++kx) {
+            const uint32_t v = (av[py + ky][px + kx] ^ w9[ky * 3 + kx]) & m[py + ky][px + kx];
+            d = (uint32_t)__builtin_popcount(v) + d;
+          }
+        D.d[py * MT + px][j] = d;
+      }
+  }
+}
+
+__device__ __forceinline__ uint32_t fold_bit(int32_t P, const FoldDev& f, int co) {
+  return ((uint32_t)(P - f.lo[co]) < f.wid[co]) ? 1u : 0u;
+}
+__device__ __forceinline__ uint32_t inv_bits(const FoldDev& f, int co0, int cog) {
+  const uint32_t w = f.inv[co0 >> 5] >> (co0 & 31);
+  return cog == 32 ? w : (w & ((1u << cog) - 1u));
+}
+template <int COG>
+__device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, int co0, uint32_t bits) {
+  uint8_t* dst = reinterpret_cast<uint8_t*>(base) + pix * (size_t)cw * 4 + (co0 >> 3);
+  if (COG == 32) *reinterpret_cast<uint32_t*>(dst) = bits;
+  else if (COG == 16) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bits;
+  else *dst = (uint8_t)bits;
+}
+
+template <int MT, int COG, int EPI, bool DUMP>
+__global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t bytes0, uint32_t bytes1) {
+  constexpr int NP = MT + 2;
+  const int tH = (a.H + MT - 1) / MT, tW = (a.W + MT - 1) / MT;
+  const int per = tH * tW;
+  const long ntiles = (long)a.N * per;
+  long tile = (long)blockIdx.x * kBlock + threadIdx.x;
+  const bool active = tile < ntiles;
+  if (!active) tile = ntiles - 1;
+  const int n = (int)(tile / per);
+  const int rr = (int)(tile - (long)n * per);
+  const int ty = rr / tW, tx = rr - ty * tW;
+  const int y0 = ty * MT, x0 = tx * MT;
+  const int co0 = blockIdx.y * COG;
+  const int coutp = (a.cout + 31) & ~31;  // weight rows are padded to 32
+
+  uint32_t m[NP][NP];
+  uint32_t voff[NP][NP];
+  bool rok[NP], cok[NP];
+  int rc[NP], cc[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int iy = y0 - 1 + i, ix = x0 - 1 + i;
+    rok[i] = iy >= 0 && iy < a.H;
+    cok[i] = ix >= 0 && ix < a.W;
+    rc[i] = rok[i] ? iy : (iy < 0 ? 0 : a.H - 1);
+    cc[i] = cok[i] ? ix : (ix < 0 ? 0 : a.W - 1);
+  }
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      m[i][k] = (rok[i] && cok[k]) ? ~0u : 0u;
+      voff[i][k] = (uint32_t)(((size_t)n * a.H + rc[i]) * a.W + cc[k]) * (uint32_t)a.cw0 * 4u;
+    }
+
+  Acc<MT, COG> D;
+#pragma unroll
+  for (int p = 0; p < MT * MT; ++p)
+#pragma unroll
+    for (int j = 0; j < COG; ++j) D.d[p][j] = 0;
+
+  {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in0, bytes0);
+#pragma unroll 1
+    for (int w = 0; w < a.cw0; ++w) {
+      uint32_t av[NP][NP];
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+#pragma unroll
+        for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, voff[i][k], (uint32_t)w * 4u);
+      accumulate<MT, COG>(D, av, m, a.wt + ((size_t)w * coutp + co0) * 9);
+    }
+  }
+  if (a.cw1 > 0) {
+    // nearest 2x of the low-res tensor placed at (oh, ow); uncovered in-image
+    // positions read as 0 bits (the reference's zero-filled concat, whose 0
+    // entries its XNOR kernels treat as -1: csrc/bnn_model.c:130-148,
+    // csrc/bnn_conv.c:123, 162)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in1, bytes1);
+    uint32_t cm[NP][NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+#pragma unroll
+      for (int k = 0; k < NP; ++k) {
+        const int uy = rc[i] - a.oh, ux = cc[k] - a.ow;
+        const bool cov = uy >= 0 && uy < a.uh && ux >= 0 && ux < a.uw;
+        cm[i][k] = cov ? ~0u : 0u;
+        const int ly = cov ? (uy >> 1) : 0, lx = cov ? (ux >> 1) : 0;
+        voff[i][k] = (uint32_t)(((size_t)n * a.h1 + ly) * a.w1 + lx) * (uint32_t)a.cw1 * 4u;
+      }
+#pragma unroll 1
+    for (int w = 0; w < a.cw1; ++w) {
+      uint32_t av[NP][NP];
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+#pragma unroll
+        for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, voff[i][k], (uint32_t)w * 4u) & cm[i][k];
+      accumulate<MT, COG>(D, av, m, a.wt + ((size_t)(a.cw0 + w) * coutp + co0) * 9);
+    }
+  }
+  if (!active) return;
+
+  // ---------------------------------------------------------- epilogue --
+  int32_t Pv[MT * MT][COG];
+  bool inimg[MT * MT];
+#pragma unroll
+  for (int py = 0; py < MT; ++py)
+#pragma unroll
+    for (int px = 0; px < MT; ++px) {
+      const int y = y0 + py, x = x0 + px;
+      inimg[py * MT + px] = y < a.H && x < a.W;
+      const int nr = (int)rok[py] + (int)rok[py + 1] + (int)rok[py + 2];
+      const int nc = (int)cok[px] + (int)cok[px + 1] + (int)cok[px + 2];
+      const int32_t nvalid = nr * nc * a.cin;
+#pragma unroll
+      for (int j = 0; j < COG; ++j) Pv[py * MT + px][j] = nvalid - 2 * (int32_t)D.d[py * MT + px][j];
+    }
+
+  const int HW = a.H * a.W;
+  if (EPI == EPI_P || DUMP) {
+#pragma unroll
+    for (int py = 0; py < MT; ++py)
+#pragma unroll
+      for (int px = 0; px < MT; ++px) {
+        if (!inimg[py * MT + px]) continue;
+        const int pix = (y0 + py) * a.W + x0 + px;
+#pragma unroll
+        for (int j = 0; j < COG; ++j)
+          if (co0 + j < a.cout) a.P[((size_t)n * a.cout + co0 + j) * HW + pix] = Pv[py * MT + px][j];
+      }
+  }
+  if (EPI == EPI_P) return;
+
+  const uint32_t inv1 = inv_bits(a.f1, co0, COG);
+  uint32_t bits[MT * MT];
+#pragma unroll
+  for (int p = 0; p < MT * MT; ++p) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int j = 0; j < COG; ++j) b |= fold_bit(Pv[p][j], a.f1, co0 + j) << j;
+    bits[p] = b ^ inv1;
+  }
+
+  if (EPI == EPI_FOLD || (EPI == EPI_POOL && a.out != nullptr)) {
+#pragma unroll
+    for (int py = 0; py < MT; ++py)
+#pragma unroll
+      for (int px = 0; px < MT; ++px)
+        if (inimg[py * MT + px])
+          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, bits[py * MT + px]);
+  }
+  if (EPI == EPI_POOL) {
+    // 2x2 floor-mode max on P (csrc/bnn_maxpool.c:28-48), then the down rule
+    if (y0 + 1 < a.H && x0 + 1 < a.W) {
+      const int Hh = a.H >> 1, Wh = a.W >> 1;
+      uint32_t b = 0;
+#pragma unroll
+      for (int j = 0; j < COG; ++j) {
+        const int32_t pm = max(max(Pv[0][j], Pv[1][j]), max(Pv[2][j], Pv[3][j]));
+        b |= fold_bit(pm, a.f2, co0 + j) << j;
+        if (DUMP && co0 + j < a.cout)
+          a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
+      }
+      b ^= inv_bits(a.f2, co0, COG);
+      store_bits<COG>(a.out2, ((size_t)n * Hh + ty) * Wh + tx, a.cwo, co0, b);
+    }
+  }
+  if (EPI == EPI_HEAD) {
+    // widen +-1 to float and the 1x1 head: bias first, then channels in
+    // order, one fused step each (csrc/bnn_head.c:21-34)
+    if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, bits[0]);
+    const int pix = y0 * a.W + x0;
+#pragma unroll 1
+    for (int o = 0; o < a.ncls; ++o) {
+      float accf = a.hb[o];
+#pragma unroll
+      for (int j = 0; j < COG; ++j)
+        if (j < a.cout)
+          accf = __fmaf_rn(a.hw[o * a.cout + j], ((bits[0] >> j) & 1u) ? 1.0f : -1.0f, accf);
+      a.logits[((size_t)n * a.ncls + o) * HW + pix] = accf;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------
+// simple kernels for the batch-1 kernel ABI
+// ------------------------------------------------------------------------
+// int8 [N][C][H][W] (value > 0 -> bit 1) -> uint32 [N][H][W][ceil(C/32)]
+__global__ void k_pack_act(const int8_t* __restrict__ a, uint32_t* __restrict__ out, int N, int C, int H, int W) {
+  const int cw = (C + 31) >> 5;
+  const long HW = (long)H * W;
+  const long total = (long)N * HW * cw;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int w = (int)(i % cw);
+  const long pix = i / cw;
+  const long n = pix / HW, p = pix - n * HW;
+  uint32_t word = 0;
+  for (int b = 0; b < 32; ++b) {
+    const int c = w * 32 + b;
+    if (c < C && a[((size_t)n * C + c) * HW + p] > 0) word |= 1u << b;
+  }
+  out[i] = word;
+}
+
+__global__ void k_bconv_generic(const uint32_t* __restrict__ act, const uint32_t* __restrict__ wt,
+                                int32_t* __restrict__ P, int cin, int H, int W, int cout, int kh, int kw,
+                                int pad, int stride) {
+  const int Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  const long total = (long)cout * Ho * Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int co = (int)(i / ((long)Ho * Wo));
+  const int r = (int)(i - (long)co * Ho * Wo);
+  const int oy = r / Wo, ox = r - oy * Wo;
+  const int cw = (cin + 31) >> 5, taps = kh * kw;
+  int nvalid = 0;
+  uint32_t d = 0;
+  for (int ky = 0; ky < kh; ++ky) {
+    const int iy = oy * stride + ky - pad;
+    if (iy < 0 || iy >= H) continue;
+    for (int kx = 0; kx < kw; ++kx) {
+      const int ix = ox * stride + kx - pad;
+      if (ix < 0 || ix >= W) continue;
+      nvalid += cin;
+      for (int w = 0; w < cw; ++w)
+        d += __builtin_popcount(act[((size_t)iy * W + ix) * cw + w] ^ wt[((size_t)w * cout + co) * taps + ky * kw + kx]);
+    }
+  }
+  P[i] = nvalid - 2 * (int32_t)d;
+}
+
+__global__ void k_bconv_naive(const int8_t* __restrict__ a, const int8_t* __restrict__ w, int32_t* __restrict__ P,
+                              int cin, int H, int W, int cout, int kh, int kw, int pad, int stride) {
+  const int Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  const long total = (long)cout * Ho * Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int co = (int)(i / ((long)Ho * Wo));
+  const int r = (int)(i - (long)co * Ho * Wo);
+  const int oy = r / Wo, ox = r - oy * Wo;
+  int32_t acc = 0;
+  for (int ci = 0; ci < cin; ++ci)
+    for (int ky = 0; ky < kh; ++ky) {
+      const int iy = oy * stride + ky - pad;
+      if (iy < 0 || iy >= H) continue;
+      for (int kx = 0; kx < kw; ++kx) {
+        const int ix = ox * stride + kx - pad;
+        if (ix < 0 || ix >= W) continue;
+        acc += (int32_t)w[(((size_t)co * cin + ci) * kh + ky) * kw + kx] * (int32_t)a[((size_t)ci * H + iy) * W + ix];
+      }
+    }
+  P[i] = acc;
+}
+
+// general-shape real conv in the reference order; w is float [cout][kh][kw][cin]
+__global__ void k_real_generic(const float* __restrict__ x, const float* __restrict__ w,
+                               const float* __restrict__ alpha, float* __restrict__ out, int cin, int H,
+                               int W, int cout, int kh, int kw, int pad, int stride) {
+  const int Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  const long total = (long)cout * Ho * Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int co = (int)(i / ((long)Ho * Wo));
+  const int r = (int)(i - (long)co * Ho * Wo);
+  const int oy = r / Wo, ox = r - oy * Wo;
+  const int y0 = oy * stride - pad, x0 = ox * stride - pad;
+  const int ky0 = y0 < 0 ? -y0 : 0, ky1 = y0 + kh > H ? H - y0 : kh;
+  const int kx0 = x0 < 0 ? -x0 : 0, kx1 = x0 + kw > W ? W - x0 : kw;
+  float acc = 0.0f;
+  for (int ky = ky0; ky < ky1; ++ky)
+    for (int kx = kx0; kx < kx1; ++kx) {
+      const float* wv = w + (((size_t)co * kh + ky) * kw + kx) * cin;
+      const size_t pix = (size_t)(y0 + ky) * W + (x0 + kx);
+      float s = 0.0f;
+      for (int ci = 0; ci < cin; ++ci) s = __fadd_rn(s, __fmul_rn(x[(size_t)ci * H * W + pix], wv[ci]));
+      acc = __fadd_rn(acc, s);
+    }
+  out[i] = __fmul_rn(alpha[co], acc);
+}
+
+__global__ void k_maxpool(const int32_t* __restrict__ P, int32_t* __restrict__ out, int C, int H, int W, int k,
+                          int stride) {
+  const int Ho = (H - k) / stride + 1, Wo = (W - k) / stride + 1;
+  const long total = (long)C * Ho * Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i / ((long)Ho * Wo));
+  const int r = (int)(i - (long)c * Ho * Wo);
+  const int oy = r / Wo, ox = r - oy * Wo;
+  int32_t mx = INT32_MIN;
+  for (int dy = 0; dy < k; ++dy)
+    for (int dx = 0; dx < k; ++dx)
+      mx = max(mx, P[((size_t)c * H + oy * stride + dy) * W + ox * stride + dx]);
+  out[i] = mx;
+}
+
+__global__ void k_fold_int(const int32_t* __restrict__ P, int8_t* __restrict__ out, int C, int HW,
+                           const int32_t* __restrict__ type, const int32_t* __restrict__ t,
+                           const int32_t* __restrict__ lo, const int32_t* __restrict__ hi) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)C * HW) return;
+  const int c = (int)(i / HW);
+  const int32_t v = P[i];
+  bool on;
+  switch (type[c]) {
+    case 0: on = t[c] > 0; break;
+    case 1: on = v >= t[c]; break;
+    case 2: on = v < t[c]; break;
+    case 3: on = v >= lo[c] && v < hi[c]; break;
+    case 4: on = v < lo[c] || v >= hi[c]; break;
+    default: on = false; break;
+  }
+  out[i] = on ? 1 : -1;
+}
+
+__global__ void k_fold_real(const float* __restrict__ x, int8_t* __restrict__ out, int C, int HW,
+                            const float* __restrict__ A, const float* __restrict__ B,
+                            const float* __restrict__ slope, const float* __restrict__ rsign) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)C * HW) return;
+  const int c = (int)(i / HW);
+  float z = __fmaf_rn(A[c], x[i], B[c]);
+  if (z < 0.0f) z = __fmul_rn(slope[c], z);
+  const float r = __fadd_rn(z, rsign[c]);
+  out[i] = r > 0.0f ? 1 : -1;
+}
+
+__global__ void k_head(const float* __restrict__ a, const float* __restrict__ W, const float* __restrict__ b,
+                       float* __restrict__ out, int cin, int HW, int cout) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)cout * HW) return;
+  const int o = (int)(i / HW);
+  const long p = i - (long)o * HW;
+  float acc = b[o];
+  for (int c = 0; c < cin; ++c) acc = __fmaf_rn(W[(size_t)o * cin + c], a[(size_t)c * HW + p], acc);
+  out[i] = acc;
+}
+
+inline unsigned blocks_for(long n, int bs = kBlock) { return (unsigned)((n + bs - 1) / bs); }
+
+template <int MT, int COG, int EPI, bool DUMP>
+hipError_t go_bconv(const BconvArgs& a, hipStream_t s) {
+  const long ntiles = (long)a.N * ((a.H + MT - 1) / MT) * ((a.W + MT - 1) / MT);
+  const int groups = (a.cout + COG - 1) / COG;
+  const uint32_t b0 = (uint32_t)((size_t)a.N * a.H * a.W * a.cw0 * 4);
+  const uint32_t b1 = a.in1 ? (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4) : 0u;
+  hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for(ntiles), groups), dim3(kBlock), 0, s, a,
+                     b0, b1);
+  return hipGetLastError();
+}
+
+template <int MT, int EPI, bool DUMP>
+hipError_t go_bconv_cog(const BconvArgs& a, int cog, hipStream_t s) {
+  switch (cog) {
+    case 8: return go_bconv<MT, 8, EPI, DUMP>(a, s);
+    case 16: return go_bconv<MT, 16, EPI, DUMP>(a, s);
+    case 32:
+      // a 2x2 block with 32 channels needs more than 256 VGPRs
+      if constexpr (MT == 1) return go_bconv<MT, 32, EPI, DUMP>(a, s);
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump, hipStream_t s) {
+  if (a.N <= 0 || a.H <= 0 || a.W <= 0) return hipSuccess;
+  if ((size_t)a.N * a.H * a.W * (a.cw0 > 0 ? a.cw0 : 1) * 4 >= 0xffffffffull) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_FOLD:
+      if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);
+      if (mt == 2) return dump ? go_bconv_cog<2, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<2, EPI_FOLD, false>(a, cog, s);
+      break;
+    case EPI_POOL:
+      if (mt == 2) return dump ? go_bconv_cog<2, EPI_POOL, true>(a, cog, s) : go_bconv_cog<2, EPI_POOL, false>(a, cog, s);
+      break;
+    case EPI_HEAD:
+      if (mt != 1) break;
+      if (cog == 16) return dump ? go_bconv<1, 16, EPI_HEAD, true>(a, s) : go_bconv<1, 16, EPI_HEAD, false>(a, s);
+      if (cog == 32) return dump ? go_bconv<1, 32, EPI_HEAD, true>(a, s) : go_bconv<1, 32, EPI_HEAD, false>(a, s);
+      break;
+    case EPI_P:
+      if (mt == 1) return go_bconv_cog<1, EPI_P, false>(a, cog, s);
+      if (mt == 2) return go_bconv_cog<2, EPI_P, false>(a, cog, s);
+      break;
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_real(const RealArgs& a, hipStream_t s) {
+  const long total = (long)a.N * a.H * a.W;
+  if (total <= 0) return hipSuccess;
+  const size_t xbytes = (size_t)a.N * a.cin * a.H * a.W * 4;
+  if (xbytes >= 0xffffffffull) return hipErrorInvalidValue;
+  if (a.CO != 16 && a.CO != 32) return hipErrorInvalidValue;
+  if (a.CO == 32)
+    hipLaunchKernelGGL(k_real_conv<32>, dim3(blocks_for(total)), dim3(kBlock), 0, s, a, (uint32_t)xbytes);
+  else
+    hipLaunchKernelGGL(k_real_conv<16>, dim3(blocks_for(total)), dim3(kBlock), 0, s, a, (uint32_t)xbytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_act(const int8_t* a, uint32_t* out, int N, int C, int H, int W, hipStream_t s) {
+  const long n = (long)N * H * W * ((C + 31) >> 5);
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pack_act, dim3(blocks_for(n)), dim3(kBlock), 0, s, a, out, N, C, H, W);
+  return hipGetLastError();
+}
+
+hipError_t launch_bconv_generic(const uint32_t* act, const uint32_t* wt, int32_t* P, int cin, int H, int W,
+                                int cout, int kh, int kw, int pad, int stride, hipStream_t s) {
+  const long Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  if (Ho <= 0 || Wo <= 0 || cout <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_bconv_generic, dim3(blocks_for((long)cout * Ho * Wo)), dim3(kBlock), 0, s, act, wt, P,
+                     cin, H, W, cout, kh, kw, pad, stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_bconv_naive(const int8_t* a, const int8_t* w, int32_t* P, int cin, int H, int W, int cout,
+                              int kh, int kw, int pad, int stride, hipStream_t s) {
+  const long Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  if (Ho <= 0 || Wo <= 0 || cout <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_bconv_naive, dim3(blocks_for((long)cout * Ho * Wo)), dim3(kBlock), 0, s, a, w, P, cin,
+                     H, W, cout, kh, kw, pad, stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_real_generic(const float* x, const float* w, const float* alpha, float* out, int cin, int H,
+                               int W, int cout, int kh, int kw, int pad, int stride, hipStream_t s) {
+  const long Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
+  if (Ho <= 0 || Wo <= 0 || cout <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_real_generic, dim3(blocks_for((long)cout * Ho * Wo)), dim3(kBlock), 0, s, x, w, alpha,
+                     out, cin, H, W, cout, kh, kw, pad, stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_maxpool(const int32_t* P, int32_t* out, int C, int H, int W, int k, int stride,
+                          hipStream_t s) {
+  const long Ho = (H - k) / stride + 1, Wo = (W - k) / stride + 1;
+  if (Ho <= 0 || Wo <= 0 || C <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_maxpool, dim3(blocks_for((long)C * Ho * Wo)), dim3(kBlock), 0, s, P, out, C, H, W, k,
+                     stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_fold_int(const int32_t* P, int8_t* out, int C, int HW, const int32_t* type, const int32_t* t,
+                           const int32_t* lo, const int32_t* hi, hipStream_t s) {
+  const long n = (long)C * HW;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fold_int, dim3(blocks_for(n)), dim3(kBlock), 0, s, P, out, C, HW, type, t, lo, hi);
+  return hipGetLastError();
+}
+
+hipError_t launch_fold_real(const float* x, int8_t* out, int C, int HW, const float* A, const float* B,
+                            const float* slope, const float* rsign, hipStream_t s) {
+  const long n = (long)C * HW;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fold_real, dim3(blocks_for(n)), dim3(kBlock), 0, s, x, out, C, HW, A, B, slope, rsign);
+  return hipGetLastError();
+}
+
+hipError_t launch_head(const float* a, const float* W, const float* b, float* out, int cin, int HW, int cout,
+                       hipStream_t s) {
+  const long n = (long)cout * HW;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_head, dim3(blocks_for(n)), dim3(kBlock), 0, s, a, W, b, out, cin, HW, cout);
+  return hipGetLastError();
+}
+
+}  // namespace bnn

@@ -1,0 +1,161 @@
+"""Seeded synthetic blobs and inputs for the v1 Bi-Real UNet.
+
+The topology is the dual-skip UNet the v1 engine assembles
+(csrc/bnn_model.c:150-253; widths as in csrc/bench_bconv.c:57-67 and
+python/bnn2c/blob_react.py:52-58): with base width c,
+
+    enc1 conv1 n_bands->c (real input), conv2 c->c
+    enc2 c->2c, 2c->2c      enc3 2c->4c, 4c->4c      enc4 4c->8c, 8c->8c
+    bott 8c->16c, 16c->16c
+    dec4 (8c+16c)->8c, 8c->8c   dec3 (4c+8c)->4c, 4c->4c
+    dec2 (2c+4c)->2c, 2c->2c    dec1 (c+2c)->c, c->c
+    head c->n_classes (fp32 1x1)
+
+Random parameters follow the benchmark recipe: binary weights are
+Bernoulli(0.5) sign bits; each integer fold is a per-channel threshold
+t ~ U[-fan_in/4, fan_in/4] with a Bernoulli(0.5) ge/lt flag; head weights
+~ N(0, 0.05).  Choices the recipe leaves open, fixed here and recorded with
+every fixture: real first-conv weights w ~ N(0, 1/sqrt(fan_in)) giving
+wsign = sign(w) (0 -> +1) and alpha = mean|w|; real fold A ~ U(0.5, 1.5),
+B ~ N(0, 0.1), slope ~ U(-0.5, 0.5), rsign ~ N(0, 0.1); head bias ~ N(0, 0.05).
+
+`coverage=True` draws every integer rule type (const, ge, lt, band_in,
+band_out and an unknown code, which the C fold maps to -1;
+csrc/bnn_fold.c:49-56) so the fold paths the recipe never reaches are
+exercised.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import blob as B
+
+
+def topology(base: int, n_bands: int):
+    """[(name, cin, cout)] for the 18 convs in blob order."""
+    c = base
+    enc = [(n_bands, c), (c, 2 * c), (2 * c, 4 * c), (4 * c, 8 * c)]
+    convs = []
+    for i, (ci, co) in enumerate(enc):
+        convs.append((f"enc{i + 1}.conv1", ci, co))
+        convs.append((f"enc{i + 1}.conv2", co, co))
+    convs.append(("bott.conv1", 8 * c, 16 * c))
+    convs.append(("bott.conv2", 16 * c, 16 * c))
+    skips = [8 * c, 4 * c, 2 * c, c]         # dec4..dec1 skip widths
+    up = 16 * c
+    for j, s in enumerate(skips):
+        convs.append((f"dec{4 - j}.conv1", s + up, s))
+        convs.append((f"dec{4 - j}.conv2", s, s))
+        up = s
+    return convs
+
+
+def _bin_conv(rng, cin, cout):
+    wsign = np.where(rng.random((cout, cin, 3, 3)) < 0.5, -1, 1).astype(np.int8)
+    return B.Conv(B.TAG_CONV_BIN, cout, cin, 3, 3, 1, 1, packed=B.pack_kidx(wsign))
+
+
+def _real_conv(rng, cin, cout):
+    fan_in = cin * 9
+    w = rng.normal(0.0, 1.0 / np.sqrt(fan_in), (cout, cin, 3, 3)).astype(np.float32)
+    wsign = np.where(w >= 0, 1, -1).astype(np.int8)
+    alpha = np.abs(w).mean(axis=(1, 2, 3)).astype(np.float32)
+    return B.Conv(B.TAG_CONV_REAL, cout, cin, 3, 3, 1, 1, wsign=wsign, alpha=alpha)
+
+
+def _int_act(rng, c, fan_in, coverage):
+    q = fan_in // 4
+    t = rng.integers(-q, q + 1, size=c).astype(np.int32)
+    ge = rng.random(c) < 0.5
+    ty = np.where(ge, B.RULE_GE, B.RULE_LT).astype(np.int32)
+    lo = np.zeros(c, np.int32)
+    hi = np.zeros(c, np.int32)
+    if coverage:
+        # mix every rule code, including an unknown one (5)
+        ty = rng.integers(0, 6, size=c).astype(np.int32)
+        s = max(1, int(np.sqrt(fan_in)))
+        centre = rng.integers(-s, s + 1, size=c)
+        width = rng.integers(0, 2 * s + 1, size=c)
+        lo = (centre - width // 2).astype(np.int32)
+        hi = (lo + width).astype(np.int32)
+        swap = rng.random(c) < 0.1           # occasionally lo >= hi
+        lo[swap], hi[swap] = hi[swap] + 1, lo[swap]
+        const = ty == B.RULE_CONST
+        t[const] = np.where(rng.random(int(const.sum())) < 0.5, 1, -1)
+    return B.Act(0, c, type=ty, t=t, lo=lo, hi=hi)
+
+
+def _real_act(rng, c):
+    A = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    Bv = rng.normal(0.0, 0.1, c).astype(np.float32)
+    slope = rng.uniform(-0.5, 0.5, c).astype(np.float32)
+    rsign = rng.normal(0.0, 0.1, c).astype(np.float32)
+    return B.Act(1, c, A=A, B=Bv, slope=slope, rsign=rsign)
+
+
+def make_blob(seed: int = 0, base: int = 16, n_bands: int = 120,
+              n_classes: int = 3, coverage: bool = False) -> B.BlobV1:
+    rng = np.random.default_rng(seed)
+    topo = dict((n, (ci, co)) for n, ci, co in topology(base, n_bands))
+    b = B.BlobV1(base_channels=base, n_bands=n_bands, n_classes=n_classes)
+    for i in range(4):
+        ci, co = topo[f"enc{i + 1}.conv1"]
+        if i == 0:
+            b.enc_conv1.append(_real_conv(rng, ci, co))
+            b.enc_act1.append(_real_act(rng, co))
+        else:
+            b.enc_conv1.append(_bin_conv(rng, ci, co))
+            b.enc_act1.append(_int_act(rng, co, ci * 9, coverage))
+        ci2, co2 = topo[f"enc{i + 1}.conv2"]
+        b.enc_conv2.append(_bin_conv(rng, ci2, co2))
+        b.enc_act2_skip.append(_int_act(rng, co2, ci2 * 9, coverage))
+        b.enc_act2_down.append(_int_act(rng, co2, ci2 * 9, coverage))
+    for k in ("conv1", "conv2"):
+        ci, co = topo[f"bott.{k}"]
+        setattr(b, f"bott_{k}", _bin_conv(rng, ci, co))
+        setattr(b, f"bott_act{k[-1]}", _int_act(rng, co, ci * 9, coverage))
+    for j in range(4):
+        st = f"dec{4 - j}"
+        ci, co = topo[f"{st}.conv1"]
+        b.dec_conv1.append(_bin_conv(rng, ci, co))
+        b.dec_act1.append(_int_act(rng, co, ci * 9, coverage))
+        ci, co = topo[f"{st}.conv2"]
+        b.dec_conv2.append(_bin_conv(rng, ci, co))
+        b.dec_act2.append(_int_act(rng, co, ci * 9, coverage))
+    W = rng.normal(0.0, 0.05, (n_classes, base)).astype(np.float32)
+    bias = rng.normal(0.0, 0.05, n_classes).astype(np.float32)
+    b.head = B.Head(n_classes, base, W, bias)
+    return b
+
+
+def make_input(seed: int, n: int, n_bands: int = 120, h: int = 32, w: int = 32) -> np.ndarray:
+    """x ~ N(0,1) float32 [n, n_bands, h, w] ([band,row,col] per patch)."""
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((n, n_bands, h, w), dtype=np.float32)
+
+
+# ------------------------------------------------- isolated-kernel configs --
+def make_bits(seed: int, n: int, h: int, w: int, c: int) -> np.ndarray:
+    """Bernoulli(0.5) +-1 activations int8 [n, c, h, w]."""
+    rng = np.random.default_rng(seed)
+    return np.where(rng.random((n, c, h, w)) < 0.5, -1, 1).astype(np.int8)
+
+
+def make_signs(seed: int, cout: int, cin: int, k: int = 3) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return np.where(rng.random((cout, cin, k, k)) < 0.5, -1, 1).astype(np.int8)
+
+
+def make_rules(seed: int, c: int, fan_in: int, coverage: bool = True):
+    """Per-channel integer rules (type, t, lo, hi) as drawn for a blob."""
+    a = _int_act(np.random.default_rng(seed), c, fan_in, coverage)
+    return a.type, a.t, a.lo, a.hi
+
+
+def make_thresholds(seed: int, c: int, bound: int):
+    """cfg2 fold: t ~ U[-bound, bound], Bernoulli(0.5) ge/lt direction."""
+    rng = np.random.default_rng(seed)
+    t = rng.integers(-bound, bound + 1, size=c).astype(np.int32)
+    ty = np.where(rng.random(c) < 0.5, B.RULE_GE, B.RULE_LT).astype(np.int32)
+    z = np.zeros(c, np.int32)
+    return ty, t, z, z.copy()

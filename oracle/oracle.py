@@ -1,0 +1,315 @@
+"""ctypes bindings for the CPU checker. TEST INFRASTRUCTURE ONLY.
+
+`Oracle` wraps liboracle.so, the clean-room C restatement of the reference v1
+forward (oracle/bnn_oracle.c).  `RefC` wraps oracle/_ref/libbnnref.so, the
+reference's own C sources compiled by `make -C oracle ref`; it exists only
+where /root/reference was present at build time (or the built file travelled
+with the tree), and every user of it must treat it as optional.
+
+Arrays are numpy, batch-1 row-major exactly as the C signatures take them.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from typing import Dict, Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libbnnref.so")
+REF_CLI = os.path.join(HERE, "_ref", "bnn_infer")
+
+_i8 = C.POINTER(C.c_int8)
+_i32 = C.POINTER(C.c_int32)
+_u64 = C.POINTER(C.c_uint64)
+_f32 = C.POINTER(C.c_float)
+_ci = C.c_int
+
+STAGE_CB = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_int,
+                       C.c_int, C.c_void_p)
+_DT = {0: np.int8, 1: np.int32, 2: np.float32}
+
+
+def _p(a: np.ndarray, ptype):
+    return a.ctypes.data_as(ptype)
+
+
+def build(force: bool = False) -> None:
+    if force or not os.path.exists(LIB):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _out_dim(n, k, pad, stride):
+    return (n + 2 * pad - k) // stride + 1
+
+
+class Oracle:
+    def __init__(self, path: str = LIB):
+        if not os.path.exists(path):
+            build()
+        L = self.lib = C.CDLL(path)
+        L.orc_parse.argtypes = [C.c_char_p, C.c_size_t, _ci, C.POINTER(C.c_void_p), C.c_char_p, _ci]
+        L.orc_free.argtypes = [C.c_void_p]
+        L.orc_forward.argtypes = [C.c_void_p, _f32, _ci, _ci, _f32, STAGE_CB, C.c_void_p]
+        L.orc_forward_batch.argtypes = [C.c_void_p, _f32, _ci, _ci, _ci, _f32]
+        L.orc_forward_batch_par.argtypes = [C.c_void_p, _f32, _ci, _ci, _ci, _f32]
+        L.orc_pack_kidx.argtypes = [_i8, _u64, _ci, _ci, _ci, _ci]
+        for nm in ("orc_bconv_dense", "orc_bconv_chan", "orc_bconv"):
+            getattr(L, nm).argtypes = [_i8, _u64, _i32] + [_ci] * 8
+        L.orc_bconv_naive.argtypes = [_i8, _i8, _i32] + [_ci] * 8
+        L.orc_conv_real.argtypes = [_f32, _i8, _f32, _f32] + [_ci] * 8
+        L.orc_fold_int.argtypes = [_i32, _i8, _ci, _ci, _ci, _i32, _i32, _i32, _i32]
+        L.orc_fold_real.argtypes = [_f32, _i8, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
+        L.orc_maxpool.argtypes = [_i32, _i32, _ci, _ci, _ci, _ci, _ci]
+        L.orc_head.argtypes = [_f32, _f32, _f32, _f32, _ci, _ci, _ci, _ci]
+        L.orc_up_cat.argtypes = [_i8, _ci, _ci, _ci, _i8, _ci, _ci, _ci, _i8]
+
+    # ---- model ----
+    def parse(self, data: bytes, strict: bool = True):
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        rc = self.lib.orc_parse(data, len(data), int(strict), C.byref(h), err, 256)
+        if rc:
+            raise ValueError(err.value.decode())
+        return OracleModel(self, h)
+
+    # ---- kernels ----
+    def pack_kidx(self, wsign):
+        w = np.ascontiguousarray(wsign, np.int8)
+        co, ci, kh, kw = w.shape
+        out = np.zeros((co, (ci * kh * kw + 63) // 64), np.uint64)
+        self.lib.orc_pack_kidx(_p(w, _i8), _p(out, _u64), co, ci, kh, kw)
+        return out
+
+    def bconv(self, a, bits, cout, kh=3, kw=3, pad=1, stride=1, kind="dispatch"):
+        a = np.ascontiguousarray(a, np.int8)
+        bits = np.ascontiguousarray(bits, np.uint64)
+        cin, H, W = a.shape
+        P = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.int32)
+        fn = {"dispatch": "orc_bconv", "dense": "orc_bconv_dense", "chan": "orc_bconv_chan"}[kind]
+        getattr(self.lib, fn)(_p(a, _i8), _p(bits, _u64), _p(P, _i32), cin, H, W, cout, kh, kw, pad, stride)
+        return P
+
+    def bconv_naive(self, a, wsign, pad=1, stride=1):
+        a = np.ascontiguousarray(a, np.int8)
+        w = np.ascontiguousarray(wsign, np.int8)
+        cin, H, W = a.shape
+        cout, _, kh, kw = w.shape
+        P = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.int32)
+        self.lib.orc_bconv_naive(_p(a, _i8), _p(w, _i8), _p(P, _i32), cin, H, W, cout, kh, kw, pad, stride)
+        return P
+
+    def conv_real(self, x, wsign, alpha, pad=1, stride=1):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(wsign, np.int8)
+        al = np.ascontiguousarray(alpha, np.float32)
+        cin, H, W = x.shape
+        cout, _, kh, kw = w.shape
+        out = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.float32)
+        self.lib.orc_conv_real(_p(x, _f32), _p(w, _i8), _p(al, _f32), _p(out, _f32),
+                               cin, H, W, cout, kh, kw, pad, stride)
+        return out
+
+    def fold_int(self, P, ty, t, lo, hi):
+        P = np.ascontiguousarray(P, np.int32)
+        c, H, W = P.shape
+        out = np.zeros(P.shape, np.int8)
+        arrs = [np.ascontiguousarray(v, np.int32) for v in (ty, t, lo, hi)]
+        self.lib.orc_fold_int(_p(P, _i32), _p(out, _i8), c, H, W, *[_p(v, _i32) for v in arrs])
+        return out
+
+    def fold_real(self, x, A, B, slope, rsign):
+        x = np.ascontiguousarray(x, np.float32)
+        c, H, W = x.shape
+        out = np.zeros(x.shape, np.int8)
+        arrs = [np.ascontiguousarray(v, np.float32) for v in (A, B, slope, rsign)]
+        self.lib.orc_fold_real(_p(x, _f32), _p(out, _i8), c, H, W, *[_p(v, _f32) for v in arrs])
+        return out
+
+    def maxpool(self, P, k=2, stride=2):
+        P = np.ascontiguousarray(P, np.int32)
+        c, H, W = P.shape
+        out = np.zeros((c, (H - k) // stride + 1, (W - k) // stride + 1), np.int32)
+        self.lib.orc_maxpool(_p(P, _i32), _p(out, _i32), c, H, W, k, stride)
+        return out
+
+    def head(self, a, Wt, bias):
+        a = np.ascontiguousarray(a, np.float32)
+        Wt = np.ascontiguousarray(Wt, np.float32)
+        b = np.ascontiguousarray(bias, np.float32)
+        cin, H, W = a.shape
+        out = np.zeros((Wt.shape[0], H, W), np.float32)
+        self.lib.orc_head(_p(a, _f32), _p(Wt, _f32), _p(b, _f32), _p(out, _f32), cin, H, W, Wt.shape[0])
+        return out
+
+    def up_cat(self, skip, x):
+        s = np.ascontiguousarray(skip, np.int8)
+        x = np.ascontiguousarray(x, np.int8)
+        sC, sH, sW = s.shape
+        xC, hH, hW = x.shape
+        out = np.zeros((sC + xC, sH, sW), np.int8)
+        self.lib.orc_up_cat(_p(s, _i8), sC, sH, sW, _p(x, _i8), xC, hH, hW, _p(out, _i8))
+        return out
+
+
+class OracleModel:
+    def __init__(self, orc: Oracle, handle):
+        self.orc = orc
+        self.h = handle
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.orc.lib.orc_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+    def _dims(self):
+        # n_bands / n_classes are the 3rd/4th int of orc_model
+        hdr = (C.c_int * 5).from_address(self.h.value)
+        return hdr[2], hdr[3]
+
+    def forward(self, x: np.ndarray, stages: bool = False):
+        """x [n_bands,H,W] -> logits [n_classes,H,W] (+ dict of every stage)."""
+        x = np.ascontiguousarray(x, np.float32)
+        nb, H, W = x.shape
+        _, ncls = self._dims()
+        logits = np.zeros((ncls, H, W), np.float32)
+        got: Dict[str, np.ndarray] = {}
+
+        def cb(_ctx, name, dtype, c, h, w, data):
+            n = c * h * w
+            arr = np.ctypeslib.as_array(C.cast(data, C.POINTER(np.ctypeslib.as_ctypes_type(_DT[dtype]))),
+                                        shape=(n,)).copy().reshape(c, h, w)
+            got[name.decode()] = arr
+
+        cbf = STAGE_CB(cb) if stages else STAGE_CB()
+        rc = self.orc.lib.orc_forward(self.h, _p(x, _f32), H, W, _p(logits, _f32), cbf, None)
+        if rc:
+            raise ValueError("oracle forward rejected the model/shape")
+        return (logits, got) if stages else logits
+
+    def forward_batch(self, x: np.ndarray, parallel: bool = True) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        N, nb, H, W = x.shape
+        _, ncls = self._dims()
+        out = np.zeros((N, ncls, H, W), np.float32)
+        fn = self.orc.lib.orc_forward_batch_par if parallel else self.orc.lib.orc_forward_batch
+        if fn(self.h, _p(x, _f32), N, H, W, _p(out, _f32)):
+            raise ValueError("oracle forward rejected the model/shape")
+        return out
+
+
+# ------------------------------------------------------------ reference C --
+def ref_available() -> bool:
+    return os.path.exists(REF_LIB)
+
+
+class RefC:
+    """The reference's own C kernels and engine, built from its sources.
+
+    bnn_load() exits the process on a malformed blob (csrc/bnn_model.c:17-24),
+    so only well-formed blobs may be given to it."""
+
+    def __init__(self, path: str = REF_LIB):
+        L = self.lib = C.CDLL(path)
+        L.bnn_load.argtypes = [C.c_char_p]
+        L.bnn_load.restype = C.c_void_p
+        L.bnn_free.argtypes = [C.c_void_p]
+        L.bnn_forward.argtypes = [C.c_void_p, _f32, _ci, _ci, _f32]
+        L.pack_weights.argtypes = [_i8, _u64, _ci, _ci, _ci, _ci]
+        for nm in ("bconv_xnor", "bconv_xnor_packed", "bconv_dispatch"):
+            getattr(L, nm).argtypes = [_i8, _u64, _i32] + [_ci] * 8
+        L.bconv_naive_int.argtypes = [_i8, _i8, _i32] + [_ci] * 8
+        L.conv_realin_naive.argtypes = [_f32, _i8, _f32, _f32] + [_ci] * 8
+        L.apply_fold_int.argtypes = [_i32, _i8, _ci, _ci, _ci, _i32, _i32, _i32, _i32]
+        L.apply_fold_real.argtypes = [_f32, _i8, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
+        L.maxpool_P.argtypes = [_i32, _i32, _ci, _ci, _ci, _ci, _ci]
+        L.head_1x1.argtypes = [_f32, _f32, _f32, _f32, _ci, _ci, _ci, _ci]
+
+    def load(self, path: str):
+        h = self.lib.bnn_load(path.encode())
+        hdr = (C.c_int * 5).from_address(h)
+        return h, hdr[2], hdr[3]
+
+    def forward(self, handle, x: np.ndarray, n_classes: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        _, H, W = x.shape
+        out = np.zeros((n_classes, H, W), np.float32)
+        self.lib.bnn_forward(C.c_void_p(handle), _p(x, _f32), H, W, _p(out, _f32))
+        return out
+
+    def free(self, handle):
+        self.lib.bnn_free(C.c_void_p(handle))
+
+    def bconv(self, a, bits, cout, kh=3, kw=3, pad=1, stride=1, kind="dispatch"):
+        a = np.ascontiguousarray(a, np.int8)
+        bits = np.ascontiguousarray(bits, np.uint64)
+        cin, H, W = a.shape
+        P = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.int32)
+        fn = {"dispatch": "bconv_dispatch", "dense": "bconv_xnor", "chan": "bconv_xnor_packed"}[kind]
+        getattr(self.lib, fn)(_p(a, _i8), _p(bits, _u64), _p(P, _i32), cin, H, W, cout, kh, kw, pad, stride)
+        return P
+
+    def bconv_naive(self, a, wsign, pad=1, stride=1):
+        a = np.ascontiguousarray(a, np.int8)
+        w = np.ascontiguousarray(wsign, np.int8)
+        cin, H, W = a.shape
+        cout, _, kh, kw = w.shape
+        P = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.int32)
+        self.lib.bconv_naive_int(_p(a, _i8), _p(w, _i8), _p(P, _i32), cin, H, W, cout, kh, kw, pad, stride)
+        return P
+
+    def pack_weights(self, wsign):
+        w = np.ascontiguousarray(wsign, np.int8)
+        co, ci, kh, kw = w.shape
+        out = np.zeros((co, (ci * kh * kw + 63) // 64), np.uint64)
+        self.lib.pack_weights(_p(w, _i8), _p(out, _u64), co, ci, kh, kw)
+        return out
+
+    def conv_real(self, x, wsign, alpha, pad=1, stride=1):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(wsign, np.int8)
+        al = np.ascontiguousarray(alpha, np.float32)
+        cin, H, W = x.shape
+        cout, _, kh, kw = w.shape
+        out = np.zeros((cout, _out_dim(H, kh, pad, stride), _out_dim(W, kw, pad, stride)), np.float32)
+        self.lib.conv_realin_naive(_p(x, _f32), _p(w, _i8), _p(al, _f32), _p(out, _f32),
+                                   cin, H, W, cout, kh, kw, pad, stride)
+        return out
+
+    def fold_int(self, P, ty, t, lo, hi):
+        P = np.ascontiguousarray(P, np.int32)
+        c, H, W = P.shape
+        out = np.zeros(P.shape, np.int8)
+        arrs = [np.ascontiguousarray(v, np.int32) for v in (ty, t, lo, hi)]
+        self.lib.apply_fold_int(_p(P, _i32), _p(out, _i8), c, H, W, *[_p(v, _i32) for v in arrs])
+        return out
+
+    def fold_real(self, x, A, B, slope, rsign):
+        x = np.ascontiguousarray(x, np.float32)
+        c, H, W = x.shape
+        out = np.zeros(x.shape, np.int8)
+        arrs = [np.ascontiguousarray(v, np.float32) for v in (A, B, slope, rsign)]
+        self.lib.apply_fold_real(_p(x, _f32), _p(out, _i8), c, H, W, *[_p(v, _f32) for v in arrs])
+        return out
+
+    def maxpool(self, P, k=2, stride=2):
+        P = np.ascontiguousarray(P, np.int32)
+        c, H, W = P.shape
+        out = np.zeros((c, (H - k) // stride + 1, (W - k) // stride + 1), np.int32)
+        self.lib.maxpool_P(_p(P, _i32), _p(out, _i32), c, H, W, k, stride)
+        return out
+
+    def head(self, a, Wt, bias):
+        a = np.ascontiguousarray(a, np.float32)
+        Wt = np.ascontiguousarray(Wt, np.float32)
+        b = np.ascontiguousarray(bias, np.float32)
+        cin, H, W = a.shape
+        out = np.zeros((Wt.shape[0], H, W), np.float32)
+        self.lib.head_1x1(_p(a, _f32), _p(Wt, _f32), _p(b, _f32), _p(out, _f32), cin, H, W, Wt.shape[0])
+        return out

@@ -1,0 +1,73 @@
+"""libbnn_hip.so loads without a GPU and exports every entry point that
+include/bnn_model.h and include/bnn_prof.h declare; host-only pieces of the
+engine are checked here against the checker."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from bnns_to_c_amd import engine as E
+from bnns_to_c_amd import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_header_symbols():
+    lib = E.lib()
+    names = set(E.header_symbols()) | set(E.header_symbols(os.path.join(ROOT, "include", "bnn_prof.h")))
+    assert {"bnn_load", "bnn_forward", "bnn_free", "bconv_dispatch", "head_1x1", "prof_report"} <= names
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", E.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert names <= exported, sorted(names - exported)
+
+
+def test_library_built_for_gfx950():
+    # the offload bundle in .hip_fatbin names its code objects by target id
+    data = open(E.LIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+    assert b"amdgcn-amd-amdhsa--gfx942" not in data
+
+
+def test_header_compiles_as_c(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "bnn_model.h"\n#include "bnn_prof.h"\n'
+                   "int main(void){ Model *m = 0; (void)m; return sizeof(Conv) > 0 ? 0 : 1; }\n")
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    "-c", str(src), "-o", str(tmp_path / "t.o")], check=True)
+
+
+def test_model_struct_prefix_matches_reference():
+    # main.c reads m->n_bands / m->n_classes: the leading ints keep their order
+    class Conv(ctypes.Structure):
+        _fields_ = [("i", ctypes.c_int * 8), ("p", ctypes.c_void_p * 3)]
+
+    assert ctypes.sizeof(Conv) == 56
+
+
+def test_fold_canon_matches_rules(orc):
+    """bit = ((uint32)(P - lo) < wid) ^ inv reproduces every rule on every
+    reachable P (|P| <= 9 * Cin), thresholds at the extremes included."""
+    rng = np.random.default_rng(0)
+    c = 400
+    ty, t, lo, hi = synth.make_rules(1, c, 288, coverage=True)
+    ty = ty.copy(); t = t.copy(); lo = lo.copy(); hi = hi.copy()
+    ext = np.array([np.iinfo(np.int32).min, np.iinfo(np.int32).max, -(1 << 30) - 5, (1 << 30) + 5], np.int32)
+    t[:40] = rng.choice(ext, 40)
+    lo[40:80] = rng.choice(ext, 40)
+    hi[60:100] = rng.choice(ext, 40)
+    ty[100:110] = [-1, 6, 100, 0, 0, 1, 2, 3, 4, 5]
+    P = np.arange(-3456, 3457, dtype=np.int64)
+    clo, cwid, cinv = E.fold_canon(ty, t, lo, hi)
+    bit = (((P[None, :] - clo[:, None].astype(np.int64)) & 0xFFFFFFFF) < cwid[:, None]) ^ (cinv[:, None] > 0)
+    want = orc.fold_int(np.broadcast_to(P.astype(np.int32), (c, 1, P.size)).copy(), ty, t, lo, hi)[:, 0, :]
+    assert np.array_equal(np.where(bit, 1, -1), want)
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run(["python", os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0 and "one GPU" in (r.stderr + r.stdout)

@@ -1,0 +1,159 @@
+"""The whole v1 forward on the GPU (csrc/bnn_model.c:150-253).
+
+Every stage (22 binary activations, 17 accumulators P, 4 pooled P, the real
+first-conv output) is compared bit for bit with the checker and with the
+stage hashes the reference's own kernels produced (tests/golden); logits
+must be bit-identical (the head keeps the reference's summation order), so
+the 1e-5 / argmax bar is met with margin.
+"""
+import hashlib
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from bnns_to_c_amd import blob as B
+from bnns_to_c_amd import engine as E
+from bnns_to_c_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _engine(tmp_path, b, name="m.blob"):
+    p = tmp_path / name
+    p.write_bytes(B.to_bytes(b))
+    return E.Engine(str(p)), str(p)
+
+
+def _same(a, b):
+    if a.dtype == np.float32:
+        return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    return np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("seed,base,cov,N,H,W", [
+    (0, 16, False, 3, 32, 32),
+    (3, 16, True, 3, 32, 32),
+    (5, 8, False, 2, 17, 23),
+    (6, 16, False, 2, 30, 34),
+    (7, 8, True, 2, 16, 16),
+    (9, 32, False, 2, 32, 32),
+    (12, 16, False, 1, 47, 33),
+])
+def test_stages_vs_checker(tmp_path, orc, seed, base, cov, N, H, W):
+    b = synth.make_blob(seed=seed, base=base, coverage=cov)
+    eng, _ = _engine(tmp_path, b)
+    model = orc.parse(B.to_bytes(b))
+    x = synth.make_input(seed + 100, N, 120, H, W)
+    logits, st = eng.forward_debug(x)
+    assert len(st) == 49 - 4  # every stage except the four materialised up+concat inputs
+    for n in range(N):
+        want, ref_st = model.forward(x[n], stages=True)
+        for name, arr in st.items():
+            if name == "logits":
+                continue
+            assert _same(arr[n], ref_st[name]), (name, n)
+        assert _same(logits[n], want), n
+    eng.close()
+
+
+def test_golden_from_reference(tmp_path, golden):
+    """stage hashes and logits recorded from the reference's own C"""
+    meta, arrays = golden
+    for name, c in meta["cases"].items():
+        b = synth.make_blob(seed=c["blob_seed"], base=c["base"], coverage=c["coverage"])
+        eng, _ = _engine(tmp_path, b, name + ".blob")
+        x = synth.make_input(c["input_seed"], c["N"], 120, c["H"], c["W"])
+        assert hashlib.sha256(x.tobytes()).hexdigest() == c["input_sha256"]
+        logits, st = eng.forward_debug(x)
+        assert _same(logits, arrays[f"{name}__logits"]), name
+        assert _same(eng.forward_batch(x), arrays[f"{name}__logits"]), name
+        for n in range(c["N"]):
+            for k, v in st.items():
+                h = hashlib.sha256(np.ascontiguousarray(v[n]).tobytes()).hexdigest()
+                assert h == c["stages"][n][k], (name, n, k)
+        eng.close()
+
+
+def test_batch_1024(tmp_path, orc):
+    b = synth.make_blob(seed=0)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(1, 1024)
+    got = eng.forward_batch(x)
+    model = orc.parse(B.to_bytes(b))
+    idx = np.r_[0:32, 500:532, 992:1024]
+    want = model.forward_batch(np.ascontiguousarray(x[idx]))
+    assert _same(got[idx], want)
+    assert np.abs(got[idx] - want).max() <= 1e-5
+    assert np.array_equal(got[idx].argmax(1), want.argmax(1))
+    # patches are independent: a patch gives the same logits in any batch position
+    assert _same(eng.forward_batch(x[idx[::-1]].copy())[::-1], got[idx])
+    eng.close()
+
+
+def test_device_api_and_dropin(tmp_path):
+    import torch
+    b = synth.make_blob(seed=2)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(2, 64)
+    ref = eng.forward_batch(x)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty((64, 3, 32, 32), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    eng.forward_device(dx.data_ptr(), 64, 32, 32, dy.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    assert _same(dy.cpu().numpy(), ref)
+    # the model's own stream
+    dy.zero_()
+    eng.forward_device(dx.data_ptr(), 64, 32, 32, dy.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert _same(dy.cpu().numpy(), ref)
+    # batch-1 drop-in entry point
+    assert _same(eng.forward(x[5]), ref[5])
+    # repeated calls are deterministic
+    assert _same(eng.forward_batch(x), ref)
+    eng.close()
+
+
+def test_shape_errors(tmp_path):
+    eng, _ = _engine(tmp_path, synth.make_blob(seed=0, base=8))
+    with pytest.raises(E.BnnError, match="H, W >= 16"):
+        eng.forward_batch(np.zeros((1, 120, 8, 32), np.float32))
+    assert eng.forward_batch(np.zeros((0, 120, 32, 32), np.float32)).shape == (0, 3, 32, 32)
+    eng.close()
+
+
+def test_cli_matches_reference_cli(tmp_path, golden):
+    """bnn_infer with the reference's argument order and `rand` input
+    (csrc/main.c:22-76) writes the same bytes as the reference CLI."""
+    meta, arrays = golden
+    for name, c in meta["cli"].items():
+        b = synth.make_blob(seed=c["blob_seed"], base=c["base"], coverage=c["coverage"])
+        p = tmp_path / (name + ".blob")
+        p.write_bytes(B.to_bytes(b))
+        out = tmp_path / (name + ".bin")
+        r = subprocess.run([E.CLI_PATH, str(p), "rand", str(out), str(c["H"]), str(c["W"]), "3"],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        assert "# forward   :" in r.stderr and f"# H={c['H']} W={c['W']} bands=120 classes=3 reps=3" in r.stderr
+        o = np.fromfile(out, np.float32).reshape(-1, c["H"], c["W"])
+        assert _same(o, arrays[f"{name}__cli"]), name
+    # input file path + profile table
+    b = synth.make_blob(seed=0)
+    p = tmp_path / "m.blob"
+    p.write_bytes(B.to_bytes(b))
+    x = synth.make_input(4, 1)[0]
+    (tmp_path / "in.bin").write_bytes(x.tobytes())
+    env = dict(os.environ, BNN_PROFILE="1")
+    r = subprocess.run([E.CLI_PATH, str(p), str(tmp_path / "in.bin"), str(tmp_path / "o.bin")],
+                       capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    assert "enc1.conv1" in r.stderr and "roll-up by op type" in r.stderr
+    eng = E.Engine(str(p))
+    assert _same(np.fromfile(tmp_path / "o.bin", np.float32).reshape(3, 32, 32), eng.forward(x))
+    eng.close()
+    # errors exit(1) with the message, like the reference
+    r = subprocess.run([E.CLI_PATH, str(tmp_path / "missing.blob"), "rand", str(tmp_path / "o.bin")],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "cannot open" in r.stderr
