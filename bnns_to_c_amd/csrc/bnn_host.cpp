@@ -615,7 +615,6 @@ int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
-  if (!s) s = D->stream;
   if ((rc = ensure_ws(m, D, N, H, W))) return rc;
   if (!g_prof_on) return enqueue_forward(m, D, d_in, N, H, W, d_logits, s, dmp, nullptr, nullptr);
   std::vector<Op> ops;
@@ -963,7 +962,7 @@ int bnn_layer_P_device(const BnnConvLayer* L, const uint32_t* d_act, int N, int 
   a.P = d_P;
   int mt, cog;
   pick_shape(EPI_P, N, H, W, a.cout, &mt, &cog);
-  HIP_TRY(launch_bconv(a, EPI_P, mt, cog, false, stream ? (hipStream_t)stream : L->dev.stream));
+  HIP_TRY(launch_bconv(a, EPI_P, mt, cog, false, (hipStream_t)stream));
   return BNN_OK;
 }
 
@@ -977,7 +976,7 @@ int bnn_layer_fold_pool_device(const BnnConvLayer* L, const uint32_t* d_act, int
   a.out = d_skip; a.out2 = d_down;
   int mt, cog;
   pick_shape(EPI_POOL, N, H, W, a.cout, &mt, &cog);
-  HIP_TRY(launch_bconv(a, EPI_POOL, mt, cog, false, stream ? (hipStream_t)stream : L->dev.stream));
+  HIP_TRY(launch_bconv(a, EPI_POOL, mt, cog, false, (hipStream_t)stream));
   return BNN_OK;
 }
 

@@ -135,10 +135,10 @@ __global__ __launch_bounds__(kBlock) void k_real_conv(const RealArgs a, uint32_t
       const float rr = __fadd_rn(z, a.rsign[co]);
       word |= (rr > 0.0f && c < nco) ? (1u << c) : 0u;
     }
+    // whole-word store: CO = 16 is used only when cout <= 16 (one launch,
+    // co0 = 0), so bits above cout are written as 0 either way
     const int cwo = (a.cout + 31) >> 5;
-    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out) + ((size_t)p * cwo) * 4 + (a.co0 >> 3);
-    if (CO == 32) *reinterpret_cast<uint32_t*>(dst) = word;
-    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+    a.out[(size_t)p * cwo + (a.co0 >> 5)] = word;
   }
 }
 
@@ -184,12 +184,18 @@ __device__ __forceinline__ uint32_t inv_bits(const FoldDev& f, int co0, int cog)
   const uint32_t w = f.inv[co0 >> 5] >> (co0 & 31);
   return cog == 32 ? w : (w & ((1u << cog) - 1u));
 }
+// Store the COG bits of one channel group.  The last group also writes 0 to
+// the bytes above it in its word (at most 3), so every word is fully
+// written even when cout is not a multiple of 32.
 template <int COG>
-__device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, int co0, uint32_t bits) {
-  uint8_t* dst = reinterpret_cast<uint8_t*>(base) + pix * (size_t)cw * 4 + (co0 >> 3);
+__device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, int co0, uint32_t bits,
+                                           int zero_end) {
+  uint8_t* row = reinterpret_cast<uint8_t*>(base) + pix * (size_t)cw * 4;
+  uint8_t* dst = row + (co0 >> 3);
   if (COG == 32) *reinterpret_cast<uint32_t*>(dst) = bits;
   else if (COG == 16) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bits;
   else *dst = (uint8_t)bits;
+  for (int b = (co0 + COG) >> 3; b < zero_end; ++b) row[b] = 0;
 }
 
 template <int MT, int COG, int EPI, bool DUMP>
@@ -306,6 +312,8 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
   }
   if (EPI == EPI_P) return;
 
+  // bytes of the pixel's words the last channel group zero-fills
+  const int zero_end = blockIdx.y == gridDim.y - 1 ? a.cwo * 4 : 0;
   const uint32_t inv1 = inv_bits(a.f1, co0, COG);
   uint32_t bits[MT * MT];
 #pragma unroll
@@ -322,7 +330,8 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
 #pragma unroll
       for (int px = 0; px < MT; ++px)
         if (inimg[py * MT + px])
-          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, bits[py * MT + px]);
+          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, bits[py * MT + px],
+                          zero_end);
   }
   if (EPI == EPI_POOL) {
     // 2x2 floor-mode max on P (csrc/bnn_maxpool.c:28-48), then the down rule
@@ -337,13 +346,13 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
           a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
       }
       b ^= inv_bits(a.f2, co0, COG);
-      store_bits<COG>(a.out2, ((size_t)n * Hh + ty) * Wh + tx, a.cwo, co0, b);
+      store_bits<COG>(a.out2, ((size_t)n * Hh + ty) * Wh + tx, a.cwo, co0, b, zero_end);
     }
   }
   if (EPI == EPI_HEAD) {
     // widen +-1 to float and the 1x1 head: bias first, then channels in
     // order, one fused step each (csrc/bnn_head.c:21-34)
-    if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, bits[0]);
+    if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, bits[0], zero_end);
     const int pix = y0 * a.W + x0;
 #pragma unroll 1
     for (int o = 0; o < a.ncls; ++o) {

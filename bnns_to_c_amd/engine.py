@@ -7,6 +7,10 @@ names, argument order and batch-1 layouts (csrc/bnn_model.h:7-23), exactly as
 the reference's ctypes harnesses bind them (python/verify/bconv_harness.py:36-47,
 forward_driver.py:55-66).  Every call runs on the GPU.  There is no CPU
 fallback: a missing library or a missing GPU raises.
+
+With PyTorch in the same process, import torch before the first call here:
+torch bundles a HIP runtime with the same soname as /opt/rocm's, and the
+library must bind to the one already loaded rather than start a second.
 """
 from __future__ import annotations
 
@@ -157,7 +161,7 @@ class Engine:
     def forward_device(self, d_in: int, N: int, H: int, W: int, d_out: int,
                        stream: Optional[int] = None) -> None:
         _check(lib().bnn_forward_device(self.h, _vp(d_in), N, H, W, _vp(d_out),
-                                        _vp(stream) if stream else None))
+                                        _vp(stream or None)))
 
     def stream(self) -> int:
         return lib().bnn_stream(self.h)
@@ -237,19 +241,19 @@ class ConvLayer:
 
     def P_device(self, d_act: int, N: int, H: int, W: int, d_P: int, stream: Optional[int] = None):
         _check(lib().bnn_layer_P_device(self.h, _vp(d_act), N, H, W, _vp(d_P),
-                                        _vp(stream) if stream else None))
+                                        _vp(stream or None)))
 
     def fold_pool_device(self, d_act: int, N: int, H: int, W: int, d_skip: Optional[int],
                          d_down: int, stream: Optional[int] = None):
         _check(lib().bnn_layer_fold_pool_device(self.h, _vp(d_act), N, H, W,
                                                 _vp(d_skip) if d_skip else None, _vp(d_down),
-                                                _vp(stream) if stream else None))
+                                                _vp(stream or None)))
 
 
 def pack_act_device(d_a: int, d_out: int, N: int, Cc: int, H: int, W: int,
                     stream: Optional[int] = None) -> None:
     _check(lib().bnn_pack_act_device(_vp(d_a), _vp(d_out), N, Cc, H, W,
-                                     _vp(stream) if stream else None))
+                                     _vp(stream or None)))
 
 
 def fold_canon(ty, t, lo, hi):

@@ -95,11 +95,12 @@ int bnn_load_status(const char *path, Model **out);
 /* N independent patches: input [N, n_bands, H, W] -> logits [N, n_classes, H, W]
  * (host pointers; the v1 forward applied to each patch, csrc/bnn_model.c:150-253) */
 int bnn_forward_batch(const Model *m, const float *input, int N, int H, int W, float *logits);
-/* same on device pointers, enqueued on `stream` (hipStream_t; NULL = the
- * model's own stream); returns once enqueued */
+/* same on device pointers, enqueued on `stream` (a hipStream_t; NULL is the
+ * HIP default stream, as everywhere in HIP); returns once enqueued.  Calls
+ * that share a model must be ordered by the caller: they share its workspace. */
 int bnn_forward_device(const Model *m, const float *d_input, int N, int H, int W,
                        float *d_logits, void *stream);
-void *bnn_stream(const Model *m);      /* the model's own hipStream_t */
+void *bnn_stream(const Model *m);      /* the model's own hipStream_t (used by the host-pointer calls) */
 
 /* Debug forward: host pointers, then every stage of the chain is handed to
  * `cb` as a host array [N][c][h][w] (dtype 0 int8 +-1, 1 int32 P, 2 float),
@@ -117,7 +118,8 @@ int bnn_prof_count(void);
 int bnn_prof_get(int i, char *label, int label_len, char *optype, int optype_len,
                  double *ms, double *work);
 
-/* Isolated kernels on device pointers (benchmark configs 1 and 2).
+/* Isolated kernels on device pointers (benchmark configs 1 and 2); `stream`
+ * is a hipStream_t, NULL = the HIP default stream.
  * act: [N][H][W][ceil(Cin/32)] uint32 channel-packed sign bits;
  * wt:  kidx-packed weights as in the blob, [Cout][ceil(Cin*9/64)] uint64 (host). */
 typedef struct BnnConvLayer BnnConvLayer;

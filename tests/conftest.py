@@ -5,6 +5,14 @@ import sys
 import numpy as np
 import pytest
 
+# torch ships its own HIP runtime under the same soname as /opt/rocm's; when
+# both are used in one process, torch must load first so libbnn_hip.so binds
+# to the runtime already present instead of initialising a second one.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)

@@ -104,10 +104,13 @@ def test_device_api_and_dropin(tmp_path):
     eng.forward_device(dx.data_ptr(), 64, 32, 32, dy.data_ptr(), s.cuda_stream)
     s.synchronize()
     assert _same(dy.cpu().numpy(), ref)
-    # the model's own stream
-    dy.zero_()
-    eng.forward_device(dx.data_ptr(), 64, 32, 32, dy.data_ptr(), None)
-    torch.cuda.synchronize()
+    # the model's own stream, then the default stream (None)
+    for st in (eng.stream(), None):
+        dy.zero_()
+        torch.cuda.synchronize()
+        eng.forward_device(dx.data_ptr(), 64, 32, 32, dy.data_ptr(), st)
+        torch.cuda.synchronize()
+        assert _same(dy.cpu().numpy(), ref)
     assert _same(dy.cpu().numpy(), ref)
     # batch-1 drop-in entry point
     assert _same(eng.forward(x[5]), ref[5])

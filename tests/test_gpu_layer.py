@@ -153,3 +153,30 @@ def test_cfg2_full_batch(torch, orc):
     assert np.array_equal(E.unpack_bits_nhwc(down.cpu().numpy().view(np.uint32), C), _host_fold(pooled, *f2))
     for n in (0, 511, 1023):
         assert np.array_equal(Ph[n], orc.bconv(a[n], bits, C)), n
+
+
+@pytest.mark.parametrize("C,H,W", [(8, 6, 6), (24, 5, 8), (40, 4, 4), (16, 32, 32)])
+def test_partial_words_fully_written(torch, orc, C, H, W):
+    """Outputs whose channel count is not a multiple of 32 still get whole
+    words: the bits above C come back 0 even over a buffer full of ones."""
+    N = 4
+    a = synth.make_bits(40, N, H, W, C)
+    w = synth.make_signs(41, C, C)
+    bits = B.pack_kidx(w)
+    f1 = synth.make_rules(42, C, C * 9, coverage=True)
+    f2 = synth.make_rules(43, C, C * 9, coverage=True)
+    L = E.ConvLayer(bits, C, C, f1, f2)
+    act = _pack_on_device(torch, a)
+    cw = (C + 31) // 32
+    skip = torch.full((N, H, W, cw), -1, dtype=torch.int32, device="cuda")
+    down = torch.full((N, H // 2, W // 2, cw), -1, dtype=torch.int32, device="cuda")
+    L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(),
+                       torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for t in (skip, down):
+        words = t.cpu().numpy().view(np.uint32)
+        if C % 32:
+            assert np.all(words[..., -1] >> np.uint32(C % 32) == 0)
+    sk = E.unpack_bits_nhwc(skip.cpu().numpy().view(np.uint32), C)
+    for n in range(N):
+        assert np.array_equal(sk[n], orc.fold_int(orc.bconv(a[n], bits, C), *f1))
