@@ -305,7 +305,7 @@ struct BnnDevice {
   int device = 0;
   hipStream_t stream = nullptr;
   std::vector<void*> allocs;
-  int rcin = 0, rcout = 0, rCO = 16, rchunks = 1;
+  int rcin = 0, rcout = 0;
   float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   float *hw = nullptr, *hb = nullptr;
@@ -359,19 +359,13 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   return BNN_OK;
 }
 
-// real conv weights [chunk][ky][kx][cin][CO] as +-1.0f, folds padded to chunk*CO
+// real conv weights in groups of kRealGroup output channels, folds padded to 32
 int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
   D->rcin = c.Cin;
   D->rcout = c.Cout;
-  D->rCO = c.Cout > 16 ? 32 : 16;
-  D->rchunks = (c.Cout + D->rCO - 1) / D->rCO;
-  const int CO = D->rCO, tot = D->rchunks * CO;
-  std::vector<float> w((size_t)D->rchunks * 9 * c.Cin * CO, 0.0f);
-  for (int co = 0; co < c.Cout; ++co)
-    for (int ci = 0; ci < c.Cin; ++ci)
-      for (int t = 0; t < 9; ++t)
-        w[(((size_t)(co / CO) * 9 + t) * c.Cin + ci) * CO + co % CO] =
-            (float)c.wsign[((size_t)co * c.Cin + ci) * 9 + t];
+  const int tot = (c.Cout + 31) / 32 * 32;
+  std::vector<float> w(real_conv_weights_len(c.Cout, c.Cin));
+  real_conv_weights(c.wsign, c.Cout, c.Cin, w.data());
   auto padv = [&](const float* src) {
     std::vector<float> v(tot, 0.0f);
     std::copy(src, src + c.Cout, v.begin());
@@ -435,8 +429,7 @@ void level_dims(int H, int W, int* hs, int* wsz) {
   for (int l = 1; l <= 4; ++l) { hs[l] = hs[l - 1] / 2; wsz[l] = wsz[l - 1] / 2; }
 }
 
-int ensure_ws(const Model* m, BnnDevice* D, int N, int H, int W) {
-  Workspace& w = D->ws;
+int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
   if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
   // a forward may still be in flight on a caller's stream
   if (w.base) { HIP_TRY(hipDeviceSynchronize()); hipFree(w.base); w.base = nullptr; }
@@ -483,6 +476,7 @@ void pick_shape(int epi, int N, int H, int W, int cout, int* mt, int* cog) {
   if (epi == EPI_HEAD) { *cog = cout <= 16 ? 16 : 32; return; }
   const long tiles = (long)N * ((H + *mt - 1) / *mt) * ((W + *mt - 1) / *mt);
   int c = *mt == 2 ? 16 : 32;
+  while (c > 8 && c / 2 >= cout) c /= 2;  // no group wider than the layer
   auto waves = [&](int g) { return ((tiles + 63) / 64) * (long)((cout + g - 1) / g); };
   while (c > 8 && waves(c) < 4096) c /= 2;
   *cog = c;
@@ -501,11 +495,12 @@ struct Op {
   double oe, taps;
 };
 
-// Enqueue the whole forward for N patches.  Each stage is one kernel; with
-// profiling on, an event pair brackets every kernel.
-int enqueue_forward(const Model* m, BnnDevice* D, const float* d_in, int N, int H, int W, float* d_logits,
-                    hipStream_t s, Dumps* dmp, std::vector<Op>* ops, std::vector<hipEvent_t>* evs) {
-  Workspace& w = D->ws;
+// Enqueue the whole forward for N patches on stream s with workspace w.
+// Each stage is one kernel; with profiling on, an event pair brackets every
+// kernel.
+int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_in, int N, int H, int W,
+                    float* d_logits, hipStream_t s, Dumps* dmp, std::vector<Op>* ops,
+                    std::vector<hipEvent_t>* evs) {
   int hs[5], wsz[5];
   level_dims(H, W, hs, wsz);
   auto mark = [&](const char* label, const char* optype, double oe, double taps) -> int {
@@ -522,20 +517,18 @@ int enqueue_forward(const Model* m, BnnDevice* D, const float* d_in, int N, int 
   int rc;
   if ((rc = mark(nullptr, nullptr, 0, 0))) return rc;
 
-  // enc1.conv1: real conv + real fold -> a1 bits
-  for (int ch = 0; ch < D->rchunks; ++ch) {
+  {
+    // enc1.conv1: real conv + real fold -> a1 bits
     RealArgs ra{};
     ra.x = d_in;
-    ra.w = D->rw + (size_t)ch * 9 * D->rcin * D->rCO;
+    ra.w = D->rw;
     ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
     ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
-    ra.CO = D->rCO;
-    ra.co0 = ch * D->rCO;
     ra.out = w.a1;
     ra.f32 = dump ? dmp->conv1 : nullptr;
     HIP_TRY(launch_real(ra, s));
+    if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
   }
-  if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
 
   auto bconv = [&](const DevBconv& L, int epi, const uint32_t* in0, const uint32_t* in1, int lvl, int lvl1,
                    uint32_t* out, uint32_t* out2, float* logits, const char* label) -> int {
@@ -603,8 +596,8 @@ int check_shape(const Model* m, int N, int H, int W) {
   if (N < 0) return set_err(BNN_EARG, "negative batch");
   if (H < 16 || W < 16)
     return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
-  if ((size_t)N * m->n_bands * H * W * 4 >= 0xffffffffull)
-    return set_err(BNN_EARG, "batch too large for one launch (%zu input bytes >= 4 GiB)",
+  if ((size_t)N * m->n_bands * H * W * 4 >= 0x80000000ull)
+    return set_err(BNN_EARG, "batch too large for one launch (%zu input bytes >= 2 GiB)",
                    (size_t)N * m->n_bands * H * W * 4);
   return BNN_OK;
 }
@@ -615,11 +608,11 @@ int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
-  if ((rc = ensure_ws(m, D, N, H, W))) return rc;
-  if (!g_prof_on) return enqueue_forward(m, D, d_in, N, H, W, d_logits, s, dmp, nullptr, nullptr);
+  if ((rc = ensure_ws(m, D, D->ws, N, H, W))) return rc;
+  if (!g_prof_on) return enqueue_forward(m, D, D->ws, d_in, N, H, W, d_logits, s, dmp, nullptr, nullptr);
   std::vector<Op> ops;
   std::vector<hipEvent_t> evs;
-  rc = enqueue_forward(m, D, d_in, N, H, W, d_logits, s, dmp, &ops, &evs);
+  rc = enqueue_forward(m, D, D->ws, d_in, N, H, W, d_logits, s, dmp, &ops, &evs);
   if (!rc && !evs.empty()) {
     HIP_TRY(hipEventSynchronize(evs.back()));
     for (size_t i = 0; i + 1 < evs.size() && i < ops.size(); ++i) {

@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <memory>
 #include <vector>
 
@@ -135,25 +136,18 @@ void conv_realin_naive(const float* x, const int8_t* wsign, const float* alpha, 
   Buf dout((size_t)Cout * Ho * Wo * 4);
   const bool fast = kh == 3 && kw == 3 && pad == 1 && stride == 1;
   if (fast) {
-    // [chunk][ky][kx][ci][CO] weights and alpha padded to whole chunks
-    const int CO = Cout > 16 ? 32 : 16, chunks = (Cout + CO - 1) / CO;
-    std::vector<float> w((size_t)chunks * 9 * Cin * CO, 0.0f), al((size_t)chunks * CO, 0.0f);
-    for (int co = 0; co < Cout; ++co) {
-      al[co] = alpha[co];
-      for (int ci = 0; ci < Cin; ++ci)
-        for (int t = 0; t < 9; ++t)
-          w[(((size_t)(co / CO) * 9 + t) * Cin + ci) * CO + co % CO] = (float)wsign[((size_t)co * Cin + ci) * 9 + t];
-    }
+    const int tot = (Cout + 31) / 32 * 32;
+    std::vector<float> w(real_conv_weights_len(Cout, Cin)), al(tot, 0.0f);
+    real_conv_weights(wsign, Cout, Cin, w.data());
+    std::copy(alpha, alpha + Cout, al.begin());
     std::unique_ptr<Buf> dw(up(w.data(), w.size() * 4)), dal(up(al.data(), al.size() * 4));
-    for (int ch = 0; ch < chunks; ++ch) {
-      RealArgs r{};
-      r.x = dx->as<float>();
-      r.w = dw->as<float>() + (size_t)ch * 9 * Cin * CO;
-      r.alpha = dal->as<float>();
-      r.N = 1; r.H = H; r.W = W; r.cin = Cin; r.cout = Cout; r.CO = CO; r.co0 = ch * CO;
-      r.f32 = dout.as<float>();
-      check(launch_real(r, 0), "conv_realin");
-    }
+    RealArgs r{};
+    r.x = dx->as<float>();
+    r.w = dw->as<float>();
+    r.alpha = dal->as<float>();
+    r.N = 1; r.H = H; r.W = W; r.cin = Cin; r.cout = Cout;
+    r.f32 = dout.as<float>();
+    check(launch_real(r, 0), "conv_realin");
   } else {
     std::vector<float> w((size_t)Cout * kh * kw * Cin);
     for (int co = 0; co < Cout; ++co)

@@ -6,7 +6,8 @@
 //                                               CW = ceil(C/32); unused high bits are 0
 //   binary weights  uint32 [CW][Cout][9]        same channel->bit map as the activations
 //                                               they meet, per 3x3 tap t = ky*3+kx
-//   real weights    float  [3 ky][3 kx][Cin][CO] +-1.0, CO = padded output width
+//   real weights    float  [ceil(Cout/G)][Cin][9][G] +-1.0 (groups of G =
+//                                               kRealGroup output channels, zero-padded), t = ky*3+kx
 //   logits          float  [N][ncls][H][W]
 #pragma once
 #include <hip/hip_runtime.h>
@@ -53,18 +54,40 @@ struct BconvArgs {
 
 struct RealArgs {
   const float* x;
-  const float* w;       // [9][cin][CO]
-  const float* alpha;
+  const float* w;       // [ceil(cout/G)][cin][9][G]
+  const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;
   const float* slope;
   const float* rsign;
   int N, H, W, cin, cout;
-  int CO;               // output channels per launch in the weight layout (16 or 32)
-  int co0;              // first output channel handled by this launch
-  uint32_t* out;        // bits [N][H][W][1]; may be null
+  uint32_t* out;        // bits [N][H][W][ceil(cout/32)]; may be null
   float* f32;           // conv output [N][cout][H][W]; may be null
 };
+
+// Real-conv work split: output channels per lane group and output rows per
+// lane (set here so the host weight layout and the kernel agree).
+#ifndef BNN_RCO
+#define BNN_RCO 4
+#endif
+#ifndef BNN_PXR
+#define BNN_PXR 2
+#endif
+constexpr int kRealGroup = BNN_RCO;
+
+// host-side: int8 sign weights [cout][cin][3][3] -> [ceil(cout/G)][cin][9][G]
+// floats, G = kRealGroup, zero-padded; sized real_conv_weights_len()
+inline size_t real_conv_weights_len(int cout, int cin) {
+  return (size_t)(cout + kRealGroup - 1) / kRealGroup * kRealGroup * cin * 9;
+}
+inline void real_conv_weights(const int8_t* wsign, int cout, int cin, float* out) {
+  constexpr int G = kRealGroup;
+  for (size_t i = 0; i < real_conv_weights_len(cout, cin); ++i) out[i] = 0.0f;
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci)
+      for (int t = 0; t < 9; ++t)
+        out[(((size_t)(co / G) * cin + ci) * 9 + t) * G + co % G] = (float)wsign[((size_t)co * cin + ci) * 9 + t];
+}
 
 // Launchers return hipSuccess or the first launch error.  mt = micro-tile
 // side (1 or 2), cog = output channels per work-item (8/16/32).

@@ -17,9 +17,8 @@
 // each output, taps in row-major order, s = x*w summed over ci from 0 in
 // sequence, acc += s, out = alpha * acc.  Every product is x * (+-1), which
 // is exact, so one fused multiply-add per term rounds exactly like the
-// reference's multiply-then-add.  Out-of-image taps are computed on a clamped
-// (in-image) address and discarded by a select before acc += s; skipping a
-// tap and adding the +0 it would sum to are the same, since s and acc never
+// reference's multiply-then-add.  Out-of-image taps read zeros and sum to
+// +0; skipping a tap and adding that +0 are the same, since s and acc never
 // hold -0.
 #include "bnn_kernels.h"
 
@@ -43,102 +42,171 @@ __device__ __forceinline__ uint32_t ld_u32(__amdgpu_buffer_rsrc_t rs, uint32_t v
 // ------------------------------------------------------------------------
 // real-input conv + real fold
 // ------------------------------------------------------------------------
-template <int CO>
-__device__ __forceinline__ void fma_terms(float (&s)[3][CO], const float (&xv)[3],
-                                          const float* __restrict__ wr, int cin, int ci) {
-#pragma unroll
-  for (int kx = 0; kx < 3; ++kx) {
-    const float* wk = wr + ((size_t)kx * cin + ci) * CO;
-#pragma unroll
-    for (int c = 0; c < CO; ++c) s[kx][c] = __fmaf_rn(xv[kx], wk[c], s[kx][c]);
-  }
-}
+// Work-group: an RT x RW output tile for RG groups of RCO output channels.
+// Each lane of a group owns PXR vertically adjacent pixels of one column;
+// the RT x RW tile takes RT/PXR x RW lanes per group (whole waves).  The
+// (RT+2) x (RW+2) input tile, CI channels at a time, is staged in LDS,
+// double-buffered, with zeros outside the image (buffer loads out of range
+// return 0), and shared by all groups, so each input byte is fetched once per
+// tile.  Each lane keeps the 9 per-tap in-order sums of its RCO channels for
+// each of its pixels over all ci, then adds them into acc in row-major tap
+// order; an out-of-image tap sums zeros to +0, which leaves acc unchanged.
+// Every weight fetched through the scalar path feeds PXR FMAs.
+#ifndef BNN_RCI
+#define BNN_RCI 8
+#endif
+constexpr int RT = 8, RW = 32, RCO = BNN_RCO, PXR = BNN_PXR, CI = BNN_RCI;
+constexpr int LR = RT + 2, LC = RW + 2, LTILE = CI * LR * LC;
+constexpr int RLANES = RT / PXR * RW;  // lanes per channel group
 
-template <int CO>
-__global__ __launch_bounds__(kBlock) void k_real_conv(const RealArgs a, uint32_t xbytes) {
+template <int RG>
+__global__ __launch_bounds__(RLANES * RG) void k_real_conv(const RealArgs a, uint32_t xbytes, int tilesH,
+                                                           int tilesW) {
+  static_assert(RLANES % 64 == 0, "channel groups must be whole waves");
+  static_assert(32 % RCO == 0, "a channel group must not straddle a 32-bit word");
+  constexpr int NT = RLANES * RG;
+  constexpr int KL = (LTILE + NT - 1) / NT;
+  constexpr int OW = (RG * RCO + 31) / 32;  // output words per pixel this block writes
+  __shared__ float tile[2][LTILE];
+  __shared__ uint32_t obits[RT * RW * OW];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < RT * RW * OW; i += NT) obits[i] = 0;
+  // a group is a whole number of waves: the group index is wave-uniform
+  const int grp = __builtin_amdgcn_readfirstlane(tid / RLANES);
+  const int lt = tid - grp * RLANES;
+  const int r0 = (lt / RW) * PXR, c = lt % RW;
+  int bid = blockIdx.x;
+  const int tx = bid % tilesW;
+  bid /= tilesW;
+  const int ty = bid % tilesH;
+  const int n = bid / tilesH;
+  const int y0 = ty * RT, x0 = tx * RW;
+  const int cog = blockIdx.y * RG + grp;  // global channel group
   const int HW = a.H * a.W;
-  const long total = (long)a.N * HW;
-  long p = (long)blockIdx.x * kBlock + threadIdx.x;
-  const bool active = p < total;
-  if (!active) p = total - 1;
-  const int n = (int)(p / HW);
-  const int r = (int)(p - (long)n * HW);
-  const int y = r / a.W, x = r - y * a.W;
-  const uint32_t plane0 = (uint32_t)n * (uint32_t)a.cin * (uint32_t)HW;
-  const uint32_t pstride = (uint32_t)HW * 4u;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
 
-  float acc[CO];
+  // this thread's share of every chunk load: byte offset within the chunk,
+  // or an offset past the buffer (reads 0) for positions outside the image,
+  // and where it goes in the [row][ci][col] tile (all CI channels and 3
+  // columns of a tile row lie within one ds_read2 offset range)
+  uint32_t goff[KL];
+  int lidx[KL];
 #pragma unroll
-  for (int c = 0; c < CO; ++c) acc[c] = 0.0f;
+  for (int k = 0; k < KL; ++k) {
+    const int e = tid + k * NT;
+    const int cil = e / (LR * LC), rem = e - cil * (LR * LC);
+    const int row = rem / LC, col = rem - row * LC;
+    lidx[k] = e < LTILE ? (row * CI + cil) * LC + col : 0;
+    const int gy = y0 - 1 + row, gx = x0 - 1 + col;
+    const bool ok = e < LTILE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+    goff[k] = ok ? (uint32_t)(((size_t)n * a.cin + cil) * HW + (size_t)gy * a.W + gx) * 4u : 0x80000000u;
+  }
+  const uint32_t chunk_bytes = (uint32_t)CI * (uint32_t)HW * 4u;
+  const int nchunk = (a.cin + CI - 1) / CI;
 
+  float st[PXR][9][RCO];
+#pragma unroll
+  for (int p = 0; p < PXR; ++p)
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+      for (int g = 0; g < RCO; ++g) st[p][t][g] = 0.0f;
+
+  float pre[KL];
+#pragma unroll
+  for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], 0);
+#pragma unroll
+  for (int k = 0; k < KL; ++k)
+    if (tid + k * NT < LTILE) tile[0][lidx[k]] = pre[k];
+  __syncthreads();
+
+  const float* wg = a.w + (size_t)cog * a.cin * 9 * RCO;  // [cin][9][RCO] of this group
+  const int lbase = r0 * CI * LC + c;
 #pragma unroll 1
-  for (int ky = 0; ky < 3; ++ky) {
-    const int iy = y + ky - 1;
-    const bool rowok = iy >= 0 && iy < a.H;
-    uint32_t off[3];
-    bool ok[3];
+  for (int ch = 0; ch < nchunk; ++ch) {
+    const int buf = ch & 1;
+    const bool more = ch + 1 < nchunk;
+    if (more) {
 #pragma unroll
-    for (int kx = 0; kx < 3; ++kx) {
-      const int ix = x + kx - 1;
-      ok[kx] = rowok && ix >= 0 && ix < a.W;
-      off[kx] = (plane0 + (ok[kx] ? (uint32_t)(iy * a.W + ix) : (uint32_t)r)) * 4u;
+      for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], (uint32_t)(ch + 1) * chunk_bytes);
     }
-    float s[3][CO];
+    const int ci0 = ch * CI;
+    const int nci = a.cin - ci0 < CI ? a.cin - ci0 : CI;
+    const float* tb = tile[buf] + lbase;
 #pragma unroll
-    for (int kx = 0; kx < 3; ++kx)
+    for (int cl = 0; cl < CI; ++cl) {
+      if (cl < nci) {
+        float xv[PXR + 2][3];
 #pragma unroll
-      for (int c = 0; c < CO; ++c) s[kx][c] = 0.0f;
-    const float* wr = a.w + (size_t)ky * 3 * a.cin * CO;
-    // two register sets: the loads for term ci+1 are in flight while ci is summed
-    float xa[3], xb[3];
+        for (int i = 0; i < PXR + 2; ++i)
 #pragma unroll
-    for (int kx = 0; kx < 3; ++kx) xa[kx] = ld_f32(rs, off[kx], 0);
-    int ci = 0;
-#pragma unroll 1
-    for (; ci + 2 <= a.cin; ci += 2) {
+          for (int kx = 0; kx < 3; ++kx) xv[i][kx] = tb[(i * CI + cl) * LC + kx];
+        const float* wp = wg + (size_t)(ci0 + cl) * 9 * RCO;
 #pragma unroll
-      for (int kx = 0; kx < 3; ++kx) xb[kx] = ld_f32(rs, off[kx], (uint32_t)(ci + 1) * pstride);
-      fma_terms<CO>(s, xa, wr, a.cin, ci);
-      const int cn = ci + 2 < a.cin ? ci + 2 : ci + 1;
+        for (int t = 0; t < 9; ++t)
 #pragma unroll
-      for (int kx = 0; kx < 3; ++kx) xa[kx] = ld_f32(rs, off[kx], (uint32_t)cn * pstride);
-      fma_terms<CO>(s, xb, wr, a.cin, ci + 1);
-    }
-    if (ci < a.cin) fma_terms<CO>(s, xa, wr, a.cin, ci);
+          for (int g = 0; g < RCO; ++g) {
+            const float w = wp[t * RCO + g];
 #pragma unroll
-    for (int kx = 0; kx < 3; ++kx)
-#pragma unroll
-      for (int c = 0; c < CO; ++c) {
-        const float t = __fadd_rn(acc[c], s[kx][c]);
-        acc[c] = ok[kx] ? t : acc[c];
+            for (int p = 0; p < PXR; ++p) st[p][t][g] = __fmaf_rn(xv[p + t / 3][t % 3], w, st[p][t][g]);
+          }
       }
-  }
-  if (!active) return;
-  const int nco = a.cout - a.co0 < CO ? a.cout - a.co0 : CO;
-  if (a.f32) {
-#pragma unroll
-    for (int c = 0; c < CO; ++c)
-      if (c < nco)
-        a.f32[((size_t)n * a.cout + a.co0 + c) * HW + r] = __fmul_rn(a.alpha[a.co0 + c], acc[c]);
-  }
-  if (a.out) {
-    // real fold (csrc/bnn_fold.c:62-77): z = fma(A, x, B); z<0 -> slope*z;
-    // r = z + rsign; bit = r > 0.  The reference build fuses A*x+B only.
-    uint32_t word = 0;
-#pragma unroll
-    for (int c = 0; c < CO; ++c) {
-      const int co = a.co0 + c;
-      const float o = __fmul_rn(a.alpha[co], acc[c]);
-      float z = __fmaf_rn(a.A[co], o, a.B[co]);
-      if (z < 0.0f) z = __fmul_rn(a.slope[co], z);
-      const float rr = __fadd_rn(z, a.rsign[co]);
-      word |= (rr > 0.0f && c < nco) ? (1u << c) : 0u;
     }
-    // whole-word store: CO = 16 is used only when cout <= 16 (one launch,
-    // co0 = 0), so bits above cout are written as 0 either way
-    const int cwo = (a.cout + 31) >> 5;
-    a.out[(size_t)p * cwo + (a.co0 >> 5)] = word;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < KL; ++k)
+        if (tid + k * NT < LTILE) tile[buf ^ 1][lidx[k]] = pre[k];
+    }
+    __syncthreads();
+  }
+
+  const int co0 = cog * RCO;
+  const int nco = a.cout - co0 < RCO ? a.cout - co0 : RCO;
+  const int cwo = (a.cout + 31) >> 5;
+  const int cb0 = blockIdx.y * RG * RCO;  // first channel of this block (a multiple of 32 when gridDim.y > 1)
+#pragma unroll
+  for (int p = 0; p < PXR; ++p) {
+    float acc[RCO];
+#pragma unroll
+    for (int g = 0; g < RCO; ++g) acc[g] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+      for (int g = 0; g < RCO; ++g) acc[g] = __fadd_rn(acc[g], st[p][t][g]);
+    const int y = y0 + r0 + p, x = x0 + c;
+    if (y >= a.H || x >= a.W || co0 >= a.cout) continue;
+    if (a.f32) {
+#pragma unroll
+      for (int g = 0; g < RCO; ++g)
+        if (g < nco)
+          a.f32[((size_t)n * a.cout + co0 + g) * HW + (size_t)y * a.W + x] = __fmul_rn(a.alpha[co0 + g], acc[g]);
+    }
+    if (a.out) {
+      // real fold (csrc/bnn_fold.c:62-77): z = fma(A, x, B); z<0 -> slope*z;
+      // r = z + rsign; bit = r > 0.  The reference build fuses A*x+B only.
+      uint32_t bits = 0;
+#pragma unroll
+      for (int g = 0; g < RCO; ++g) {
+        const int co = co0 + g;
+        const float o = __fmul_rn(a.alpha[co], acc[g]);
+        float z = __fmaf_rn(a.A[co], o, a.B[co]);
+        if (z < 0.0f) z = __fmul_rn(a.slope[co], z);
+        const float rr = __fadd_rn(z, a.rsign[co]);
+        bits |= (rr > 0.0f && g < nco) ? (1u << g) : 0u;
+      }
+      const int cl = co0 - cb0;  // RCO divides 32: a group never straddles a word
+      atomicOr(&obits[((r0 + p) * RW + c) * OW + (cl >> 5)], bits << (cl & 31));
+    }
+  }
+  if (!a.out) return;
+  // whole words of the block's channels (bits above cout stay 0)
+  __syncthreads();
+  for (int i = tid; i < RT * RW * OW; i += NT) {
+    const int pl = i / OW, wd = i - pl * OW;
+    const int y = y0 + pl / RW, x = x0 + pl % RW;
+    const int word = (cb0 >> 5) + wd;
+    if (y < a.H && x < a.W && word < cwo)
+      a.out[((size_t)n * HW + (size_t)y * a.W + x) * cwo + word] = obits[i];
   }
 }
 
@@ -574,15 +642,23 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
 }
 
 hipError_t launch_real(const RealArgs& a, hipStream_t s) {
-  const long total = (long)a.N * a.H * a.W;
-  if (total <= 0) return hipSuccess;
+  if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   const size_t xbytes = (size_t)a.N * a.cin * a.H * a.W * 4;
-  if (xbytes >= 0xffffffffull) return hipErrorInvalidValue;
-  if (a.CO != 16 && a.CO != 32) return hipErrorInvalidValue;
-  if (a.CO == 32)
-    hipLaunchKernelGGL(k_real_conv<32>, dim3(blocks_for(total)), dim3(kBlock), 0, s, a, (uint32_t)xbytes);
-  else
-    hipLaunchKernelGGL(k_real_conv<16>, dim3(blocks_for(total)), dim3(kBlock), 0, s, a, (uint32_t)xbytes);
+  if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
+  const int tilesH = (a.H + RT - 1) / RT, tilesW = (a.W + RW - 1) / RW;
+  const int groups = (a.cout + RCO - 1) / RCO;
+  constexpr int maxg = 1024 / RLANES;
+  const int rg = groups >= maxg ? maxg : groups;
+  // blocks split along channels must each cover whole 32-bit output words
+  if (groups > rg && (rg * RCO) % 32 != 0) return hipErrorInvalidValue;
+  dim3 grid((unsigned)((long)a.N * tilesH * tilesW), (unsigned)((groups + rg - 1) / rg));
+  switch (rg) {
+#define BNN_RG(k) \
+  case k: if constexpr (k <= maxg) hipLaunchKernelGGL(k_real_conv<k>, grid, dim3(RLANES * k), 0, s, a, (uint32_t)xbytes, tilesH, tilesW); break;
+    BNN_RG(1) BNN_RG(2) BNN_RG(3) BNN_RG(4) BNN_RG(5) BNN_RG(6) BNN_RG(7) BNN_RG(8)
+#undef BNN_RG
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

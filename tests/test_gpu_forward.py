@@ -160,3 +160,22 @@ def test_cli_matches_reference_cli(tmp_path, golden):
     r = subprocess.run([E.CLI_PATH, str(tmp_path / "missing.blob"), "rand", str(tmp_path / "o.bin")],
                        capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "cannot open" in r.stderr
+
+
+@pytest.mark.parametrize("N", [256, 300, 1031])
+def test_batch_size_independent(tmp_path, N):
+    """Any batch size, including ones that fill the last block partially,
+    gives the same bits for every patch as batches of 64."""
+    import torch
+    b = synth.make_blob(seed=11)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(12, N)
+    small = np.concatenate([eng.forward_batch(x[i:i + 64]) for i in range(0, N, 64)])
+    big = eng.forward_batch(x)
+    assert _same(big, small)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.full((N, 3, 32, 32), float("nan"), device="cuda")
+    eng.forward_device(dx.data_ptr(), N, 32, 32, dy.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert _same(dy.cpu().numpy(), small)
+    eng.close()
