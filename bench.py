@@ -48,6 +48,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the real first conv from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated there against a
+    device copy of known size), or None if the summary is absent."""
+    p = os.path.join(ROOT, "profiles", "unet_b1024_hbm_traffic.md")
+    try:
+        txt = open(p).read()
+    except OSError:
+        return None
+    m = re.search(r"`k_real_conv`[^\n]*?moves ([\d.]+) MB in and ([\d.]+) MB out", txt)
+    return round((float(m.group(1)) + float(m.group(2))) * 1e6) if m else None
+
+
 def cpu_baseline(blob_path: str, budget_s: float) -> dict:
     cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     from oracle.oracle import REF_CLI
@@ -224,7 +237,8 @@ def main() -> int:
                    "batch": N, "H": H, "W": W, "n_bands": 120, "n_classes": 3, "base_channels": 16},
         "roofline": {"bound": "valu", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32 FMA)",
                      "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, calibrated)",
                      "algorithmic": f"{real_flops:.4g} FLOP/launch = 2 x 17,694,720 MAC x {N} patches"},
         "bconv": {"kernels": 17, "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
                   "frac": round(bin_rate / valu_binop_peak(), 4), "ms": round(bin_ms, 5),
