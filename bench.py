@@ -7,9 +7,10 @@ base 16, x ~ N(0,1)) with the input already resident in HBM; K steps are
 timed between device synchronisations.  Prints ONE JSON line on stdout:
 
   value         patches/s over the K timed steps
-  roofline      the dominant kernel (the order-exact real first conv): FP32
-                FMA work per launch / its mean hipEvent-measured duration
-                against the published FP32 vector peak
+  roofline      the dominant kernel (the order-exact real first conv, on the
+                matrix cores): FP32 FMA work per launch / its mean
+                hipEvent-measured duration against the published dense FP32
+                matrix peak
   bconv         the 17 binary convs: binary-op/s (2 per bit-MAC, border taps
                 counted) against the VALU-popcount roofline
   fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
@@ -34,7 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 # MI355X published peaks
-PEAK_FP32_FLOPS = 157.3e12          # vector FP32 (with packed math)
+PEAK_FP32_FLOPS = 157.3e12          # dense FP32 matrix (MFMA); also the packed-vector figure
 PEAK_HBM = 8.0e12
 
 
@@ -57,7 +58,7 @@ def measured_traffic():
         txt = open(p).read()
     except OSError:
         return None
-    m = re.search(r"`k_real_conv`[^\n]*?moves ([\d.]+) MB in and ([\d.]+) MB out", txt)
+    m = re.search(r"`k_real_\w+`[^\n]*?moves ([\d.]+) MB in and ([\d.]+) MB out", txt)
     return round((float(m.group(1)) + float(m.group(2))) * 1e6) if m else None
 
 
@@ -235,7 +236,7 @@ def main() -> int:
                 "ge/lt thresholds) and x ~ N(0,1) patches, resident in HBM",
         "config": {"workload": "v1 Bi-Real binary UNet forward (nearest upsampler), 32x32x120 patches",
                    "batch": N, "H": H, "W": W, "n_bands": 120, "n_classes": 3, "base_channels": 16},
-        "roofline": {"bound": "valu", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32 FMA)",
+        "roofline": {"bound": "mfma", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32, K=1 MFMA)",
                      "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": measured_traffic(),
                      "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, calibrated)",

@@ -270,18 +270,29 @@ std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int t
 
 struct FoldHost {
   std::vector<int32_t> lo;
-  std::vector<uint32_t> wid, inv;
+  std::vector<uint32_t> wid;
 };
 
+// bnn_fold_canon's (lo, wid, inv) as one modular interval per channel:
+// !((uint32)(P - lo) < wid) == (uint32)(P - (lo + wid)) < 2^32 - wid for every
+// P.  An always-true rule (wid 0, inv 1) becomes [2^31, 2^31 + 2^32 - 1),
+// which holds every P with |P| < 2^30.  Padded channels keep wid = 0.
 FoldHost canon_fold(const Act& a, int coutp) {
   FoldHost f;
   f.lo.assign(coutp, 0);
   f.wid.assign(coutp, 0);
-  f.inv.assign(coutp / 32, 0);
   std::vector<uint8_t> inv(coutp, 0);
   bnn_fold_canon(a.type, a.t, a.lo, a.hi, a.C, f.lo.data(), f.wid.data(), inv.data());
-  for (int c = 0; c < a.C; ++c)
-    if (inv[c]) f.inv[c >> 5] |= 1u << (c & 31);
+  for (int c = 0; c < a.C; ++c) {
+    if (!inv[c]) continue;
+    if (f.wid[c] == 0) {
+      f.lo[c] = INT32_MIN;
+      f.wid[c] = 0xFFFFFFFFu;
+    } else {
+      f.lo[c] = (int32_t)((uint32_t)f.lo[c] + f.wid[c]);
+      f.wid[c] = 0u - f.wid[c];
+    }
+  }
   return f;
 }
 
@@ -306,6 +317,7 @@ struct BnnDevice {
   hipStream_t stream = nullptr;
   std::vector<void*> allocs;
   int rcin = 0, rcout = 0;
+  uint64_t* rwm = nullptr;  // lane-mask weights (all signs +-1), else null and rw is used
   float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   float *hw = nullptr, *hb = nullptr;
@@ -337,12 +349,11 @@ int dev_upload(BnnDevice* D, T** dst, const T* src, size_t n) {
 int upload_fold(BnnDevice* D, FoldDev* fd, const Act& a, int coutp) {
   FoldHost f = canon_fold(a, coutp);
   int32_t* lo;
-  uint32_t *wid, *inv;
+  uint32_t* wid;
   int rc;
   if ((rc = dev_upload(D, &lo, f.lo.data(), f.lo.size()))) return rc;
   if ((rc = dev_upload(D, &wid, f.wid.data(), f.wid.size()))) return rc;
-  if ((rc = dev_upload(D, &inv, f.inv.data(), f.inv.size()))) return rc;
-  fd->lo = lo; fd->wid = wid; fd->inv = inv;
+  fd->lo = lo; fd->wid = wid;
   return BNN_OK;
 }
 
@@ -359,20 +370,28 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   return BNN_OK;
 }
 
-// real conv weights in groups of kRealGroup output channels, folds padded to 32
+// real conv weights: lane masks for the matrix-core kernel when every sign
+// is +-1, else floats in groups of kRealGroup output channels for the
+// vector-ALU kernel; folds padded to 32
 int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
   D->rcin = c.Cin;
   D->rcout = c.Cout;
   const int tot = (c.Cout + 31) / 32 * 32;
-  std::vector<float> w(real_conv_weights_len(c.Cout, c.Cin));
-  real_conv_weights(c.wsign, c.Cout, c.Cin, w.data());
   auto padv = [&](const float* src) {
     std::vector<float> v(tot, 0.0f);
     std::copy(src, src + c.Cout, v.begin());
     return v;
   };
   int rc;
-  if ((rc = dev_upload(D, &D->rw, w.data(), w.size()))) return rc;
+  if (real_conv_signs_only(c.wsign, c.Cout, c.Cin)) {
+    std::vector<uint64_t> wm(real_conv_masks_len(c.Cout, c.Cin));
+    real_conv_masks(c.wsign, c.Cout, c.Cin, wm.data());
+    if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
+  } else {
+    std::vector<float> w(real_conv_weights_len(c.Cout, c.Cin));
+    real_conv_weights(c.wsign, c.Cout, c.Cin, w.data());
+    if ((rc = dev_upload(D, &D->rw, w.data(), w.size()))) return rc;
+  }
   std::vector<float> v;
   v = padv(c.alpha); if ((rc = dev_upload(D, &D->ralpha, v.data(), v.size()))) return rc;
   v = padv(a.A); if ((rc = dev_upload(D, &D->rA, v.data(), v.size()))) return rc;
@@ -522,6 +541,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     RealArgs ra{};
     ra.x = d_in;
     ra.w = D->rw;
+    ra.wm = D->rwm;
     ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
     ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
     ra.out = w.a1;

@@ -137,13 +137,22 @@ void conv_realin_naive(const float* x, const int8_t* wsign, const float* alpha, 
   const bool fast = kh == 3 && kw == 3 && pad == 1 && stride == 1;
   if (fast) {
     const int tot = (Cout + 31) / 32 * 32;
-    std::vector<float> w(real_conv_weights_len(Cout, Cin)), al(tot, 0.0f);
-    real_conv_weights(wsign, Cout, Cin, w.data());
+    std::vector<float> al(tot, 0.0f);
     std::copy(alpha, alpha + Cout, al.begin());
-    std::unique_ptr<Buf> dw(up(w.data(), w.size() * 4)), dal(up(al.data(), al.size() * 4));
+    std::unique_ptr<Buf> dw, dal(up(al.data(), al.size() * 4));
     RealArgs r{};
+    if (real_conv_signs_only(wsign, Cout, Cin)) {
+      std::vector<uint64_t> wm(real_conv_masks_len(Cout, Cin));
+      real_conv_masks(wsign, Cout, Cin, wm.data());
+      dw.reset(up(wm.data(), wm.size() * 8));
+      r.wm = dw->as<uint64_t>();
+    } else {
+      std::vector<float> w(real_conv_weights_len(Cout, Cin));
+      real_conv_weights(wsign, Cout, Cin, w.data());
+      dw.reset(up(w.data(), w.size() * 4));
+      r.w = dw->as<float>();
+    }
     r.x = dx->as<float>();
-    r.w = dw->as<float>();
     r.alpha = dal->as<float>();
     r.N = 1; r.H = H; r.W = W; r.cin = Cin; r.cout = Cout;
     r.f32 = dout.as<float>();

@@ -22,13 +22,30 @@ enum Epi : int {
   EPI_P = 3,     // raw int32 P [N][Cout][H][W]
 };
 
-// One canonical interval per channel: bit = ((uint32)(P - lo) < wid) ^ inv.
-// Covers every integer rule type (csrc/bnn_fold.c:37-60).
+// One modular interval per channel: bit = (uint32)(P - lo) < wid.  Covers
+// every integer rule type (csrc/bnn_fold.c:37-60); a complemented interval
+// [lo, lo+wid) is the interval [lo+wid, lo+2^32), so no inversion flag is
+// needed.  Arrays are padded to a multiple of 32 channels with wid = 0.
 struct FoldDev {
   const int32_t* lo;
   const uint32_t* wid;
-  const uint32_t* inv;  // bit c & 31 of word c >> 5
 };
+
+// n / d by multiply-high for 0 <= n < 2^31: q = d == 1 ? n : mulhi(n, mul) >> shr
+// with mul = ceil(2^p / d), p = 31 + ceil(log2 d), shr = p - 32.
+struct FastDiv {
+  uint32_t d, mul, shr;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0u, 0u};
+  if (d <= 1) return f;
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint32_t p = 31 + l;
+  f.mul = (uint32_t)(((1ull << p) + d - 1) / d);
+  f.shr = p - 32;
+  return f;
+}
 
 struct BconvArgs {
   const uint32_t* in0;  // plain input, or the skip half of a concat
@@ -39,6 +56,8 @@ struct BconvArgs {
   int uh, uw;           // rows/cols of H x W the upsample covers (from oh/ow)
   int N, H, W;
   int cin, cout;        // true channel counts
+  uint32_t ntiles;      // N * tiles per patch (set by launch_bconv)
+  FastDiv dper, dtw;    // tiles per patch, tiles per row (set by launch_bconv)
   const uint32_t* wt;   // [cw0+cw1][cout][9]
   FoldDev f1, f2;
   uint32_t* out;        // bits [N][H][W][cwo]  (EPI_FOLD/POOL)
@@ -54,7 +73,8 @@ struct BconvArgs {
 
 struct RealArgs {
   const float* x;
-  const float* w;       // [ceil(cout/G)][cin][9][G]
+  const float* w;       // [ceil(cout/G)][cin][9][G] (vector-ALU kernel)
+  const uint64_t* wm;   // [ceil(cout/16)][cin][9] lane masks (matrix-core kernel), or null
   const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;
@@ -87,6 +107,25 @@ inline void real_conv_weights(const int8_t* wsign, int cout, int cin, float* out
     for (int ci = 0; ci < cin; ++ci)
       for (int t = 0; t < 9; ++t)
         out[(((size_t)(co / G) * cin + ci) * 9 + t) * G + co % G] = (float)wsign[((size_t)co * cin + ci) * 9 + t];
+}
+
+// Matrix-core real-conv weights, for +-1 signs only: one 64-bit lane mask per
+// (16-channel group g, ci, tap t), bit l set iff w[16g + l%16][ci][t] > 0.
+// Channels past cout leave their bits 0.
+inline size_t real_conv_masks_len(int cout, int cin) { return (size_t)((cout + 15) / 16) * cin * 9; }
+inline bool real_conv_signs_only(const int8_t* wsign, int cout, int cin) {
+  for (size_t i = 0; i < (size_t)cout * cin * 9; ++i)
+    if (wsign[i] != 1 && wsign[i] != -1) return false;
+  return true;
+}
+inline void real_conv_masks(const int8_t* wsign, int cout, int cin, uint64_t* out) {
+  for (size_t i = 0; i < real_conv_masks_len(cout, cin); ++i) out[i] = 0;
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci)
+      for (int t = 0; t < 9; ++t)
+        if (wsign[((size_t)co * cin + ci) * 9 + t] > 0)
+          for (int q = 0; q < 4; ++q)
+            out[((size_t)(co / 16) * cin + ci) * 9 + t] |= 1ull << (16 * q + co % 16);
 }
 
 // Launchers return hipSuccess or the first launch error.  mt = micro-tile

@@ -211,8 +211,164 @@ __global__ __launch_bounds__(RLANES * RG) void k_real_conv(const RealArgs a, uin
 }
 
 // ------------------------------------------------------------------------
+// real-input conv on the matrix cores
+// ------------------------------------------------------------------------
+// v_mfma_f32_16x16x1_4b_f32 computes, for 4 blocks b, D_b[i][j] =
+// fma(A_b[i], B_b[j], C_b[i][j]), each element rounded once to nearest
+// even: with K = 1 an element is exactly one step s = fma(x, w, s) of the
+// reference's per-tap chain (the device matches fmaf bit for bit, signed
+// zeros and denormals included).  Rows i are 16 output channels, columns j
+// 16 pixels of an output row, blocks 4 consecutive rows, so a wave owns a
+// 4 x 16 pixel tile and keeps one 16-register accumulator block per tap.
+// Operand A is the +-1 weight of the lane's channel, selected by a
+// per-(ci, tap) lane mask; operand B is the input value the lane's pixel
+// sees through the tap, read from the LDS tile.  Lane layout: A lane l ->
+// block l/16, row l%16; B lane l -> block l/16, column l%16; D register r
+// of lane l -> block r/4, row 4*(l/16) + r%4, column l%16.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int WR, int WC>  // waves along rows / columns: tile (4*WR) x (16*WC)
+__global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH,
+                                                            int tilesW) {
+  constexpr int TR = 4 * WR, TC = 16 * WC, NT = 64 * WR * WC;
+  constexpr int CI = 8;  // input channels per LDS chunk
+  constexpr int LR = TR + 2, LC = TC + 2, LPL = LR * LC, LTILE = CI * LPL;
+  constexpr int KL = (LTILE + NT - 1) / NT;
+  __shared__ float tile[2][LTILE];  // [ci][row][col], zero outside the image
+  __shared__ uint32_t obits[TR * TC];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = (wv / WC) * 4, wc = (wv % WC) * 16;
+  int bid = blockIdx.x;
+  const int tx = bid % tilesW;
+  bid /= tilesW;
+  const int ty = bid % tilesH;
+  const int n = bid / tilesH;
+  const int y0 = ty * TR, x0 = tx * TC;
+  const int g = blockIdx.y;  // 16-channel group
+  const int HW = a.H * a.W;
+  for (int i = tid; i < TR * TC; i += NT) obits[i] = 0;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
+
+  // this thread's share of every chunk: tile element e = tid + k*NT (the
+  // tile is stored in e order) and its byte offset in the chunk, or an
+  // offset past the buffer (reads 0) outside the image
+  uint32_t goff[KL];
+#pragma unroll
+  for (int k = 0; k < KL; ++k) {
+    const int e = tid + k * NT;
+    const int cil = e / LPL, rem = e - cil * LPL;
+    const int row = rem / LC, col = rem - row * LC;
+    const int gy = y0 - 1 + row, gx = x0 - 1 + col;
+    const bool ok = e < LTILE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+    goff[k] = ok ? (uint32_t)(((size_t)n * a.cin + cil) * HW + (size_t)gy * a.W + gx) * 4u : 0x80000000u;
+  }
+  const uint32_t chunk_bytes = (uint32_t)CI * (uint32_t)HW * 4u;
+  const int nchunk = (a.cin + CI - 1) / CI;
+
+  f32x16 acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+
+  float pre[KL];
+#pragma unroll
+  for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], 0);
+#pragma unroll
+  for (int k = 0; k < KL; ++k)
+    if (tid + k * NT < LTILE) tile[0][tid + k * NT] = pre[k];
+  __syncthreads();
+
+  const uint64_t* wm = a.wm + (size_t)g * a.cin * 9;
+  const int lb = (wr + (lane >> 4)) * LC + wc + (lane & 15);
+#pragma unroll 1
+  for (int ch = 0; ch < nchunk; ++ch) {
+    const int buf = ch & 1;
+    const bool more = ch + 1 < nchunk;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], (uint32_t)(ch + 1) * chunk_bytes);
+    }
+    const int ci0 = ch * CI;
+    const int nci = a.cin - ci0 < CI ? a.cin - ci0 : CI;
+    const float* tb = tile[buf] + lb;
+#pragma unroll
+    for (int cl = 0; cl < CI; ++cl) {
+      if (cl < nci) {
+        float xb[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) xb[t] = tb[cl * LPL + (t / 3) * LC + t % 3];
+        const uint64_t* m = wm + (size_t)(ci0 + cl) * 9;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+          const float w = __builtin_amdgcn_inverse_ballot_w64(m[t]) ? 1.0f : -1.0f;
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x1f32(w, xb[t], acc[t], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < KL; ++k)
+        if (tid + k * NT < LTILE) tile[buf ^ 1][tid + k * NT] = pre[k];
+    }
+    __syncthreads();
+  }
+
+  // taps in row-major order into acc (an out-of-image tap summed zeros to
+  // +0 and leaves it unchanged), alpha, then the real fold
+  // (csrc/bnn_fold.c:62-77): z = fma(A, x, B); z<0 -> slope*z; r = z + rsign;
+  // bit = r > 0.  The reference build fuses A*x+B only.
+  const int xo = x0 + wc + (lane & 15);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 9; ++t) v = __fadd_rn(v, acc[t][r]);
+    const int yl = wr + (r >> 2);
+    const int y = y0 + yl;
+    const int co = g * 16 + 4 * (lane >> 4) + (r & 3);
+    if (y >= a.H || xo >= a.W || co >= a.cout) continue;
+    const float o = __fmul_rn(a.alpha[co], v);
+    if (a.f32) a.f32[((size_t)n * a.cout + co) * HW + (size_t)y * a.W + xo] = o;
+    if (a.out) {
+      float z = __fmaf_rn(a.A[co], o, a.B[co]);
+      if (z < 0.0f) z = __fmul_rn(a.slope[co], z);
+      const float rr = __fadd_rn(z, a.rsign[co]);
+      if (rr > 0.0f) atomicOr(&obits[yl * TC + wc + (lane & 15)], 1u << (co & 31));
+    }
+  }
+  if (!a.out) return;
+  // group g owns bits [16g, 16g+16) of each pixel: a 16-bit store, or the
+  // whole word (upper half 0) when it is the last group and starts a word
+  __syncthreads();
+  const int cwo = (a.cout + 31) >> 5;
+  const bool whole = (g & 1) == 0 && g == (int)gridDim.y - 1;
+  for (int i = tid; i < TR * TC; i += NT) {
+    const int y = y0 + i / TC, x = x0 + i % TC;
+    if (y >= a.H || x >= a.W) continue;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)y * a.W + x) * cwo) + g * 2;
+    if (whole) *reinterpret_cast<uint32_t*>(dst) = obits[i];
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(obits[i] >> ((g & 1) * 16));
+  }
+}
+
+// ------------------------------------------------------------------------
 // binary conv with fused epilogues
 // ------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return f.d == 1 ? n : (__umulhi(n, f.mul) >> f.shr);
+}
+
+// acc + popcount(x) as one v_bcnt_u32_b32.  Written as a chain on purpose:
+// left to itself the compiler turns the per-tap sum into popcount-into-zero
+// plus v_add3 trees, a quarter more VALU work for the same count.
+__device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
+  uint32_t r;
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+  return r;
+}
+
 template <int MT, int COG>
 struct Acc {
   uint32_t d[MT * MT][COG];
@@ -236,32 +392,62 @@ __device__ __forceinline__ void accumulate(Acc<MT, COG>& D, const uint32_t (&av)
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky)
 #pragma unroll
-          for (int kx = 0; kx < 3; ++kx) {
-            const uint32_t v = (av[py + ky][px + kx] ^ w9[ky * 3 + kx]) & m[py + ky][px + kx];
-            d = (uint32_t)__builtin_popcount(v) + d;
-          }
+          for (int kx = 0; kx < 3; ++kx)
+            d = bcnt_acc((av[py + ky][px + kx] ^ w9[ky * 3 + kx]) & m[py + ky][px + kx], d);
         D.d[py * MT + px][j] = d;
       }
   }
 }
 
-__device__ __forceinline__ uint32_t fold_bit(int32_t P, const FoldDev& f, int co) {
-  return ((uint32_t)(P - f.lo[co]) < f.wid[co]) ? 1u : 0u;
+template <int NP>
+__device__ __forceinline__ void load_window(uint32_t (&av)[NP][NP], __amdgpu_buffer_rsrc_t rs,
+                                            const uint32_t (&vo)[NP][NP], uint32_t soff) {
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+#pragma unroll
+    for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, vo[i][k], soff);
 }
-__device__ __forceinline__ uint32_t inv_bits(const FoldDev& f, int co0, int cog) {
-  const uint32_t w = f.inv[co0 >> 5] >> (co0 & 31);
-  return cog == 32 ? w : (w & ((1u << cog) - 1u));
+
+// Sum one input segment (cw words per pixel) into D.  Two windows
+// alternate so that the next word's loads are in flight while the current
+// word is consumed.  The loads are unconditional (a conditional load makes
+// the compiler wait for every outstanding load before the next use), so the
+// last pair also fetches the word after the segment: the pixel's next word,
+// the next pixel's first word, or past the end of the buffer, which reads 0.
+// That word is never used.
+template <int MT, int COG>
+__device__ __forceinline__ void conv_segment(Acc<MT, COG>& D, __amdgpu_buffer_rsrc_t rs,
+                                             const uint32_t (&vo)[MT + 2][MT + 2],
+                                             const uint32_t (&m)[MT + 2][MT + 2], int cw,
+                                             const uint32_t* __restrict__ wt, int rowstride) {
+  constexpr int NP = MT + 2;
+  uint32_t wa[NP][NP], wb[NP][NP];
+  load_window<NP>(wa, rs, vo, 0u);
+  int w = 0;
+#pragma unroll 1
+  for (; w + 1 < cw; w += 2) {
+    load_window<NP>(wb, rs, vo, (uint32_t)(w + 1) * 4u);
+    accumulate<MT, COG>(D, wa, m, wt + (size_t)w * rowstride);
+    load_window<NP>(wa, rs, vo, (uint32_t)(w + 2) * 4u);
+    accumulate<MT, COG>(D, wb, m, wt + (size_t)(w + 1) * rowstride);
+  }
+  if (w < cw) accumulate<MT, COG>(D, wa, m, wt + (size_t)w * rowstride);
 }
-// Store the COG bits of one channel group.  The last group also writes 0 to
-// the bytes above it in its word (at most 3), so every word is fully
-// written even when cout is not a multiple of 32.
+
+// Store the COG bits of one channel group.  A group that alone covers its
+// 32-bit word writes the whole word; otherwise the last group also writes 0
+// to the bytes above it (at most 3), so every word is fully written even
+// when cout is not a multiple of 32.
 template <int COG>
-__device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, int co0, uint32_t bits,
+__device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, int co0, int cout, uint32_t bits,
                                            int zero_end) {
   uint8_t* row = reinterpret_cast<uint8_t*>(base) + pix * (size_t)cw * 4;
   uint8_t* dst = row + (co0 >> 3);
-  if (COG == 32) *reinterpret_cast<uint32_t*>(dst) = bits;
-  else if (COG == 16) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bits;
+  if (COG == 32 || ((co0 & 31) == 0 && co0 + COG >= cout)) {
+    *reinterpret_cast<uint32_t*>(dst) = bits;
+    return;
+  }
+  if (COG == 16) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bits;
   else *dst = (uint8_t)bits;
   for (int b = (co0 + COG) >> 3; b < zero_end; ++b) row[b] = 0;
 }
@@ -269,38 +455,47 @@ __device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, i
 template <int MT, int COG, int EPI, bool DUMP>
 __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t bytes0, uint32_t bytes1) {
   constexpr int NP = MT + 2;
-  const int tH = (a.H + MT - 1) / MT, tW = (a.W + MT - 1) / MT;
-  const int per = tH * tW;
-  const long ntiles = (long)a.N * per;
-  long tile = (long)blockIdx.x * kBlock + threadIdx.x;
-  const bool active = tile < ntiles;
-  if (!active) tile = ntiles - 1;
-  const int n = (int)(tile / per);
-  const int rr = (int)(tile - (long)n * per);
-  const int ty = rr / tW, tx = rr - ty * tW;
-  const int y0 = ty * MT, x0 = tx * MT;
+  uint32_t tile = blockIdx.x * kBlock + threadIdx.x;
+  const bool active = tile < a.ntiles;
+  if (!active) tile = a.ntiles - 1;
+  const uint32_t n = fdiv(tile, a.dper);
+  const uint32_t rr = tile - n * a.dper.d;
+  const uint32_t ty = fdiv(rr, a.dtw);
+  const uint32_t tx = rr - ty * a.dtw.d;
+  const int y0 = (int)ty * MT, x0 = (int)tx * MT;
   const int co0 = blockIdx.y * COG;
   const int coutp = (a.cout + 31) & ~31;  // weight rows are padded to 32
 
-  uint32_t m[NP][NP];
-  uint32_t voff[NP][NP];
+  // The (MT+2)^2 window around the tile: a row or column outside the image
+  // gets a zero mask and is read from the tile's own first row or column,
+  // so every load stays inside the tensor.
   bool rok[NP], cok[NP];
   int rc[NP], cc[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int iy = y0 - 1 + i, ix = x0 - 1 + i;
-    rok[i] = iy >= 0 && iy < a.H;
-    cok[i] = ix >= 0 && ix < a.W;
-    rc[i] = rok[i] ? iy : (iy < 0 ? 0 : a.H - 1);
-    cc[i] = cok[i] ? ix : (ix < 0 ? 0 : a.W - 1);
+    rok[i] = (uint32_t)iy < (uint32_t)a.H;
+    cok[i] = (uint32_t)ix < (uint32_t)a.W;
+    rc[i] = rok[i] ? iy : y0;
+    cc[i] = cok[i] ? ix : x0;
   }
+  uint32_t m[NP][NP], vo[NP][NP];
+  {
+    const uint32_t cw4 = (uint32_t)a.cw0 * 4u;
+    uint32_t ro[NP], co[NP];
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
-#pragma unroll
-    for (int k = 0; k < NP; ++k) {
-      m[i][k] = (rok[i] && cok[k]) ? ~0u : 0u;
-      voff[i][k] = (uint32_t)(((size_t)n * a.H + rc[i]) * a.W + cc[k]) * (uint32_t)a.cw0 * 4u;
+    for (int i = 0; i < NP; ++i) {
+      ro[i] = (n * (uint32_t)a.H + (uint32_t)rc[i]) * (uint32_t)a.W * cw4;
+      co[i] = (uint32_t)cc[i] * cw4;
     }
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+#pragma unroll
+      for (int k = 0; k < NP; ++k) {
+        m[i][k] = (rok[i] && cok[k]) ? ~0u : 0u;
+        vo[i][k] = ro[i] + co[k];
+      }
+  }
 
   Acc<MT, COG> D;
 #pragma unroll
@@ -308,62 +503,46 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
 #pragma unroll
     for (int j = 0; j < COG; ++j) D.d[p][j] = 0;
 
-  {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in0, bytes0);
-#pragma unroll 1
-    for (int w = 0; w < a.cw0; ++w) {
-      uint32_t av[NP][NP];
-#pragma unroll
-      for (int i = 0; i < NP; ++i)
-#pragma unroll
-        for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, voff[i][k], (uint32_t)w * 4u);
-      accumulate<MT, COG>(D, av, m, a.wt + ((size_t)w * coutp + co0) * 9);
-    }
-  }
+  conv_segment<MT, COG>(D, make_rsrc(a.in0, bytes0), vo, m, a.cw0, a.wt + (size_t)co0 * 9, coutp * 9);
   if (a.cw1 > 0) {
-    // nearest 2x of the low-res tensor placed at (oh, ow); uncovered in-image
-    // positions read as 0 bits (the reference's zero-filled concat, whose 0
-    // entries its XNOR kernels treat as -1: csrc/bnn_model.c:130-148,
-    // csrc/bnn_conv.c:123, 162)
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in1, bytes1);
-    uint32_t cm[NP][NP];
+    // nearest 2x of the low-res tensor placed at (oh, ow); in-image positions
+    // it does not cover read as 0 bits (the reference's zero-filled concat,
+    // whose 0 entries its XNOR kernels treat as -1: csrc/bnn_model.c:130-148,
+    // csrc/bnn_conv.c:123, 162).  They are given an offset past the end of
+    // the buffer, where buffer loads return 0.
+    const uint32_t cw4 = (uint32_t)a.cw1 * 4u;
+    uint32_t lr[NP], lc[NP];
+    bool rcov[NP], ccov[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int uy = rc[i] - a.oh, ux = cc[i] - a.ow;
+      rcov[i] = (uint32_t)uy < (uint32_t)a.uh;
+      ccov[i] = (uint32_t)ux < (uint32_t)a.uw;
+      lr[i] = (n * (uint32_t)a.h1 + (uint32_t)(rcov[i] ? uy >> 1 : 0)) * (uint32_t)a.w1 * cw4;
+      lc[i] = (uint32_t)(ccov[i] ? ux >> 1 : 0) * cw4;
+    }
 #pragma unroll
     for (int i = 0; i < NP; ++i)
 #pragma unroll
-      for (int k = 0; k < NP; ++k) {
-        const int uy = rc[i] - a.oh, ux = cc[k] - a.ow;
-        const bool cov = uy >= 0 && uy < a.uh && ux >= 0 && ux < a.uw;
-        cm[i][k] = cov ? ~0u : 0u;
-        const int ly = cov ? (uy >> 1) : 0, lx = cov ? (ux >> 1) : 0;
-        voff[i][k] = (uint32_t)(((size_t)n * a.h1 + ly) * a.w1 + lx) * (uint32_t)a.cw1 * 4u;
-      }
-#pragma unroll 1
-    for (int w = 0; w < a.cw1; ++w) {
-      uint32_t av[NP][NP];
-#pragma unroll
-      for (int i = 0; i < NP; ++i)
-#pragma unroll
-        for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, voff[i][k], (uint32_t)w * 4u) & cm[i][k];
-      accumulate<MT, COG>(D, av, m, a.wt + ((size_t)(a.cw0 + w) * coutp + co0) * 9);
-    }
+      for (int k = 0; k < NP; ++k) vo[i][k] = (rcov[i] && ccov[k]) ? lr[i] + lc[k] : 0x80000000u;
+    conv_segment<MT, COG>(D, make_rsrc(a.in1, bytes1), vo, m, a.cw1,
+                          a.wt + ((size_t)a.cw0 * coutp + co0) * 9, coutp * 9);
   }
   if (!active) return;
 
   // ---------------------------------------------------------- epilogue --
-  int32_t Pv[MT * MT][COG];
+  int32_t nvalid[MT * MT];
   bool inimg[MT * MT];
 #pragma unroll
   for (int py = 0; py < MT; ++py)
 #pragma unroll
     for (int px = 0; px < MT; ++px) {
-      const int y = y0 + py, x = x0 + px;
-      inimg[py * MT + px] = y < a.H && x < a.W;
+      inimg[py * MT + px] = y0 + py < a.H && x0 + px < a.W;
       const int nr = (int)rok[py] + (int)rok[py + 1] + (int)rok[py + 2];
       const int nc = (int)cok[px] + (int)cok[px + 1] + (int)cok[px + 2];
-      const int32_t nvalid = nr * nc * a.cin;
-#pragma unroll
-      for (int j = 0; j < COG; ++j) Pv[py * MT + px][j] = nvalid - 2 * (int32_t)D.d[py * MT + px][j];
+      nvalid[py * MT + px] = nr * nc * a.cin;
     }
+  auto Pof = [&](int p, int j) -> int32_t { return nvalid[p] - 2 * (int32_t)D.d[p][j]; };
 
   const int HW = a.H * a.W;
   if (EPI == EPI_P || DUMP) {
@@ -375,60 +554,87 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
         const int pix = (y0 + py) * a.W + x0 + px;
 #pragma unroll
         for (int j = 0; j < COG; ++j)
-          if (co0 + j < a.cout) a.P[((size_t)n * a.cout + co0 + j) * HW + pix] = Pv[py * MT + px][j];
+          if (co0 + j < a.cout) a.P[((size_t)n * a.cout + co0 + j) * HW + pix] = Pof(py * MT + px, j);
       }
   }
   if (EPI == EPI_P) return;
 
   // bytes of the pixel's words the last channel group zero-fills
   const int zero_end = blockIdx.y == gridDim.y - 1 ? a.cwo * 4 : 0;
-  const uint32_t inv1 = inv_bits(a.f1, co0, COG);
+  const int32_t* lo1 = a.f1.lo + co0;
+  const uint32_t* wd1 = a.f1.wid + co0;
   uint32_t bits[MT * MT];
 #pragma unroll
-  for (int p = 0; p < MT * MT; ++p) {
-    uint32_t b = 0;
+  for (int p = 0; p < MT * MT; ++p) bits[p] = 0;
+
+  if (EPI == EPI_POOL) {
+    // rule 1 on each P, 2x2 floor-mode max of P (csrc/bnn_maxpool.c:28-48),
+    // then rule 2 on the max
+    const int32_t* lo2 = a.f2.lo + co0;
+    const uint32_t* wd2 = a.f2.wid + co0;
+    const bool pooled = y0 + 1 < a.H && x0 + 1 < a.W;
+    const int Hh = a.H >> 1, Wh = a.W >> 1;
+    uint32_t b2 = 0;
 #pragma unroll
-    for (int j = 0; j < COG; ++j) b |= fold_bit(Pv[p][j], a.f1, co0 + j) << j;
-    bits[p] = b ^ inv1;
+    for (int j = 0; j < COG; ++j) {
+      int32_t pm = INT32_MIN;
+#pragma unroll
+      for (int p = 0; p < MT * MT; ++p) {
+        const int32_t P = Pof(p, j);
+        bits[p] |= ((uint32_t)P - (uint32_t)lo1[j] < wd1[j] ? 1u : 0u) << j;
+        pm = max(pm, P);
+      }
+      b2 |= ((uint32_t)pm - (uint32_t)lo2[j] < wd2[j] ? 1u : 0u) << j;
+      if (DUMP && pooled && co0 + j < a.cout)
+        a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
+    }
+    if (a.out != nullptr) {
+#pragma unroll
+      for (int py = 0; py < MT; ++py)
+#pragma unroll
+        for (int px = 0; px < MT; ++px)
+          if (inimg[py * MT + px])
+            store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, a.cout,
+                            bits[py * MT + px], zero_end);
+    }
+    if (pooled) store_bits<COG>(a.out2, ((size_t)n * Hh + ty) * Wh + tx, a.cwo, co0, a.cout, b2, zero_end);
+    return;
   }
 
-  if (EPI == EPI_FOLD || (EPI == EPI_POOL && a.out != nullptr)) {
+  if (EPI == EPI_FOLD) {
+#pragma unroll
+    for (int j = 0; j < COG; ++j)
+#pragma unroll
+      for (int p = 0; p < MT * MT; ++p) bits[p] |= ((uint32_t)Pof(p, j) - (uint32_t)lo1[j] < wd1[j] ? 1u : 0u) << j;
 #pragma unroll
     for (int py = 0; py < MT; ++py)
 #pragma unroll
       for (int px = 0; px < MT; ++px)
         if (inimg[py * MT + px])
-          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, bits[py * MT + px],
-                          zero_end);
+          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, a.cout,
+                          bits[py * MT + px], zero_end);
+    return;
   }
-  if (EPI == EPI_POOL) {
-    // 2x2 floor-mode max on P (csrc/bnn_maxpool.c:28-48), then the down rule
-    if (y0 + 1 < a.H && x0 + 1 < a.W) {
-      const int Hh = a.H >> 1, Wh = a.W >> 1;
-      uint32_t b = 0;
-#pragma unroll
-      for (int j = 0; j < COG; ++j) {
-        const int32_t pm = max(max(Pv[0][j], Pv[1][j]), max(Pv[2][j], Pv[3][j]));
-        b |= fold_bit(pm, a.f2, co0 + j) << j;
-        if (DUMP && co0 + j < a.cout)
-          a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
-      }
-      b ^= inv_bits(a.f2, co0, COG);
-      store_bits<COG>(a.out2, ((size_t)n * Hh + ty) * Wh + tx, a.cwo, co0, b, zero_end);
-    }
-  }
+
   if (EPI == EPI_HEAD) {
-    // widen +-1 to float and the 1x1 head: bias first, then channels in
-    // order, one fused step each (csrc/bnn_head.c:21-34)
-    if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, bits[0], zero_end);
+    // rule, widen to +-1 and the 1x1 head: bias first, then channels in
+    // order, one fused step each (csrc/bnn_head.c:21-34).  One group holds
+    // every channel (cout <= COG).
+    float sg[COG];
+#pragma unroll
+    for (int j = 0; j < COG; ++j) {
+      const bool b = (uint32_t)Pof(0, j) - (uint32_t)lo1[j] < wd1[j];
+      bits[0] |= (b ? 1u : 0u) << j;
+      sg[j] = b ? 1.0f : -1.0f;
+    }
+    if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, a.cout, bits[0], zero_end);
     const int pix = y0 * a.W + x0;
 #pragma unroll 1
     for (int o = 0; o < a.ncls; ++o) {
       float accf = a.hb[o];
 #pragma unroll
       for (int j = 0; j < COG; ++j)
-        if (j < a.cout)
-          accf = __fmaf_rn(a.hw[o * a.cout + j], ((bits[0] >> j) & 1u) ? 1.0f : -1.0f, accf);
+        if (j < a.cout) accf = __fmaf_rn(a.hw[o * a.cout + j], sg[j], accf);
       a.logits[((size_t)n * a.ncls + o) * HW + pix] = accf;
     }
   }
@@ -592,13 +798,18 @@ __global__ void k_head(const float* __restrict__ a, const float* __restrict__ W,
 inline unsigned blocks_for(long n, int bs = kBlock) { return (unsigned)((n + bs - 1) / bs); }
 
 template <int MT, int COG, int EPI, bool DUMP>
-hipError_t go_bconv(const BconvArgs& a, hipStream_t s) {
-  const long ntiles = (long)a.N * ((a.H + MT - 1) / MT) * ((a.W + MT - 1) / MT);
+hipError_t go_bconv(BconvArgs a, hipStream_t s) {
+  const uint32_t tH = (uint32_t)(a.H + MT - 1) / MT, tW = (uint32_t)(a.W + MT - 1) / MT;
+  const uint64_t ntiles = (uint64_t)a.N * tH * tW;
+  if (ntiles >= 0x80000000ull) return hipErrorInvalidValue;
+  a.ntiles = (uint32_t)ntiles;
+  a.dper = make_fastdiv(tH * tW);
+  a.dtw = make_fastdiv(tW);
   const int groups = (a.cout + COG - 1) / COG;
   const uint32_t b0 = (uint32_t)((size_t)a.N * a.H * a.W * a.cw0 * 4);
   const uint32_t b1 = a.in1 ? (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4) : 0u;
-  hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for(ntiles), groups), dim3(kBlock), 0, s, a,
-                     b0, b1);
+  hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for((long)ntiles), groups), dim3(kBlock), 0, s,
+                     a, b0, b1);
   return hipGetLastError();
 }
 
@@ -619,7 +830,9 @@ hipError_t go_bconv_cog(const BconvArgs& a, int cog, hipStream_t s) {
 
 hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump, hipStream_t s) {
   if (a.N <= 0 || a.H <= 0 || a.W <= 0) return hipSuccess;
-  if ((size_t)a.N * a.H * a.W * (a.cw0 > 0 ? a.cw0 : 1) * 4 >= 0xffffffffull) return hipErrorInvalidValue;
+  // byte offsets are 32-bit and 0x80000000 marks "reads 0": tensors stay below 2 GiB
+  if ((size_t)a.N * a.H * a.W * (a.cw0 > 0 ? a.cw0 : 1) * 4 >= 0x80000000ull) return hipErrorInvalidValue;
+  if (a.in1 && (size_t)a.N * a.h1 * a.w1 * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_FOLD:
       if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);
@@ -641,10 +854,24 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   return hipErrorInvalidValue;
 }
 
+#ifndef BNN_MWR
+#define BNN_MWR 4
+#endif
+#ifndef BNN_MWC
+#define BNN_MWC 2
+#endif
+
 hipError_t launch_real(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   const size_t xbytes = (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
+  if (a.wm) {
+    constexpr int WR = BNN_MWR, WC = BNN_MWC;
+    const int tilesH = (a.H + 4 * WR - 1) / (4 * WR), tilesW = (a.W + 16 * WC - 1) / (16 * WC);
+    dim3 grid((unsigned)((long)a.N * tilesH * tilesW), (unsigned)((a.cout + 15) / 16));
+    hipLaunchKernelGGL((k_real_mfma<WR, WC>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH, tilesW);
+    return hipGetLastError();
+  }
   const int tilesH = (a.H + RT - 1) / RT, tilesW = (a.W + RW - 1) / RW;
   const int groups = (a.cout + RCO - 1) / RCO;
   constexpr int maxg = 1024 / RLANES;

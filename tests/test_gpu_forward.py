@@ -58,6 +58,32 @@ def test_stages_vs_checker(tmp_path, orc, seed, base, cov, N, H, W):
     eng.close()
 
 
+def test_first_conv_general_signs(tmp_path, orc):
+    """A first-conv weight outside {-1, +1} (0, +-2: the products stay
+    exact) sends the engine to its vector-ALU real conv; the +-1 blob of the
+    same seed runs on the matrix cores.  Both match the checker bit for bit."""
+    b = synth.make_blob(seed=21)
+    x = synth.make_input(22, 3, 120, 32, 32)
+    rng = np.random.default_rng(23)
+    w = b.enc_conv1[0].wsign.copy()
+    flat = w.reshape(-1)
+    idx = rng.choice(flat.size, 64, replace=False)
+    flat[idx[:32]] = 0
+    flat[idx[32:48]] = 2
+    flat[idx[48:]] = -2
+    for ws in (b.enc_conv1[0].wsign, w):
+        b.enc_conv1[0].wsign = ws
+        eng, _ = _engine(tmp_path, b)
+        model = orc.parse(B.to_bytes(b))
+        logits, st = eng.forward_debug(x)
+        for n in range(3):
+            want, ref_st = model.forward(x[n], stages=True)
+            for name in ("enc1.conv1", "enc1.act1"):
+                assert _same(st[name][n], ref_st[name]), (name, n)
+            assert _same(logits[n], want), n
+        eng.close()
+
+
 def test_golden_from_reference(tmp_path, golden):
     """stage hashes and logits recorded from the reference's own C"""
     meta, arrays = golden
