@@ -74,7 +74,7 @@ struct BconvArgs {
 struct RealArgs {
   const float* x;
   const float* w;       // [ceil(cout/G)][cin][9][G] (vector-ALU kernel)
-  const uint64_t* wm;   // [ceil(cout/16)][cin][9] lane masks (matrix-core kernel), or null
+  const uint64_t* wm;   // [ceil(cout/16)][cin padded][3] lane masks (matrix-core kernel), or null
   const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;
@@ -109,23 +109,32 @@ inline void real_conv_weights(const int8_t* wsign, int cout, int cin, float* out
         out[(((size_t)(co / G) * cin + ci) * 9 + t) * G + co % G] = (float)wsign[((size_t)co * cin + ci) * 9 + t];
 }
 
-// Matrix-core real-conv weights, for +-1 signs only: one 64-bit lane mask per
-// (16-channel group g, ci, tap t), bit l set iff w[16g + l%16][ci][t] > 0.
-// Channels past cout leave their bits 0.
-inline size_t real_conv_masks_len(int cout, int cin) { return (size_t)((cout + 15) / 16) * cin * 9; }
+// Matrix-core real-conv weights, for +-1 signs only.  Input channels come
+// in chunks of kRealMfmaCI (the array is zero-padded to whole chunks); per
+// (16-channel group g, ci) there are three 64-bit lane masks, mask q
+// holding taps 4q..4q+3: bit 16k + i is set iff w[16g + i][ci][4q + k] > 0
+// (taps past 8 and channels past cout leave their bits 0).
+#ifndef BNN_MCI
+#define BNN_MCI 8
+#endif
+constexpr int kRealMfmaCI = BNN_MCI;
+inline int real_conv_cin_pad(int cin) { return (cin + kRealMfmaCI - 1) / kRealMfmaCI * kRealMfmaCI; }
+inline size_t real_conv_masks_len(int cout, int cin) {
+  return (size_t)((cout + 15) / 16) * real_conv_cin_pad(cin) * 3;
+}
 inline bool real_conv_signs_only(const int8_t* wsign, int cout, int cin) {
   for (size_t i = 0; i < (size_t)cout * cin * 9; ++i)
     if (wsign[i] != 1 && wsign[i] != -1) return false;
   return true;
 }
 inline void real_conv_masks(const int8_t* wsign, int cout, int cin, uint64_t* out) {
+  const int cp = real_conv_cin_pad(cin);
   for (size_t i = 0; i < real_conv_masks_len(cout, cin); ++i) out[i] = 0;
   for (int co = 0; co < cout; ++co)
     for (int ci = 0; ci < cin; ++ci)
       for (int t = 0; t < 9; ++t)
         if (wsign[((size_t)co * cin + ci) * 9 + t] > 0)
-          for (int q = 0; q < 4; ++q)
-            out[((size_t)(co / 16) * cin + ci) * 9 + t] |= 1ull << (16 * q + co % 16);
+          out[((size_t)(co / 16) * cp + ci) * 3 + t / 4] |= 1ull << (16 * (t % 4) + co % 16);
 }
 
 // Launchers return hipSuccess or the first launch error.  mt = micro-tile

@@ -20,6 +20,8 @@
 // reference's multiply-then-add.  Out-of-image taps read zeros and sum to
 // +0; skipping a tap and adding that +0 are the same, since s and acc never
 // hold -0.
+#include <utility>
+
 #include "bnn_kernels.h"
 
 namespace bnn {
@@ -214,28 +216,46 @@ __global__ __launch_bounds__(RLANES * RG) void k_real_conv(const RealArgs a, uin
 // real-input conv on the matrix cores
 // ------------------------------------------------------------------------
 // v_mfma_f32_16x16x1_4b_f32 computes, for 4 blocks b, D_b[i][j] =
-// fma(A_b[i], B_b[j], C_b[i][j]), each element rounded once to nearest
-// even: with K = 1 an element is exactly one step s = fma(x, w, s) of the
+// fma(A[i], B_b[j], C_b[i][j]), each element rounded once to nearest even:
+// with K = 1 an element is exactly one step s = fma(x, w, s) of the
 // reference's per-tap chain (the device matches fmaf bit for bit, signed
 // zeros and denormals included).  Rows i are 16 output channels, columns j
 // 16 pixels of an output row, blocks 4 consecutive rows, so a wave owns a
 // 4 x 16 pixel tile and keeps one 16-register accumulator block per tap.
-// Operand A is the +-1 weight of the lane's channel, selected by a
-// per-(ci, tap) lane mask; operand B is the input value the lane's pixel
-// sees through the tap, read from the LDS tile.  Lane layout: A lane l ->
-// block l/16, row l%16; B lane l -> block l/16, column l%16; D register r
-// of lane l -> block r/4, row 4*(l/16) + r%4, column l%16.
+// Operand B is the input value the lane's pixel sees through the tap, read
+// from the LDS tile.  Operand A is the +-1 weight of row i: with CBSZ = 2 the
+// A values of block ABID feed all four blocks, so one register holds the
+// weights of four taps (lanes 16k..16k+15 = tap 4q+k), made from a lane mask
+// by one v_cndmask.  Lane layout: B lane l -> block l/16, column l%16;
+// D register r of lane l -> block r/4, row 4*(l/16) + r%4, column l%16.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// the nine taps of one input channel: tap t takes A from block t%4 of
+// register wa[t/4] (the broadcast fields must be literal constants)
+template <int T>
+__device__ __forceinline__ void mfma_tap(f32x16 (&acc)[9], const float (&wa)[3], const float (&xb)[9]) {
+  acc[T] = __builtin_amdgcn_mfma_f32_16x16x1f32(wa[T >> 2], xb[T], acc[T], 2, T & 3, 0);
+}
+template <int... T>
+__device__ __forceinline__ void mfma_taps(f32x16 (&acc)[9], const float (&wa)[3], const float (&xb)[9],
+                                          std::integer_sequence<int, T...>) {
+  (mfma_tap<T>(acc, wa, xb), ...);
+}
+
+#ifndef BNN_MWPE
+#define BNN_MWPE 2
+#endif
 template <int WR, int WC>  // waves along rows / columns: tile (4*WR) x (16*WC)
-__global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH,
-                                                            int tilesW) {
+__global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(BNN_MWPE)))
+void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   constexpr int TR = 4 * WR, TC = 16 * WC, NT = 64 * WR * WC;
-  constexpr int CI = 8;  // input channels per LDS chunk
-  constexpr int LR = TR + 2, LC = TC + 2, LPL = LR * LC, LTILE = CI * LPL;
-  constexpr int KL = (LTILE + NT - 1) / NT;
-  __shared__ float tile[2][LTILE];  // [ci][row][col], zero outside the image
-  __shared__ uint32_t obits[TR * TC];
+  constexpr int CI = kRealMfmaCI;  // input channels per LDS chunk
+  // LDS rows are padded to LC = 16 (mod 32) floats: the four 16-lane rows of
+  // a wave's B read then fall in disjoint banks
+  constexpr int LR = TR + 2, LW = TC + 2, LC = (LW + 15) / 32 * 32 + 16, LPL = LR * LC;
+  constexpr int LE = CI * LR * LW;  // tile elements loaded per chunk
+  constexpr int KL = (LE + NT - 1) / NT;
+  __shared__ float tile[2][CI * LPL];  // [ci][row][col], zero outside the image
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = (wv / WC) * 4, wc = (wv % WC) * 16;
@@ -247,24 +267,47 @@ __global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, ui
   const int y0 = ty * TR, x0 = tx * TC;
   const int g = blockIdx.y;  // 16-channel group
   const int HW = a.H * a.W;
-  for (int i = tid; i < TR * TC; i += NT) obits[i] = 0;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
+  // the lane's four output channels (16g + 4*(lane/16) + k) and their alpha
+  // and fold parameters, fetched now so the epilogue does not wait on them
+  // (the parameter arrays are padded to 32 channels)
+  const int cq = g * 16 + 4 * (lane >> 4);
+  float p_al[4], p_A[4], p_B[4], p_sl[4], p_rs[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    p_al[k] = a.alpha[cq + k];
+    if (a.out) {
+      p_A[k] = a.A[cq + k];
+      p_B[k] = a.B[cq + k];
+      p_sl[k] = a.slope[cq + k];
+      p_rs[k] = a.rsign[cq + k];
+    }
+  }
 
-  // this thread's share of every chunk: tile element e = tid + k*NT (the
-  // tile is stored in e order) and its byte offset in the chunk, or an
-  // offset past the buffer (reads 0) outside the image
+  // this thread's share of every chunk: tile element e = tid + k*NT, its
+  // byte offset in the chunk (or an offset past the buffer, which reads 0,
+  // outside the image) and its LDS slot.  Channels past cin in the last
+  // chunk also read 0: a product w * 0 adds +-0 to a chain that never holds
+  // -0, which leaves it unchanged, so every chunk runs all CI channels.
   uint32_t goff[KL];
+  int lidx[KL];
 #pragma unroll
   for (int k = 0; k < KL; ++k) {
     const int e = tid + k * NT;
-    const int cil = e / LPL, rem = e - cil * LPL;
-    const int row = rem / LC, col = rem - row * LC;
+    const int cil = e / (LR * LW), rem = e - cil * (LR * LW);
+    const int row = rem / LW, col = rem - row * LW;
     const int gy = y0 - 1 + row, gx = x0 - 1 + col;
-    const bool ok = e < LTILE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+    const bool ok = e < LE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
     goff[k] = ok ? (uint32_t)(((size_t)n * a.cin + cil) * HW + (size_t)gy * a.W + gx) * 4u : 0x80000000u;
+    lidx[k] = e < LE ? cil * LPL + row * LC + col : 0;
   }
   const uint32_t chunk_bytes = (uint32_t)CI * (uint32_t)HW * 4u;
   const int nchunk = (a.cin + CI - 1) / CI;
+  // byte offset of element k in chunk ch, 0x80000000 for a channel past cin
+  auto chunk_off = [&](int k, int ch) -> uint32_t {
+    const int cil = (tid + k * NT) / (LR * LW);
+    return ch * CI + cil < a.cin ? goff[k] + (uint32_t)ch * chunk_bytes : 0x80000000u;
+  };
 
   f32x16 acc[9];
 #pragma unroll
@@ -274,13 +317,13 @@ __global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, ui
 
   float pre[KL];
 #pragma unroll
-  for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], 0);
+  for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, chunk_off(k, 0), 0);
 #pragma unroll
   for (int k = 0; k < KL; ++k)
-    if (tid + k * NT < LTILE) tile[0][tid + k * NT] = pre[k];
+    if (tid + k * NT < LE) tile[0][lidx[k]] = pre[k];
   __syncthreads();
 
-  const uint64_t* wm = a.wm + (size_t)g * a.cin * 9;
+  const uint64_t* wm = a.wm + (size_t)g * nchunk * CI * 3;
   const int lb = (wr + (lane >> 4)) * LC + wc + (lane & 15);
 #pragma unroll 1
   for (int ch = 0; ch < nchunk; ++ch) {
@@ -288,29 +331,38 @@ __global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, ui
     const bool more = ch + 1 < nchunk;
     if (more) {
 #pragma unroll
-      for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, goff[k], (uint32_t)(ch + 1) * chunk_bytes);
+      for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, chunk_off(k, ch + 1), 0);
     }
     const int ci0 = ch * CI;
-    const int nci = a.cin - ci0 < CI ? a.cin - ci0 : CI;
     const float* tb = tile[buf] + lb;
+    // the chunk's weight masks arrive in one scalar batch; channel cl+1's
+    // inputs are read while channel cl's nine products run (the scheduling
+    // barriers keep the compiler from moving the reads next to their use)
+    uint64_t mk[CI][3];
+#pragma unroll
+    for (int cl = 0; cl < CI; ++cl)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) mk[cl][q] = wm[(size_t)(ci0 + cl) * 3 + q];
+    float xb[2][9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) xb[0][t] = tb[(t / 3) * LC + t % 3];
 #pragma unroll
     for (int cl = 0; cl < CI; ++cl) {
-      if (cl < nci) {
-        float xb[9];
+      float wa[3];
 #pragma unroll
-        for (int t = 0; t < 9; ++t) xb[t] = tb[cl * LPL + (t / 3) * LC + t % 3];
-        const uint64_t* m = wm + (size_t)(ci0 + cl) * 9;
+      for (int q = 0; q < 3; ++q) wa[q] = __builtin_amdgcn_inverse_ballot_w64(mk[cl][q]) ? 1.0f : -1.0f;
+      if (cl + 1 < CI) {
 #pragma unroll
-        for (int t = 0; t < 9; ++t) {
-          const float w = __builtin_amdgcn_inverse_ballot_w64(m[t]) ? 1.0f : -1.0f;
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x1f32(w, xb[t], acc[t], 0, 0, 0);
-        }
+        for (int t = 0; t < 9; ++t) xb[(cl + 1) & 1][t] = tb[(cl + 1) * LPL + (t / 3) * LC + t % 3];
       }
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_taps(acc, wa, xb[cl & 1], std::make_integer_sequence<int, 9>{});
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more) {
 #pragma unroll
       for (int k = 0; k < KL; ++k)
-        if (tid + k * NT < LTILE) tile[buf ^ 1][tid + k * NT] = pre[k];
+        if (tid + k * NT < LE) tile[buf ^ 1][lidx[k]] = pre[k];
     }
     __syncthreads();
   }
@@ -318,39 +370,49 @@ __global__ __launch_bounds__(64 * WR * WC) void k_real_mfma(const RealArgs a, ui
   // taps in row-major order into acc (an out-of-image tap summed zeros to
   // +0 and leaves it unchanged), alpha, then the real fold
   // (csrc/bnn_fold.c:62-77): z = fma(A, x, B); z<0 -> slope*z; r = z + rsign;
-  // bit = r > 0.  The reference build fuses A*x+B only.
+  // bit = r > 0.  The reference build fuses A*x+B only.  Register r of lane
+  // l is pixel row r/4, channel 4*(l/16) + r%4: each lane builds the nibble
+  // of its four channels for each of its four pixels, and two xor shuffles
+  // gather the 16-bit words of all four pixels in every lane of a column.
   const int xo = x0 + wc + (lane & 15);
+  uint32_t w01 = 0, w23 = 0;  // pixel rows 0,1 / 2,3: 16 bits each
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     float v = 0.0f;
 #pragma unroll
     for (int t = 0; t < 9; ++t) v = __fadd_rn(v, acc[t][r]);
-    const int yl = wr + (r >> 2);
-    const int y = y0 + yl;
-    const int co = g * 16 + 4 * (lane >> 4) + (r & 3);
-    if (y >= a.H || xo >= a.W || co >= a.cout) continue;
-    const float o = __fmul_rn(a.alpha[co], v);
-    if (a.f32) a.f32[((size_t)n * a.cout + co) * HW + (size_t)y * a.W + xo] = o;
+    const int k = r & 3, b = r >> 2;
+    const int y = y0 + wr + b;
+    const int co = cq + k;
+    const float o = __fmul_rn(p_al[k], v);
+    if (a.f32 && y < a.H && xo < a.W && co < a.cout)
+      a.f32[((size_t)n * a.cout + co) * HW + (size_t)y * a.W + xo] = o;
     if (a.out) {
-      float z = __fmaf_rn(a.A[co], o, a.B[co]);
-      if (z < 0.0f) z = __fmul_rn(a.slope[co], z);
-      const float rr = __fadd_rn(z, a.rsign[co]);
-      if (rr > 0.0f) atomicOr(&obits[yl * TC + wc + (lane & 15)], 1u << (co & 31));
+      float z = __fmaf_rn(p_A[k], o, p_B[k]);
+      if (z < 0.0f) z = __fmul_rn(p_sl[k], z);
+      const float rr = __fadd_rn(z, p_rs[k]);
+      const uint32_t bit = (rr > 0.0f && co < a.cout) ? 1u : 0u;
+      const int sh = 16 * (b & 1) + 4 * (lane >> 4) + k;
+      if (b < 2) w01 |= bit << sh;
+      else w23 |= bit << sh;
     }
   }
   if (!a.out) return;
-  // group g owns bits [16g, 16g+16) of each pixel: a 16-bit store, or the
-  // whole word (upper half 0) when it is the last group and starts a word
-  __syncthreads();
+  w01 |= (uint32_t)__shfl_xor((int)w01, 16);
+  w01 |= (uint32_t)__shfl_xor((int)w01, 32);
+  w23 |= (uint32_t)__shfl_xor((int)w23, 16);
+  w23 |= (uint32_t)__shfl_xor((int)w23, 32);
+  // lane group q stores pixel row q of its column.  Group g owns bits
+  // [16g, 16g+16) of the pixel: a 16-bit store, or the whole word (upper
+  // half 0) when it is the last group and starts a word.
+  const int q = lane >> 4;
+  const uint32_t word = ((q < 2 ? w01 : w23) >> (16 * (q & 1))) & 0xFFFFu;
+  const int y = y0 + wr + q;
+  if (y >= a.H || xo >= a.W) return;
   const int cwo = (a.cout + 31) >> 5;
-  const bool whole = (g & 1) == 0 && g == (int)gridDim.y - 1;
-  for (int i = tid; i < TR * TC; i += NT) {
-    const int y = y0 + i / TC, x = x0 + i % TC;
-    if (y >= a.H || x >= a.W) continue;
-    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)y * a.W + x) * cwo) + g * 2;
-    if (whole) *reinterpret_cast<uint32_t*>(dst) = obits[i];
-    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(obits[i] >> ((g & 1) * 16));
-  }
+  uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)y * a.W + xo) * cwo) + g * 2;
+  if ((g & 1) == 0 && g == (int)gridDim.y - 1) *reinterpret_cast<uint32_t*>(dst) = word;
+  else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
 }
 
 // ------------------------------------------------------------------------
@@ -855,7 +917,7 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
 }
 
 #ifndef BNN_MWR
-#define BNN_MWR 4
+#define BNN_MWR 2
 #endif
 #ifndef BNN_MWC
 #define BNN_MWC 2
