@@ -15,6 +15,8 @@ timed between device synchronisations.  Prints ONE JSON line on stdout:
                 counted) against the VALU-popcount roofline
   fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
                 32x32, batch 1024 (the benchmark's fused-kernel config)
+  scene         benchmark config 3: a 956x684x120 scene by 32x32 patches,
+                device-resident and from host memory (PCIe included)
   cpu_baseline  the reference C CLI (oracle/_ref/bnn_infer, built from the
                 reference sources) timed on this host: median of reps of one
                 patch, like csrc/main.c:55-61; falls back to the checker
@@ -58,7 +60,7 @@ def measured_traffic():
         txt = open(p).read()
     except OSError:
         return None
-    m = re.search(r"`k_real_\w+`[^\n]*?moves ([\d.]+) MB in and ([\d.]+) MB out", txt)
+    m = re.search(r"`k_real_[^`]*`[^\n]*?moves ([\d.]+) MB in and ([\d.]+) MB out", txt)
     return round((float(m.group(1)) + float(m.group(2))) * 1e6) if m else None
 
 
@@ -213,6 +215,38 @@ def main() -> int:
         f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
     L.close()
 
+    # benchmark config 3: a 956 x 684 x 120 scene (N(0,1) plus a per-band
+    # offset U(-0.5, 0.5)) cut into 32 x 32 patches, 30 x 22 = 660 with the
+    # edge patches zero past the scene; the device call reads the patches
+    # straight out of the cube, the host call adds the strip-wise PCIe copy
+    SH, SW, PS = 956, 684, 32
+    rng = np.random.default_rng(40)
+    cube = rng.standard_normal((b.n_bands, SH, SW), dtype=np.float32)
+    cube += rng.uniform(-0.5, 0.5, (b.n_bands, 1, 1)).astype(np.float32)
+    npatch = ((SH + PS - 1) // PS) * ((SW + PS - 1) // PS)
+    d_cube = torch.from_numpy(cube).cuda()
+    d_map = torch.empty((b.n_classes, SH, SW), dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
+    torch.cuda.synchronize()
+    reps = 10
+    e0.record(stream)
+    for _ in range(reps):
+        eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    scene_dev_ms = e0.elapsed_time(e1) / reps
+    host_map = eng.forward_patched(cube, PS)
+    assert np.array_equal(host_map.view(np.uint32), d_map.cpu().numpy().view(np.uint32))
+    t0 = time.perf_counter()
+    for _ in range(3):
+        eng.forward_patched(cube, PS)
+    scene_host_ms = (time.perf_counter() - t0) / 3 * 1e3
+    log(f"scene {SH}x{SW}x{b.n_bands} ({npatch} patches): device {scene_dev_ms:.3f} ms "
+        f"({npatch / scene_dev_ms * 1e3:,.0f} patches/s), host pointers {scene_host_ms:.2f} ms "
+        f"({cube.nbytes / scene_host_ms / 1e6:.1f} GB/s of input)")
+    del d_cube, d_map
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -247,6 +281,11 @@ def main() -> int:
         "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
                        "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
                        "frac": round(pool_rate / valu_binop_peak(), 4)},
+        "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
+                            "past the scene), benchmark config 3",
+                  "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
+                  "host_ms": round(scene_host_ms, 3),
+                  "host_note": "host cube in, host map out: strips through pinned buffers over PCIe"},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "bnn_kernels.h"
@@ -327,6 +328,11 @@ struct BnnDevice {
   size_t stage_in_cap = 0;
   float* stage_out = nullptr;
   size_t stage_out_cap = 0;
+  // scene pipeline: pinned host strips, their copy stream and events
+  float* pin[2] = {};
+  size_t pin_cap = 0;
+  hipStream_t copy = nullptr;
+  hipEvent_t ev_copied[2] = {}, ev_free[2] = {};
 };
 
 struct BnnConvLayer {
@@ -409,6 +415,13 @@ void release(BnnDevice* D) {
   if (D->ws.base) hipFree(D->ws.base);
   if (D->stage_in) hipFree(D->stage_in);
   if (D->stage_out) hipFree(D->stage_out);
+  if (D->copy) hipStreamSynchronize(D->copy);
+  for (int k = 0; k < 2; ++k) {
+    if (D->pin[k]) hipHostFree(D->pin[k]);
+    if (D->ev_copied[k]) hipEventDestroy(D->ev_copied[k]);
+    if (D->ev_free[k]) hipEventDestroy(D->ev_free[k]);
+  }
+  if (D->copy) hipStreamDestroy(D->copy);
   if (D->stream) hipStreamDestroy(D->stream);
   D->stream = nullptr;
 }
@@ -508,6 +521,13 @@ struct Dumps {
   int32_t* P2[4] = {};
 };
 
+// Scene mode: the input is one cube [n_bands][sH][sW] cut into patches,
+// pcols per row starting at patch row prow0; logits go to the map
+// [n_classes][sH][sW]
+struct Scene {
+  int sH, sW, pcols, prow0;
+};
+
 struct Op {
   const char* label;
   const char* optype;
@@ -519,7 +539,7 @@ struct Op {
 // kernel.
 int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_in, int N, int H, int W,
                     float* d_logits, hipStream_t s, Dumps* dmp, std::vector<Op>* ops,
-                    std::vector<hipEvent_t>* evs) {
+                    std::vector<hipEvent_t>* evs, const Scene* sc = nullptr) {
   int hs[5], wsz[5];
   level_dims(H, W, hs, wsz);
   auto mark = [&](const char* label, const char* optype, double oe, double taps) -> int {
@@ -546,6 +566,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
     ra.out = w.a1;
     ra.f32 = dump ? dmp->conv1 : nullptr;
+    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
     HIP_TRY(launch_real(ra, s));
     if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
   }
@@ -566,6 +587,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     a.wt = L.wt; a.f1 = L.f1; a.f2 = L.f2;
     a.out = out; a.out2 = out2; a.cwo = words(L.cout);
     a.logits = logits; a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
+    if (sc && epi == EPI_HEAD) { a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0; }
     if (dump) {
       a.P = dmp->P[pi++];
       if (epi == EPI_POOL) a.P2 = dmp->P2[lvl];
@@ -643,6 +665,112 @@ int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_
   }
   for (hipEvent_t e : evs) hipEventDestroy(e);
   return rc;
+}
+
+int grow(float** p, size_t* cap, size_t bytes);
+
+// ------------------------------------------------------------ scenes
+// Patch-wise scene inference with the tiling of
+// csrc/bnn_model_react.c:454-476: P x P patches start at multiples of P, an
+// edge patch is zero past the scene, every patch runs as its own image and
+// its logits inside the scene go to the map.  The real conv reads the
+// patches straight out of the cube and the head writes the map, so no
+// patch is ever copied.
+int check_scene(const Model* m, int H, int W, int P) {
+  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+  if (P < 16 || P % 16) return set_err(BNN_EARG, "patch size %d: must be a positive multiple of 16 (four 2x2 pools)", P);
+  if (H < 1 || W < 1) return set_err(BNN_EARG, "scene %dx%d is empty", H, W);
+  if ((size_t)m->n_bands * H * W * 4 >= 0x80000000ull)
+    return set_err(BNN_EARG, "scene too large for one launch (%zu cube bytes >= 2 GiB)",
+                   (size_t)m->n_bands * H * W * 4);
+  return BNN_OK;
+}
+
+// patch rows [prow0, prow0 + nrows) of the scene
+int run_scene_rows(const Model* m, const float* d_cube, int H, int W, float* d_map, int P, int prow0, int nrows,
+                   hipStream_t s) {
+  const int pcols = (W + P - 1) / P;
+  const int N = nrows * pcols;
+  if (N <= 0) return BNN_OK;
+  BnnDevice* D = m->dev;
+  int rc;
+  if ((rc = ensure_ws(m, D, D->ws, N, P, P))) return rc;
+  const Scene sc{H, W, pcols, prow0};
+  if (!g_prof_on) return enqueue_forward(m, D, D->ws, d_cube, N, P, P, d_map, s, nullptr, nullptr, nullptr, &sc);
+  std::vector<Op> ops;
+  std::vector<hipEvent_t> evs;
+  rc = enqueue_forward(m, D, D->ws, d_cube, N, P, P, d_map, s, nullptr, &ops, &evs, &sc);
+  if (!rc && !evs.empty()) {
+    HIP_TRY(hipEventSynchronize(evs.back()));
+    for (size_t i = 0; i + 1 < evs.size() && i < ops.size(); ++i) {
+      float ms = 0;
+      HIP_TRY(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
+      prof_add(ops[i].label, ops[i].optype, ops[i].oe, ops[i].taps, ms * 1e-3);
+    }
+  }
+  for (hipEvent_t e : evs) hipEventDestroy(e);
+  return rc;
+}
+
+// Host cube -> host map.  The cube goes to the device in strips of whole
+// patch rows through two pinned buffers: host threads fill one buffer while
+// the copy stream moves the other and the model's stream runs the strip
+// before; the map comes back once at the end.
+int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, int P) {
+  int rc;
+  if ((rc = check_scene(m, H, W, P))) return rc;
+  BnnDevice* D = m->dev;
+  const int nb = m->n_bands, ncls = m->n_classes;
+  const int prows = (H + P - 1) / P;
+  // strips of about 32 MB of input
+  const size_t row_bytes = (size_t)nb * P * W * 4;
+  const int R = std::max(1, (int)std::min<size_t>(prows, (32u << 20) / row_bytes));
+  const size_t strip_bytes = row_bytes * R;
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, (size_t)nb * H * W * 4))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, (size_t)ncls * H * W * 4))) return rc;
+  if (D->pin_cap < strip_bytes) {
+    HIP_TRY(hipDeviceSynchronize());
+    for (int k = 0; k < 2; ++k) {
+      if (D->pin[k]) hipHostFree(D->pin[k]);
+      D->pin[k] = nullptr;
+    }
+    D->pin_cap = 0;
+    for (int k = 0; k < 2; ++k) HIP_TRY(hipHostMalloc((void**)&D->pin[k], strip_bytes, hipHostMallocDefault));
+    D->pin_cap = strip_bytes;
+  }
+  if (!D->copy) {
+    HIP_TRY(hipStreamCreateWithFlags(&D->copy, hipStreamNonBlocking));
+    for (int k = 0; k < 2; ++k) {
+      HIP_TRY(hipEventCreateWithFlags(&D->ev_copied[k], hipEventDisableTiming));
+      HIP_TRY(hipEventCreateWithFlags(&D->ev_free[k], hipEventDisableTiming));
+    }
+  }
+  const unsigned nthr = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  for (int k = 0, pr0 = 0; pr0 < prows; ++k, pr0 += R) {
+    const int b = k & 1;
+    const int nr = std::min(R, prows - pr0);
+    const int r0 = pr0 * P, rows = std::min(nr * P, H - r0);
+    if (k >= 2) HIP_TRY(hipEventSynchronize(D->ev_free[b]));  // its copy two strips ago is done
+    // [nb][rows][W] of the strip into the pinned buffer, bands split over threads
+    float* dst = D->pin[b];
+    auto fill = [&](int b0, int b1) {
+      for (int band = b0; band < b1; ++band)
+        memcpy(dst + (size_t)band * rows * W, cube + ((size_t)band * H + r0) * W, (size_t)rows * W * 4);
+    };
+    std::vector<std::thread> th;
+    for (unsigned t = 1; t < nthr; ++t) th.emplace_back(fill, nb * t / nthr, nb * (t + 1) / nthr);
+    fill(0, nb / nthr);
+    for (auto& t : th) t.join();
+    HIP_TRY(hipMemcpy2DAsync(D->stage_in + (size_t)r0 * W, (size_t)H * W * 4, dst, (size_t)rows * W * 4,
+                             (size_t)rows * W * 4, nb, hipMemcpyHostToDevice, D->copy));
+    HIP_TRY(hipEventRecord(D->ev_free[b], D->copy));
+    HIP_TRY(hipEventRecord(D->ev_copied[b], D->copy));
+    HIP_TRY(hipStreamWaitEvent(D->stream, D->ev_copied[b], 0));
+    if ((rc = run_scene_rows(m, D->stage_in, H, W, D->stage_out, P, pr0, nr, D->stream))) return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(map, D->stage_out, (size_t)ncls * H * W * 4, hipMemcpyDeviceToHost, D->stream));
+  HIP_TRY(hipStreamSynchronize(D->stream));
+  return BNN_OK;
 }
 
 int grow(float** p, size_t* cap, size_t bytes) {
@@ -734,6 +862,17 @@ int bnn_forward_device(const Model* m, const float* d_input, int N, int H, int W
 }
 
 void* bnn_stream(const Model* m) { return (m && m->dev) ? (void*)m->dev->stream : nullptr; }
+
+int bnn_forward_patched(const Model* m, const float* input, int H, int W, float* logits, int P) {
+  return run_scene_host(m, input, H, W, logits, P);
+}
+
+int bnn_forward_patched_device(const Model* m, const float* d_input, int H, int W, float* d_logits, int P,
+                               void* stream) {
+  int rc;
+  if ((rc = check_scene(m, H, W, P))) return rc;
+  return run_scene_rows(m, d_input, H, W, d_logits, P, 0, (H + P - 1) / P, (hipStream_t)stream);
+}
 
 int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, float* logits, bnn_stage_cb cb,
                       void* ctx) {

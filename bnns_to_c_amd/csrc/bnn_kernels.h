@@ -65,10 +65,11 @@ struct BconvArgs {
   int cwo;
   int32_t* P;           // EPI_P output, or the P dump of a fused epilogue
   int32_t* P2;          // pooled-P dump (EPI_POOL)
-  float* logits;        // EPI_HEAD
+  float* logits;        // EPI_HEAD: [N][ncls][H][W], or the scene map [ncls][sH][sW]
   const float* hw;      // head W [ncls][cout]
   const float* hb;      // head bias [ncls]
   int ncls;
+  int sH, sW, pcols, prow0;  // scene mode (pcols > 0), as in RealArgs
 };
 
 struct RealArgs {
@@ -83,6 +84,10 @@ struct RealArgs {
   int N, H, W, cin, cout;
   uint32_t* out;        // bits [N][H][W][ceil(cout/32)]; may be null
   float* f32;           // conv output [N][cout][H][W]; may be null
+  // scene mode (pcols > 0): x is one cube [cin][sH][sW] cut into H x W
+  // patches, pcols per row, patch n at row prow0 + n / pcols, column
+  // n % pcols; a patch's rows and columns past the cube read 0
+  int sH, sW, pcols, prow0;
 };
 
 // Real-conv work split: output channels per lane group and output rows per

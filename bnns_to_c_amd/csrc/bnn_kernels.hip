@@ -41,6 +41,33 @@ __device__ __forceinline__ uint32_t ld_u32(__amdgpu_buffer_rsrc_t rs, uint32_t v
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0);
 }
 
+// Where the real conv finds patch n: in a batch [N][cin][H][W], or in one
+// scene cube [cin][sH][sW] cut into H x W patches (pcols per row), where the
+// rows and columns of an edge patch past the cube count as outside (0).
+struct InGeom {
+  size_t base, cstride;  // element offsets: patch origin, one channel
+  int rstride;           // one row
+  int ylim, xlim;        // rows / columns of the patch inside the input
+};
+__device__ __forceinline__ InGeom in_geom(const RealArgs& a, int n) {
+  InGeom g;
+  if (a.pcols > 0) {
+    const int pr = a.prow0 + n / a.pcols, pc = n % a.pcols;
+    g.base = (size_t)pr * a.H * a.sW + (size_t)pc * a.W;
+    g.cstride = (size_t)a.sH * a.sW;
+    g.rstride = a.sW;
+    g.ylim = min(a.H, a.sH - pr * a.H);
+    g.xlim = min(a.W, a.sW - pc * a.W);
+  } else {
+    g.base = (size_t)n * a.cin * a.H * a.W;
+    g.cstride = (size_t)a.H * a.W;
+    g.rstride = a.W;
+    g.ylim = a.H;
+    g.xlim = a.W;
+  }
+  return g;
+}
+
 // ------------------------------------------------------------------------
 // real-input conv + real fold
 // ------------------------------------------------------------------------
@@ -91,6 +118,7 @@ __global__ __launch_bounds__(RLANES * RG) void k_real_conv(const RealArgs a, uin
   // or an offset past the buffer (reads 0) for positions outside the image,
   // and where it goes in the [row][ci][col] tile (all CI channels and 3
   // columns of a tile row lie within one ds_read2 offset range)
+  const InGeom ig = in_geom(a, n);
   uint32_t goff[KL];
   int lidx[KL];
 #pragma unroll
@@ -100,10 +128,10 @@ __global__ __launch_bounds__(RLANES * RG) void k_real_conv(const RealArgs a, uin
     const int row = rem / LC, col = rem - row * LC;
     lidx[k] = e < LTILE ? (row * CI + cil) * LC + col : 0;
     const int gy = y0 - 1 + row, gx = x0 - 1 + col;
-    const bool ok = e < LTILE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
-    goff[k] = ok ? (uint32_t)(((size_t)n * a.cin + cil) * HW + (size_t)gy * a.W + gx) * 4u : 0x80000000u;
+    const bool ok = e < LTILE && gy >= 0 && gy < ig.ylim && gx >= 0 && gx < ig.xlim;
+    goff[k] = ok ? (uint32_t)(ig.base + cil * ig.cstride + (size_t)gy * ig.rstride + gx) * 4u : 0x80000000u;
   }
-  const uint32_t chunk_bytes = (uint32_t)CI * (uint32_t)HW * 4u;
+  const uint32_t chunk_bytes = (uint32_t)(CI * ig.cstride * 4u);
   const int nchunk = (a.cin + CI - 1) / CI;
 
   float st[PXR][9][RCO];
@@ -289,6 +317,7 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   // outside the image) and its LDS slot.  Channels past cin in the last
   // chunk also read 0: a product w * 0 adds +-0 to a chain that never holds
   // -0, which leaves it unchanged, so every chunk runs all CI channels.
+  const InGeom ig = in_geom(a, n);
   uint32_t goff[KL];
   int lidx[KL];
 #pragma unroll
@@ -297,11 +326,11 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
     const int cil = e / (LR * LW), rem = e - cil * (LR * LW);
     const int row = rem / LW, col = rem - row * LW;
     const int gy = y0 - 1 + row, gx = x0 - 1 + col;
-    const bool ok = e < LE && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
-    goff[k] = ok ? (uint32_t)(((size_t)n * a.cin + cil) * HW + (size_t)gy * a.W + gx) * 4u : 0x80000000u;
+    const bool ok = e < LE && gy >= 0 && gy < ig.ylim && gx >= 0 && gx < ig.xlim;
+    goff[k] = ok ? (uint32_t)(ig.base + cil * ig.cstride + (size_t)gy * ig.rstride + gx) * 4u : 0x80000000u;
     lidx[k] = e < LE ? cil * LPL + row * LC + col : 0;
   }
-  const uint32_t chunk_bytes = (uint32_t)CI * (uint32_t)HW * 4u;
+  const uint32_t chunk_bytes = (uint32_t)(CI * ig.cstride * 4u);
   const int nchunk = (a.cin + CI - 1) / CI;
   // byte offset of element k in chunk ch, 0x80000000 for a channel past cin
   auto chunk_off = [&](int k, int ch) -> uint32_t {
@@ -691,13 +720,25 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
     }
     if (a.out) store_bits<COG>(a.out, ((size_t)n * a.H + y0) * a.W + x0, a.cwo, co0, a.cout, bits[0], zero_end);
     const int pix = y0 * a.W + x0;
+    // batch: logits [N][ncls][H][W]; scene: the map [ncls][sH][sW], pixels
+    // of an edge patch past the scene dropped
+    size_t lbase = (size_t)n * a.ncls * HW + pix, lstride = HW;
+    bool keep = true;
+    if (a.pcols > 0) {
+      const int pr = a.prow0 + (int)n / a.pcols, pc = (int)n % a.pcols;
+      const int sy = pr * a.H + y0, sx = pc * a.W + x0;
+      keep = sy < a.sH && sx < a.sW;
+      lbase = (size_t)sy * a.sW + sx;
+      lstride = (size_t)a.sH * a.sW;
+    }
+    if (!keep) return;
 #pragma unroll 1
     for (int o = 0; o < a.ncls; ++o) {
       float accf = a.hb[o];
 #pragma unroll
       for (int j = 0; j < COG; ++j)
         if (j < a.cout) accf = __fmaf_rn(a.hw[o * a.cout + j], sg[j], accf);
-      a.logits[((size_t)n * a.ncls + o) * HW + pix] = accf;
+      a.logits[lbase + (size_t)o * lstride] = accf;
     }
   }
 }
@@ -925,7 +966,7 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
 
 hipError_t launch_real(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
-  const size_t xbytes = (size_t)a.N * a.cin * a.H * a.W * 4;
+  const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
   if (a.wm) {
     constexpr int WR = BNN_MWR, WC = BNN_MWC;

@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
     L.bnn_forward_batch.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32]
     L.bnn_forward_device.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
     L.bnn_forward_debug.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32, STAGE_CB, _vp]
+    L.bnn_forward_patched.argtypes = [_vp, _f32, _ci, _ci, _f32, _ci]
+    L.bnn_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
     L.bnn_stream.argtypes = [_vp]
     L.bnn_stream.restype = _vp
     L.bnn_prof_enable.argtypes = [_ci]
@@ -162,6 +164,20 @@ class Engine:
                        stream: Optional[int] = None) -> None:
         _check(lib().bnn_forward_device(self.h, _vp(d_in), N, H, W, _vp(d_out),
                                         _vp(stream or None)))
+
+    def forward_patched(self, cube: np.ndarray, P: int = 32) -> np.ndarray:
+        """Scene [n_bands, H, W] -> logit map [n_classes, H, W] by independent
+        P x P patches, edge patches zero past the scene (bnn_forward_patched)."""
+        cube = np.ascontiguousarray(cube, np.float32)
+        nb, H, W = cube.shape
+        out = np.empty((self.n_classes, H, W), np.float32)
+        _check(lib().bnn_forward_patched(self.h, _p(cube, _f32), H, W, _p(out, _f32), P))
+        return out
+
+    def forward_patched_device(self, d_cube: int, H: int, W: int, d_map: int, P: int = 32,
+                               stream: Optional[int] = None) -> None:
+        _check(lib().bnn_forward_patched_device(self.h, _vp(d_cube), H, W, _vp(d_map), P,
+                                                _vp(stream or None)))
 
     def stream(self) -> int:
         return lib().bnn_stream(self.h)

@@ -102,6 +102,18 @@ int bnn_forward_device(const Model *m, const float *d_input, int N, int H, int W
                        float *d_logits, void *stream);
 void *bnn_stream(const Model *m);      /* the model's own hipStream_t (used by the host-pointer calls) */
 
+/* Scene inference by independent P x P patches, the tiling of the reference's
+ * csrc/bnn_model_react.c:454-476 (bnn_forward_react_patched) applied to the v1
+ * forward: patches start at multiples of P (a multiple of 16), an edge patch
+ * is zero past the scene, each patch runs as its own P x P image and its
+ * logits inside the scene are written to the map.
+ * input [n_bands][H][W], logits [n_classes][H][W]; the cube must be < 2 GiB.
+ * Host pointers: the cube crosses PCIe in strips, overlapped with compute. */
+int bnn_forward_patched(const Model *m, const float *input, int H, int W, float *logits, int P);
+/* same on device pointers, enqueued on `stream` (NULL = HIP default stream) */
+int bnn_forward_patched_device(const Model *m, const float *d_input, int H, int W, float *d_logits, int P,
+                               void *stream);
+
 /* Debug forward: host pointers, then every stage of the chain is handed to
  * `cb` as a host array [N][c][h][w] (dtype 0 int8 +-1, 1 int32 P, 2 float),
  * named as in the reference forward: enc1.conv1, enc1.act1, encK.conv1.P,
