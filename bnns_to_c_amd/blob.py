@@ -24,6 +24,7 @@ import numpy as np
 
 MAGIC = b"BNNC"
 VERSION = 1
+VERSION_STEM = 2            # spectral-stem blobs (python/bnn2c/blob.py:229-230)
 UPSAMPLER_NEAREST = 0
 
 TAG_CONV_BIN = 1
@@ -138,6 +139,15 @@ class BlobV1:
     dec_conv2: List[Conv] = field(default_factory=list)
     dec_act2: List[Act] = field(default_factory=list)
     head: Optional[Head] = None
+    # v2 (spectral stem, python/bnn2c/blob.py:203-245): version 2, a <7i>
+    # header with has_stem = n_stem_layers = 1, the stem records after it,
+    # and a binary enc1.conv1 with an integer enc1.act1
+    stem_conv: Optional[Conv] = None
+    stem_act: Optional[Act] = None
+
+    @property
+    def has_stem(self) -> bool:
+        return self.version == VERSION_STEM
 
 
 # ----------------------------------------------------------------- writer --
@@ -170,11 +180,17 @@ def _w_act(f, a: Act) -> None:
 
 
 def to_bytes(b: BlobV1) -> bytes:
-    """Serialise in the v1 record order (python/bnn2c/blob.py:181-199)."""
+    """Serialise in the record order of python/bnn2c/blob.py:181-199 (v1) or
+    :226-245 (v2: the stem records right after the header)."""
     f = io.BytesIO()
     f.write(MAGIC)
-    f.write(struct.pack("<5i", b.version, b.base_channels, b.n_bands,
-                        b.n_classes, b.upsampler))
+    if b.has_stem:
+        f.write(struct.pack("<7i", b.version, b.base_channels, b.n_bands,
+                            b.n_classes, b.upsampler, 1, 1))
+        _w_conv(f, b.stem_conv); _w_act(f, b.stem_act)
+    else:
+        f.write(struct.pack("<5i", b.version, b.base_channels, b.n_bands,
+                            b.n_classes, b.upsampler))
     for i in range(4):
         _w_conv(f, b.enc_conv1[i]); _w_act(f, b.enc_act1[i])
         _w_conv(f, b.enc_conv2[i]); _w_act(f, b.enc_act2_skip[i])
@@ -250,18 +266,23 @@ def _r_act(r: _Rd) -> Act:
 
 
 def from_bytes(data: bytes, strict: bool = True) -> BlobV1:
-    """Parse a v1 blob.  strict=True also rejects version != 1 and
-    upsampler != 0 (the nearest-upsampler engine is the only v1 engine)."""
+    """Parse a v1 or v2 blob.  strict=True also rejects other versions and
+    upsampler != 0 (the nearest-upsampler engines are the only ones)."""
     r = _Rd(data)
     if bytes(r.take(4)) != MAGIC:
         raise BlobError("bad magic")
     version, base, nb, nc, ups = r.ints(5)
-    if strict and version != VERSION:
+    if strict and version not in (VERSION, VERSION_STEM):
         raise BlobError(f"unsupported blob version {version}")
     if strict and ups != UPSAMPLER_NEAREST:
         raise BlobError(f"unsupported upsampler {ups}")
     b = BlobV1(base_channels=base, n_bands=nb, n_classes=nc, upsampler=ups,
                version=version)
+    if version == VERSION_STEM:
+        has_stem, n_stem = r.ints(2)
+        if (has_stem, n_stem) != (1, 1):
+            raise BlobError("only has_stem=1, n_stem_layers=1 supported")
+        b.stem_conv = _r_conv(r); b.stem_act = _r_act(r)
     for _ in range(4):
         b.enc_conv1.append(_r_conv(r)); b.enc_act1.append(_r_act(r))
         b.enc_conv2.append(_r_conv(r)); b.enc_act2_skip.append(_r_act(r))

@@ -19,6 +19,8 @@ every fixture: real first-conv weights w ~ N(0, 1/sqrt(fan_in)) giving
 wsign = sign(w) (0 -> +1) and alpha = mean|w|; real fold A ~ U(0.5, 1.5),
 B ~ N(0, 0.1), slope ~ U(-0.5, 0.5), rsign ~ N(0, 0.1); head bias ~ N(0, 0.05).
 
+`make_blob_v2` builds the spectral-stem variant (blob version 2).
+
 `coverage=True` draws every integer rule type (const, ge, lt, band_in,
 band_out and an unknown code, which the C fold maps to -1;
 csrc/bnn_fold.c:49-56) so the fold paths the recipe never reaches are
@@ -55,12 +57,13 @@ def _bin_conv(rng, cin, cout):
     return B.Conv(B.TAG_CONV_BIN, cout, cin, 3, 3, 1, 1, packed=B.pack_kidx(wsign))
 
 
-def _real_conv(rng, cin, cout):
-    fan_in = cin * 9
-    w = rng.normal(0.0, 1.0 / np.sqrt(fan_in), (cout, cin, 3, 3)).astype(np.float32)
+def _real_conv(rng, cin, cout, k=3):
+    fan_in = cin * k * k
+    w = rng.normal(0.0, 1.0 / np.sqrt(fan_in), (cout, cin, k, k)).astype(np.float32)
     wsign = np.where(w >= 0, 1, -1).astype(np.int8)
     alpha = np.abs(w).mean(axis=(1, 2, 3)).astype(np.float32)
-    return B.Conv(B.TAG_CONV_REAL, cout, cin, 3, 3, 1, 1, wsign=wsign, alpha=alpha)
+    pad = 1 if k == 3 else 0
+    return B.Conv(B.TAG_CONV_REAL, cout, cin, k, k, pad, 1, wsign=wsign, alpha=alpha)
 
 
 def _int_act(rng, c, fan_in, coverage):
@@ -125,6 +128,22 @@ def make_blob(seed: int = 0, base: int = 16, n_bands: int = 120,
     W = rng.normal(0.0, 0.05, (n_classes, base)).astype(np.float32)
     bias = rng.normal(0.0, 0.05, n_classes).astype(np.float32)
     b.head = B.Head(n_classes, base, W, bias)
+    return b
+
+
+def make_blob_v2(seed: int = 0, base: int = 16, n_bands: int = 120, n_classes: int = 3,
+                 stem: int = 16, coverage: bool = False) -> B.BlobV1:
+    """A v2 (spectral-stem) blob: a real-input 1x1 binary-weight stem
+    n_bands -> stem with a real fold, then the v1 body with enc1.conv1 binary
+    (stem -> base) and an integer enc1.act1 (csrc/bnn_model_stem.c:4-9).
+    The stem follows the real first conv's recipe with fan_in = n_bands."""
+    rng = np.random.default_rng(seed)
+    b = make_blob(seed=seed + 7919, base=base, n_bands=n_bands, n_classes=n_classes, coverage=coverage)
+    b.version = B.VERSION_STEM
+    b.stem_conv = _real_conv(rng, n_bands, stem, k=1)
+    b.stem_act = _real_act(rng, stem)
+    b.enc_conv1[0] = _bin_conv(rng, stem, base)
+    b.enc_act1[0] = _int_act(rng, base, stem * 9, coverage)
     return b
 
 

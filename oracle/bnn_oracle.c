@@ -128,6 +128,7 @@ void orc_free(orc_model *m) {
     }
     free_conv(&m->bott_c1); free_conv(&m->bott_c2);
     free_act(&m->bott_a1); free_act(&m->bott_a2);
+    free_conv(&m->stem_c); free_act(&m->stem_a);
     free(m->head_w); free(m->head_b);
     free(m);
 }
@@ -144,8 +145,16 @@ int orc_parse(const uint8_t *buf, size_t len, int strict, orc_model **out,
     m->version = take_i32(&r); m->base = take_i32(&r);
     m->n_bands = take_i32(&r); m->n_classes = take_i32(&r);
     m->upsampler = take_i32(&r);
-    if (!r.bad && strict && m->version != 1) fail(&r, "unsupported blob version %d", m->version);
+    if (!r.bad && strict && m->version != 1 && m->version != 2)
+        fail(&r, "unsupported blob version %d", m->version);
     if (!r.bad && strict && m->upsampler != 0) fail(&r, "unsupported upsampler %d", m->upsampler);
+    if (!r.bad && m->version == 2) {
+        /* <7i> header and the stem records (csrc/bnn_model_stem.c:86-96) */
+        m->has_stem = take_i32(&r); m->n_stem_layers = take_i32(&r);
+        if (!r.bad && (m->has_stem != 1 || m->n_stem_layers != 1))
+            fail(&r, "only has_stem=1, n_stem_layers=1 supported");
+        parse_conv(&r, &m->stem_c); parse_act(&r, &m->stem_a);
+    }
     for (int i = 0; i < 4; ++i) {
         parse_conv(&r, &m->enc_c1[i]); parse_act(&r, &m->enc_a1[i]);
         parse_conv(&r, &m->enc_c2[i]); parse_act(&r, &m->enc_skip[i]);
@@ -476,11 +485,19 @@ static int model_ok(const orc_model *m, int H, int W) {
     if (H < 16 || W < 16) return 0;            /* four 2x2 pools need >= 1 pixel */
     if (m->n_bands <= 0 || m->n_classes <= 0) return 0;
     int c = m->n_bands;
+    const int stem = m->has_stem;
+    if (stem) {
+        const orc_conv *s = &m->stem_c;
+        if (s->tag != TAG_REAL || s->cin != c || s->cout <= 0 || s->kh != 1 || s->kw != 1 ||
+            s->pad != 0 || s->stride != 1 || !act_ok(&m->stem_a, 1, s->cout)) return 0;
+        c = s->cout;
+    }
     int skipc[4];
     for (int i = 0; i < 4; ++i) {
         const orc_conv *c1 = &m->enc_c1[i], *c2 = &m->enc_c2[i];
-        if (!conv_ok(c1, i == 0 ? TAG_REAL : TAG_BIN, c)) return 0;
-        if (!act_ok(&m->enc_a1[i], i == 0, c1->cout)) return 0;
+        const int real = i == 0 && !stem;
+        if (!conv_ok(c1, real ? TAG_REAL : TAG_BIN, c)) return 0;
+        if (!act_ok(&m->enc_a1[i], real, c1->cout)) return 0;
         if (!conv_ok(c2, TAG_BIN, c1->cout)) return 0;
         if (!act_ok(&m->enc_skip[i], 0, c2->cout) || !act_ok(&m->enc_down[i], 0, c2->cout)) return 0;
         skipc[i] = c = c2->cout;
@@ -534,8 +551,19 @@ int orc_forward(const orc_model *m, const float *in, int H, int W, float *logits
     int8_t *x;
     int xC, xH = H, xW = W;
 
-    /* enc1: real conv -> real fold, then conv2 with two consumers */
-    {
+    if (m->has_stem) {
+        /* v2: 1x1 real stem -> real fold (csrc/bnn_model_stem.c:175-190) */
+        const orc_conv *sc = &m->stem_c;
+        float *r = xalloc((size_t)sc->cout * H * W * 4);
+        orc_conv_real(in, sc->wsign, sc->alpha, r, sc->cin, H, W, sc->cout, 1, 1, 0, 1);
+        emit(cb, ctx, "stem.conv", 2, sc->cout, H, W, r);
+        x = xalloc((size_t)sc->cout * H * W);
+        orc_fold_real(r, x, sc->cout, H, W, m->stem_a.A, m->stem_a.B, m->stem_a.slope, m->stem_a.rsign);
+        emit(cb, ctx, "stem.act", 0, sc->cout, H, W, x);
+        free(r);
+        xC = sc->cout;
+    } else {
+        /* v1 enc1: real conv -> real fold, then conv2 with two consumers */
         const orc_conv *c1 = &m->enc_c1[0], *c2 = &m->enc_c2[0];
         float *r = xalloc((size_t)c1->cout * H * W * 4);
         orc_conv_real(in, c1->wsign, c1->alpha, r, c1->cin, H, W, c1->cout, 3, 3, 1, 1);
@@ -550,7 +578,7 @@ int orc_forward(const orc_model *m, const float *in, int H, int W, float *logits
     }
     for (int i = 0; i < 4; ++i) {
         int8_t *h;
-        if (i == 0) {
+        if (i == 0 && !m->has_stem) {
             h = x;
         } else {
             snprintf(nm, sizeof nm, "enc%d.conv1", i + 1);

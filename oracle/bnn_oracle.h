@@ -42,6 +42,11 @@ typedef struct {
 
 typedef struct {
     int version, base, n_bands, n_classes, upsampler;
+    /* v2 (csrc/bnn_model_stem.h:38-56): a real-input 1x1 binary-weight stem
+     * and real fold before a uniformly binary encoder (enc1.conv1 binary) */
+    int has_stem, n_stem_layers;
+    orc_conv stem_c;
+    orc_act stem_a;
     orc_conv enc_c1[4], enc_c2[4];
     orc_act enc_a1[4], enc_skip[4], enc_down[4];
     orc_conv bott_c1, bott_c2;
@@ -59,7 +64,8 @@ void orc_free(orc_model *m);
 
 /* ---- forward ----
  * Stage callback: dtype 0 = int8 +-1, 1 = int32 accumulator P, 2 = float32.
- * Names: enc1.conv1, enc1.act1, encK.conv1.P (K>1), encK.act1, encK.conv2.P,
+ * Names: enc1.conv1, enc1.act1 (v1) or stem.conv, stem.act, enc1.conv1.P,
+ * enc1.act1 (v2), encK.conv1.P (K>1), encK.act1, encK.conv2.P,
  * encK.act2_skip, encK.pool.P, encK.act2_down, bott.conv{1,2}.P, bott.act{1,2},
  * decK.upcat, decK.conv{1,2}.P, decK.act{1,2}, logits. */
 typedef void (*orc_stage_cb)(void *ctx, const char *name, int dtype,

@@ -21,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libbnnref.so")
 REF_CLI = os.path.join(HERE, "_ref", "bnn_infer")
+REF_CLI_STEM = os.path.join(HERE, "_ref", "bnn_infer_stem")
 
 _i8 = C.POINTER(C.c_int8)
 _i32 = C.POINTER(C.c_int32)
@@ -230,6 +231,27 @@ class RefC:
         L.apply_fold_real.argtypes = [_f32, _i8, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
         L.maxpool_P.argtypes = [_i32, _i32, _ci, _ci, _ci, _ci, _ci]
         L.head_1x1.argtypes = [_f32, _f32, _f32, _f32, _ci, _ci, _ci, _ci]
+        # v2 engine (csrc/bnn_model_stem.h:61-64)
+        L.bnn_stem_load.argtypes = [C.c_char_p]
+        L.bnn_stem_load.restype = C.c_void_p
+        L.bnn_stem_free.argtypes = [C.c_void_p]
+        L.bnn_stem_forward.argtypes = [C.c_void_p, _f32, _ci, _ci, _f32]
+
+    def stem_load(self, path: str):
+        """bnn_stem_load: (handle, n_bands, n_classes); exits on a bad blob"""
+        h = self.lib.bnn_stem_load(path.encode())
+        hdr = (C.c_int * 7).from_address(h)
+        return h, hdr[2], hdr[3]
+
+    def stem_forward(self, handle, x: np.ndarray, n_classes: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        _, H, W = x.shape
+        out = np.zeros((n_classes, H, W), np.float32)
+        self.lib.bnn_stem_forward(C.c_void_p(handle), _p(x, _f32), H, W, _p(out, _f32))
+        return out
+
+    def stem_free(self, handle):
+        self.lib.bnn_stem_free(C.c_void_p(handle))
 
     def load(self, path: str):
         h = self.lib.bnn_load(path.encode())

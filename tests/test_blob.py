@@ -85,7 +85,7 @@ def _corruptions():
            ("short read", data[:-1]),
            ("short read", data[:30]),
            ("short read", data[:2]),
-           ("unsupported blob version", data[:4] + struct.pack("<i", 2) + data[8:]),
+           ("unsupported blob version", data[:4] + struct.pack("<i", 3) + data[8:]),
            ("unsupported upsampler", data[:20] + struct.pack("<i", 1) + data[24:]),
            ("bad conv tag", data[:24] + struct.pack("<i", 9) + data[28:])]
     # first act record follows the real conv: 28 + 16*120*9 + 16*4 bytes after the header
@@ -140,3 +140,20 @@ def test_engine_accepts_valid(tmp_path):
         p = tmp_path / f"ok{base}.blob"
         p.write_bytes(B.to_bytes(synth.make_blob(seed=base, base=base)))
         engine.blob_check(str(p))
+
+
+def test_v2_roundtrip_and_header():
+    """v2 blobs: <7i> header (version 2, ..., has_stem 1, n_stem_layers 1),
+    stem records right after it (python/bnn2c/blob.py:226-233)"""
+    import struct
+    b = synth.make_blob_v2(seed=3, base=8, stem=24)
+    data = B.to_bytes(b)
+    assert struct.unpack("<7i", data[4:32]) == (2, 8, 120, 3, 0, 1, 1)
+    assert struct.unpack("<7i", data[32:60]) == (B.TAG_CONV_REAL, 24, 120, 1, 1, 0, 1)
+    b2 = B.from_bytes(data)
+    assert b2.has_stem and B.to_bytes(b2) == data
+    assert b2.enc_conv1[0].tag == B.TAG_CONV_BIN and b2.enc_act1[0].kind == 0
+    bad = bytearray(data)
+    bad[24:28] = (0).to_bytes(4, "little")          # has_stem = 0
+    with pytest.raises(B.BlobError, match="has_stem"):
+        B.from_bytes(bytes(bad))

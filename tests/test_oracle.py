@@ -320,3 +320,54 @@ def test_batch_paths_agree(orc):
     par = m.forward_batch(x, parallel=True)
     assert np.array_equal(seq, par)
     assert np.array_equal(seq[4], m.forward(x[4]))
+
+
+# ---------------------------------------------------------------- v2 stem --
+@pytest.mark.parametrize("seed,base,stem,cov,H,W", [(1, 16, 16, False, 32, 32), (2, 8, 32, True, 17, 23),
+                                                   (4, 32, 16, True, 16, 16), (6, 16, 24, False, 30, 34)])
+def test_stem_forward_vs_reference(orc, ref, blob_file, seed, base, stem, cov, H, W):
+    """the restated v2 forward against the reference's bnn_stem_forward
+    (csrc/bnn_model_stem.c:168-255) built from its sources"""
+    b = synth.make_blob_v2(seed=seed, base=base, stem=stem, coverage=cov)
+    path = blob_file(b)
+    model = orc.parse(B.to_bytes(b))
+    h, _, ncls = ref.stem_load(path)
+    x = synth.make_input(seed + 60, 2, 120, H, W)
+    try:
+        for n in range(2):
+            got = model.forward(x[n])
+            want = ref.stem_forward(h, x[n], ncls)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    finally:
+        ref.stem_free(h)
+
+
+def test_stem_stages_vs_golden(orc, golden):
+    """every v2 stage against the reference kernel chain (stem 1x1 conv,
+    real fold, binary enc1 ...) recorded in tests/golden"""
+    import hashlib
+    meta, arrays = golden
+    assert meta["stem_cases"]
+    for name, c in meta["stem_cases"].items():
+        b = synth.make_blob_v2(seed=c["blob_seed"], base=c["base"], stem=c["stem"], coverage=c["coverage"])
+        assert hashlib.sha256(B.to_bytes(b)).hexdigest() == c["blob_sha256"], name
+        model = orc.parse(B.to_bytes(b))
+        x = synth.make_input(c["input_seed"], c["N"], 120, c["H"], c["W"])
+        for n in range(c["N"]):
+            logits, st = model.forward(x[n], stages=True)
+            assert "stem.conv" in st and "enc1.conv1.P" in st and "enc1.conv1" not in st
+            assert set(st) == set(c["stages"][n]), name
+            for k, v in st.items():
+                assert hashlib.sha256(np.ascontiguousarray(v).tobytes()).hexdigest() == c["stages"][n][k], (name, k)
+            assert np.array_equal(logits.view(np.uint32), arrays[f"{name}__logits"][n].view(np.uint32))
+
+
+def test_stem_blob_checks(orc):
+    b = synth.make_blob_v2(seed=5)
+    data = bytearray(B.to_bytes(b))
+    m = orc.parse(bytes(data))
+    assert m.forward(synth.make_input(1, 1)[0]).shape == (3, 32, 32)
+    bad = bytearray(data)
+    bad[28:32] = (2).to_bytes(4, "little")          # n_stem_layers = 2
+    with pytest.raises(Exception, match="n_stem_layers"):
+        orc.parse(bytes(bad))
