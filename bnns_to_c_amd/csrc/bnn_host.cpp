@@ -1,15 +1,20 @@
-// bnn_host.cpp - libbnn_hip.so host side: blob v1 parsing, device model,
-// the batched forward, the debug/profiling paths and the C ABI.
+// bnn_host.cpp - libbnn_hip.so host side: blob parsing (v1 and the v2
+// spectral-stem model), device model, the batched forward, the
+// debug/profiling paths and the C ABI.
 //
-// Blob layout and record order: python/bnn2c/blob.py:36-114,159-200 read the
-// way csrc/bnn_model.c:27-96 reads it (same checks, plus version == 1 and
-// upsampler == 0, which the reference reads but never checks).  The forward
-// follows csrc/bnn_model.c:150-253 stage for stage; every stage runs as one
-// kernel on the model's HIP stream over a batch of N independent patches.
+// Blob layout and record order: python/bnn2c/blob.py:36-114,159-200 (v1) and
+// :204-240 (v2) read the way csrc/bnn_model.c:27-96 and
+// csrc/bnn_model_stem.c:79-122 read them (same checks, plus upsampler == 0,
+// which the references read but never check, and version == 1 for v1).  The
+// forward follows csrc/bnn_model.c:150-253 stage for stage, and for v2
+// csrc/bnn_model_stem.c:171-253 (the stem, then enc1.conv1 binary like
+// enc2..4); every stage runs as one kernel on the model's HIP stream over a
+// batch of N independent patches.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -19,6 +24,7 @@
 
 #include "bnn_kernels.h"
 #include "bnn_model.h"
+#include "bnn_model_stem.h"
 #include "bnn_prof.h"
 
 using namespace bnn;
@@ -149,7 +155,15 @@ void free_host(Model* m) {
   free(m->head_W); free(m->head_bias);
 }
 
-int parse_blob(const char* path, Model** out) {
+// the v2 records ahead of the body (csrc/bnn_model_stem.c:94-100)
+struct StemPart {
+  int has_stem = 0, n_stem_layers = 0;
+  Conv c{};
+  Act a{};
+};
+
+// want = 1: a v1 blob into *out; want = 2: a v2 blob, its stem into *st
+int parse_blob(const char* path, Model** out, int want = 1, StemPart* st = nullptr) {
   *out = nullptr;
   FILE* f = fopen(path, "rb");
   if (!f) return set_err(BNN_EBLOB, "cannot open %s", path);
@@ -163,17 +177,30 @@ int parse_blob(const char* path, Model** out) {
   r.off = 4;
   Model* m = (Model*)calloc(1, sizeof(Model));
   if (!m) return set_err(BNN_EBLOB, "out of memory");
-  m->version = r.i32(); m->base_channels = r.i32();
-  m->n_bands = r.i32(); m->n_classes = r.i32(); m->upsampler = r.i32();
-  if (!r.bad && m->version != 1) {
-    char msg[64];
-    snprintf(msg, sizeof msg, "unsupported blob version %d", m->version);
+  m->version = r.i32();
+  if (!r.bad && m->version != want) {
+    char msg[128];
+    if (want == 2)
+      snprintf(msg, sizeof msg, "bnn_stem: expected v2 blob, got v%d (use the v1 engine for non-stem models)",
+               m->version);
+    else if (m->version == 2)
+      snprintf(msg, sizeof msg, "unsupported blob version 2 (a spectral-stem model: load it with bnn_stem_load)");
+    else
+      snprintf(msg, sizeof msg, "unsupported blob version %d", m->version);
     r.fail(msg);
   }
+  m->base_channels = r.i32();
+  m->n_bands = r.i32(); m->n_classes = r.i32(); m->upsampler = r.i32();
   if (!r.bad && m->upsampler != 0) {
     char msg[64];
     snprintf(msg, sizeof msg, "unsupported upsampler %d (v1 engine runs nearest only)", m->upsampler);
     r.fail(msg);
+  }
+  if (want == 2) {
+    st->has_stem = r.i32(); st->n_stem_layers = r.i32();
+    if (!r.bad && (st->has_stem != 1 || st->n_stem_layers != 1))
+      r.fail("bnn_stem: only has_stem=1, n_stem_layers=1 supported");
+    read_conv(r, &st->c); read_act(r, &st->a);
   }
   for (int i = 0; i < 4; ++i) {
     read_conv(r, &m->enc_conv1[i]); read_act(r, &m->enc_act1[i]);
@@ -199,6 +226,7 @@ int parse_blob(const char* path, Model** out) {
   if (r.bad) {
     free_host(m);
     free(m);
+    if (st) { free_conv(&st->c); free_act(&st->a); }
     return BNN_EBLOB;
   }
   *out = m;
@@ -212,13 +240,23 @@ bool conv_ok(const Conv& c, int tag, int cin) {
 }
 bool act_ok(const Act& a, bool real, int c) { return a.C == c && (real ? a.kind != 0 : a.kind == 0); }
 
-int validate(const Model* m) {
+// st: the v2 stem (1x1 real conv from n_bands channels, real fold), after
+// which enc1.conv1 is binary
+int validate(const Model* m, const StemPart* st = nullptr) {
   if (m->n_bands <= 0 || m->n_classes <= 0) return set_err(BNN_EBLOB, "bad n_bands/n_classes");
   int c = m->n_bands, skipc[4];
+  if (st) {
+    const Conv& sc = st->c;
+    if (sc.tag != TAG_REAL || sc.Cin != c || sc.Cout <= 0 || sc.kh != 1 || sc.kw != 1 || sc.pad != 0 ||
+        sc.stride != 1 || !act_ok(st->a, true, sc.Cout))
+      return set_err(BNN_EBLOB, "stem does not chain (a 1x1 pad-0 real conv from n_bands, then a real fold)");
+    c = sc.Cout;
+  }
   for (int i = 0; i < 4; ++i) {
     const Conv &c1 = m->enc_conv1[i], &c2 = m->enc_conv2[i];
-    if (!conv_ok(c1, i == 0 ? TAG_REAL : TAG_BIN, c)) return set_err(BNN_EBLOB, "enc%d.conv1 does not chain", i + 1);
-    if (!act_ok(m->enc_act1[i], i == 0, c1.Cout)) return set_err(BNN_EBLOB, "enc%d.act1 does not chain", i + 1);
+    const bool real = i == 0 && !st;
+    if (!conv_ok(c1, real ? TAG_REAL : TAG_BIN, c)) return set_err(BNN_EBLOB, "enc%d.conv1 does not chain", i + 1);
+    if (!act_ok(m->enc_act1[i], real, c1.Cout)) return set_err(BNN_EBLOB, "enc%d.act1 does not chain", i + 1);
     if (!conv_ok(c2, TAG_BIN, c1.Cout)) return set_err(BNN_EBLOB, "enc%d.conv2 does not chain", i + 1);
     if (!act_ok(m->enc_act2_skip[i], false, c2.Cout) || !act_ok(m->enc_act2_down[i], false, c2.Cout))
       return set_err(BNN_EBLOB, "enc%d.act2 does not chain", i + 1);
@@ -317,8 +355,10 @@ struct BnnDevice {
   int device = 0;
   hipStream_t stream = nullptr;
   std::vector<void*> allocs;
+  // the first stage: v1 enc1.conv1 (3x3) or the v2 stem (1x1), real conv + real fold
+  bool stem = false;
   int rcin = 0, rcout = 0;
-  uint64_t* rwm = nullptr;  // lane-mask weights (all signs +-1), else null and rw is used
+  uint64_t* rwm = nullptr;  // lane-mask weights (v1: all signs +-1, else null and rw is used)
   float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   float *hw = nullptr, *hb = nullptr;
@@ -376,9 +416,10 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   return BNN_OK;
 }
 
-// real conv weights: lane masks for the matrix-core kernel when every sign
-// is +-1, else floats in groups of kRealGroup output channels for the
-// vector-ALU kernel; folds padded to 32
+// real conv weights.  v2 stem: lane masks of the 1x1 matrix-core kernel
+// (signs +1, -1 or 0).  v1 3x3: lane masks for the matrix-core kernel when
+// every sign is +-1, else floats in groups of kRealGroup output channels for
+// the vector-ALU kernel.  Folds padded to 32.
 int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
   D->rcin = c.Cin;
   D->rcout = c.Cout;
@@ -389,7 +430,11 @@ int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
     return v;
   };
   int rc;
-  if (real_conv_signs_only(c.wsign, c.Cout, c.Cin)) {
+  if (D->stem) {
+    std::vector<uint64_t> wm(real_stem_masks_len(c.Cout, c.Cin));
+    real_stem_masks(c.wsign, c.Cout, c.Cin, wm.data());
+    if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
+  } else if (real_conv_signs_only(c.wsign, c.Cout, c.Cin)) {
     std::vector<uint64_t> wm(real_conv_masks_len(c.Cout, c.Cin));
     real_conv_masks(c.wsign, c.Cout, c.Cin, wm.data());
     if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
@@ -426,7 +471,7 @@ void release(BnnDevice* D) {
   D->stream = nullptr;
 }
 
-int build_device(Model* m) {
+int build_device(Model* m, const StemPart* st = nullptr) {
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
     return set_err(BNN_EHIP, "no HIP device visible: libbnn_hip runs the forward on the GPU only");
@@ -435,11 +480,14 @@ int build_device(Model* m) {
   HIP_TRY(hipGetDevice(&D->device));
   HIP_TRY(hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking));
   int rc;
-  if ((rc = upload_real(D, m->enc_conv1[0], m->enc_act1[0]))) return rc;
+  D->stem = st != nullptr;
+  if ((rc = st ? upload_real(D, st->c, st->a) : upload_real(D, m->enc_conv1[0], m->enc_act1[0]))) return rc;
   if ((rc = upload_bconv(D, &D->e2[0], m->enc_conv2[0], 0, &m->enc_act2_skip[0], &m->enc_act2_down[0]))) return rc;
-  for (int i = 1; i < 4; ++i) {
+  for (int i = 0; i < 4; ++i) {
+    if (i == 0 && !st) continue;  // v1 enc1.conv1 is the real conv above
     if ((rc = upload_bconv(D, &D->e1[i], m->enc_conv1[i], 0, &m->enc_act1[i], nullptr))) return rc;
-    if ((rc = upload_bconv(D, &D->e2[i], m->enc_conv2[i], 0, &m->enc_act2_skip[i], &m->enc_act2_down[i]))) return rc;
+    if (i && (rc = upload_bconv(D, &D->e2[i], m->enc_conv2[i], 0, &m->enc_act2_skip[i], &m->enc_act2_down[i])))
+      return rc;
   }
   if ((rc = upload_bconv(D, &D->b1, m->bott_conv1, 0, &m->bott_act1, nullptr))) return rc;
   if ((rc = upload_bconv(D, &D->b2, m->bott_conv2, 0, &m->bott_act2, nullptr))) return rc;
@@ -469,9 +517,9 @@ int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
   level_dims(H, W, hs, ws);
   std::vector<std::pair<uint32_t**, size_t>> plan;
   auto add = [&](uint32_t** p, int lvl, int c) { plan.push_back({p, (size_t)N * hs[lvl] * ws[lvl] * words(c)}); };
-  add(&w.a1, 0, m->enc_conv1[0].Cout);
+  add(&w.a1, 0, D->rcout);  // first-stage bits
   for (int i = 0; i < 4; ++i) {
-    if (i) add(&w.h[i], i, m->enc_conv1[i].Cout);
+    if (i || D->stem) add(&w.h[i], i, m->enc_conv1[i].Cout);
     add(&w.skip[i], i, m->enc_conv2[i].Cout);
     add(&w.down[i], i + 1, m->enc_conv2[i].Cout);
   }
@@ -557,7 +605,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   if ((rc = mark(nullptr, nullptr, 0, 0))) return rc;
 
   {
-    // enc1.conv1: real conv + real fold -> a1 bits
+    // v1 enc1.conv1 (3x3) or the v2 stem (1x1): real conv + real fold -> a1 bits
     RealArgs ra{};
     ra.x = d_in;
     ra.w = D->rw;
@@ -567,8 +615,13 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     ra.out = w.a1;
     ra.f32 = dump ? dmp->conv1 : nullptr;
     if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
-    HIP_TRY(launch_real(ra, s));
-    if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
+    if (D->stem) {
+      HIP_TRY(launch_stem(ra, s));
+      if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
+    } else {
+      HIP_TRY(launch_real(ra, s));
+      if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
+    }
   }
 
   auto bconv = [&](const DevBconv& L, int epi, const uint32_t* in0, const uint32_t* in1, int lvl, int lvl1,
@@ -599,14 +652,14 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     return mark(label, ot, (double)N * L.cout * a.H * a.W, (double)L.cin * 9);
   };
 
-  static const char* enc_c1[4] = {"", "enc2.c1", "enc3.c1", "enc4.c1"};
+  static const char* enc_c1[4] = {"enc1.c1", "enc2.c1", "enc3.c1", "enc4.c1"};
   static const char* enc_c2[4] = {"enc1.c2", "enc2.c2", "enc3.c2", "enc4.c2"};
   static const char* dec_c1[4] = {"dec4.c1", "dec3.c1", "dec2.c1", "dec1.c1"};
   static const char* dec_c2[4] = {"dec4.c2", "dec3.c2", "dec2.c2", "dec1.c2"};
   const uint32_t* x = w.a1;
   for (int i = 0; i < 4; ++i) {
     const uint32_t* hin = x;
-    if (i) {
+    if (i || D->stem) {
       if ((rc = bconv(D->e1[i], EPI_FOLD, x, nullptr, i, 0, w.h[i], nullptr, nullptr, enc_c1[i]))) return rc;
       hin = w.h[i];
     }
@@ -885,6 +938,7 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
   // P dumps in launch order, with the (c, level) of each
   struct PInfo { const char* name; int c, lvl; };
   std::vector<PInfo> pinfo;
+  if (D->stem) pinfo.push_back({"enc1.conv1.P", m->enc_conv1[0].Cout, 0});
   pinfo.push_back({"enc1.conv2.P", m->enc_conv2[0].Cout, 0});
   static const char* encn[4][2] = {{"", "enc1.conv2.P"}, {"enc2.conv1.P", "enc2.conv2.P"},
                                    {"enc3.conv1.P", "enc3.conv2.P"}, {"enc4.conv1.P", "enc4.conv2.P"}};
@@ -910,7 +964,7 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
     return p;
   };
   auto cleanup = [&]() { for (void* p : tmp) hipFree(p); };
-  d.conv1 = (float*)alloc((size_t)N * m->enc_conv1[0].Cout * H * W * 4);
+  d.conv1 = (float*)alloc((size_t)N * D->rcout * H * W * 4);
   for (size_t i = 0; i < pinfo.size(); ++i)
     d.P[i] = (int32_t*)alloc((size_t)N * pinfo[i].c * hs[pinfo[i].lvl] * ws[pinfo[i].lvl] * 4);
   for (int i = 0; i < 4; ++i) d.P2[i] = (int32_t*)alloc((size_t)N * m->enc_conv2[i].Cout * hs[i + 1] * ws[i + 1] * 4);
@@ -944,10 +998,10 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
     };
     char nm[48];
     int pi = 0;
-    if ((rc = emit_f("enc1.conv1", d.conv1, 2, m->enc_conv1[0].Cout, 0))) goto done;
-    if ((rc = emit_b("enc1.act1", w.a1, m->enc_conv1[0].Cout, 0))) goto done;
+    if ((rc = emit_f(D->stem ? "stem.conv" : "enc1.conv1", d.conv1, 2, D->rcout, 0))) goto done;
+    if ((rc = emit_b(D->stem ? "stem.act" : "enc1.act1", w.a1, D->rcout, 0))) goto done;
     for (int i = 0; i < 4; ++i) {
-      if (i) {
+      if (i || D->stem) {
         if ((rc = emit_f(pinfo[pi].name, d.P[pi], 1, pinfo[pi].c, i))) goto done;
         ++pi;
         snprintf(nm, sizeof nm, "enc%d.act1", i + 1);
@@ -984,6 +1038,140 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
 done:
   cleanup();
   return rc;
+}
+
+// =========================================================== v2 stem C ABI
+}  // extern "C"
+
+namespace {
+// A StemModel handed out by bnn_stem_load is the first member of this holder;
+// `body` is the same network seen as a Model (the stem's records aside, the
+// v2 body has v1's records in v1's order), sharing the host arrays, so the
+// v1 machinery runs it with the device model's stem flag set.
+struct StemHolder {
+  StemModel pub;
+  Model body;
+  StemPart st;
+};
+static_assert(offsetof(StemHolder, pub) == 0, "StemModel must be the holder's first member");
+static_assert(sizeof(ConvS) == sizeof(Conv) && sizeof(ActS) == sizeof(Act), "v1 and v2 records differ");
+
+const Model* body_of(const StemModel* m) {
+  return m ? &reinterpret_cast<const StemHolder*>(m)->body : nullptr;
+}
+
+void stem_public(StemHolder* h) {
+  StemModel& p = h->pub;
+  const Model& b = h->body;
+  p.version = b.version; p.base_channels = b.base_channels;
+  p.n_bands = b.n_bands; p.n_classes = b.n_classes; p.upsampler = b.upsampler;
+  p.has_stem = h->st.has_stem; p.n_stem_layers = h->st.n_stem_layers;
+  memcpy(&p.stem_conv, &h->st.c, sizeof(Conv));
+  memcpy(&p.stem_act, &h->st.a, sizeof(Act));
+  for (int i = 0; i < 4; ++i) {
+    memcpy(&p.enc_conv1[i], &b.enc_conv1[i], sizeof(Conv)); memcpy(&p.enc_conv2[i], &b.enc_conv2[i], sizeof(Conv));
+    memcpy(&p.enc_act1[i], &b.enc_act1[i], sizeof(Act));
+    memcpy(&p.enc_act2_skip[i], &b.enc_act2_skip[i], sizeof(Act));
+    memcpy(&p.enc_act2_down[i], &b.enc_act2_down[i], sizeof(Act));
+    memcpy(&p.dec_conv1[i], &b.dec_conv1[i], sizeof(Conv)); memcpy(&p.dec_conv2[i], &b.dec_conv2[i], sizeof(Conv));
+    memcpy(&p.dec_act1[i], &b.dec_act1[i], sizeof(Act)); memcpy(&p.dec_act2[i], &b.dec_act2[i], sizeof(Act));
+  }
+  memcpy(&p.bott_conv1, &b.bott_conv1, sizeof(Conv)); memcpy(&p.bott_conv2, &b.bott_conv2, sizeof(Conv));
+  memcpy(&p.bott_act1, &b.bott_act1, sizeof(Act)); memcpy(&p.bott_act2, &b.bott_act2, sizeof(Act));
+  p.head_Cout = b.head_Cout; p.head_Cin = b.head_Cin;
+  p.head_W = b.head_W; p.head_bias = b.head_bias;
+  p.dev = b.dev;
+}
+}  // namespace
+
+extern "C" {
+
+int bnn_stem_blob_check(const char* path) {
+  Model* m = nullptr;
+  StemPart st;
+  int rc = parse_blob(path, &m, 2, &st);
+  if (rc) return rc;
+  rc = validate(m, &st);
+  free_host(m);
+  free(m);
+  free_conv(&st.c);
+  free_act(&st.a);
+  return rc;
+}
+
+void bnn_stem_free(StemModel* sm) {
+  if (!sm) return;
+  StemHolder* h = reinterpret_cast<StemHolder*>(sm);
+  if (h->body.dev) {
+    release(h->body.dev);
+    delete h->body.dev;
+    h->body.dev = nullptr;
+  }
+  free_host(&h->body);
+  free_conv(&h->st.c);
+  free_act(&h->st.a);
+  free(h);
+}
+
+int bnn_stem_load_status(const char* path, StemModel** out) {
+  *out = nullptr;
+  Model* m = nullptr;
+  StemPart st;
+  int rc = parse_blob(path, &m, 2, &st);
+  if (rc) return rc;
+  StemHolder* h = (StemHolder*)calloc(1, sizeof(StemHolder));
+  if (!h) {
+    free_host(m); free(m); free_conv(&st.c); free_act(&st.a);
+    return set_err(BNN_EBLOB, "out of memory");
+  }
+  h->body = *m;  // takes over the arrays
+  free(m);
+  h->st = st;
+  if ((rc = validate(&h->body, &h->st)) || (rc = build_device(&h->body, &h->st))) {
+    const std::string keep = g_err;
+    bnn_stem_free(&h->pub);
+    g_err = keep;
+    return rc;
+  }
+  stem_public(h);
+  *out = &h->pub;
+  return BNN_OK;
+}
+
+StemModel* bnn_stem_load(const char* path) {
+  StemModel* m = nullptr;
+  if (bnn_stem_load_status(path, &m)) die();
+  return m;
+}
+
+int bnn_stem_forward_batch(const StemModel* m, const float* input, int N, int H, int W, float* logits) {
+  return run_host(body_of(m), input, N, H, W, logits, nullptr);
+}
+
+void bnn_stem_forward(const StemModel* m, const float* input, int H, int W, float* logits) {
+  prof_reset();
+  if (bnn_stem_forward_batch(m, input, 1, H, W, logits)) die();
+}
+
+int bnn_stem_forward_device(const StemModel* m, const float* d_input, int N, int H, int W, float* d_logits,
+                            void* stream) {
+  return run_device(body_of(m), d_input, N, H, W, d_logits, (hipStream_t)stream, nullptr);
+}
+
+void* bnn_stem_stream(const StemModel* m) { return bnn_stream(body_of(m)); }
+
+int bnn_stem_forward_patched(const StemModel* m, const float* input, int H, int W, float* logits, int P) {
+  return bnn_forward_patched(body_of(m), input, H, W, logits, P);
+}
+
+int bnn_stem_forward_patched_device(const StemModel* m, const float* d_input, int H, int W, float* d_logits,
+                                    int P, void* stream) {
+  return bnn_forward_patched_device(body_of(m), d_input, H, W, d_logits, P, stream);
+}
+
+int bnn_stem_forward_debug(const StemModel* m, const float* input, int N, int H, int W, float* logits,
+                           bnn_stem_stage_cb cb, void* ctx) {
+  return bnn_forward_debug(body_of(m), input, N, H, W, logits, cb, ctx);
 }
 
 // ----------------------------------------------------------- profiler API

@@ -1,5 +1,8 @@
-// bnn_infer - command-line driver, a drop-in for the reference's csrc/bnn_infer
-// (csrc/main.c:1-80): same arguments, same "rand" input, same stderr report.
+// bnn_infer / bnn_infer_stem - command-line drivers, drop-ins for the
+// reference's csrc/bnn_infer (csrc/main.c:1-80) and csrc/bnn_infer_stem
+// (csrc/main_stem.c:24-88): same arguments, same "rand" input, same stderr
+// report.  One source: built with -DBNN_CLI_STEM=1 it is bnn_infer_stem
+// (v2 spectral-stem blobs, bnn_model_stem.h).
 //
 //   bnn_infer weights.blob input.bin|rand output.bin [H W [reps]]
 //     input.bin : n_bands*H*W float32, [band,row,col]; "rand" = srand(1234)
@@ -16,7 +19,40 @@
 #include <algorithm>
 
 #include "bnn_model.h"
+#include "bnn_model_stem.h"
 #include "bnn_prof.h"
+
+#ifndef BNN_CLI_STEM
+#define BNN_CLI_STEM 0
+#endif
+
+namespace {
+// the one model type this binary drives
+template <bool STEM>
+struct Api;
+template <>
+struct Api<false> {
+  using M = Model;
+  static M* load(const char* p) { return bnn_load(p); }
+  static void forward(const M* m, const float* x, int H, int W, float* y) { bnn_forward(m, x, H, W, y); }
+  static void release(M* m) { bnn_free(m); }
+  static void banner(const M* m, int H, int W, int reps) {
+    fprintf(stderr, "# H=%d W=%d bands=%d classes=%d reps=%d\n", H, W, m->n_bands, m->n_classes, reps);
+  }
+};
+template <>
+struct Api<true> {
+  using M = StemModel;
+  static M* load(const char* p) { return bnn_stem_load(p); }
+  static void forward(const M* m, const float* x, int H, int W, float* y) { bnn_stem_forward(m, x, H, W, y); }
+  static void release(M* m) { bnn_stem_free(m); }
+  static void banner(const M* m, int H, int W, int reps) {
+    fprintf(stderr, "# [stem] H=%d W=%d bands=%d classes=%d stem_channels=%d reps=%d\n", H, W, m->n_bands,
+            m->n_classes, m->stem_conv.Cout, reps);
+  }
+};
+using A = Api<BNN_CLI_STEM != 0>;
+}  // namespace
 
 int main(int argc, char** argv) {
   if (argc < 4) {
@@ -31,7 +67,7 @@ int main(int argc, char** argv) {
   const bool profile = pe && *pe && strcmp(pe, "0") != 0;
 
   const double t0 = prof_now();
-  Model* m = bnn_load(argv[1]);
+  A::M* m = A::load(argv[1]);
   const double t_load = prof_now() - t0;
 
   const long n_in = (long)m->n_bands * H * W;
@@ -54,7 +90,7 @@ int main(int argc, char** argv) {
   for (int r = 0; r < reps; ++r) {
     if (profile) bnn_prof_enable(r == reps - 1);  // per-op rows of the last rep
     const double f0 = prof_now();
-    bnn_forward(m, input.data(), H, W, logits.data());
+    A::forward(m, input.data(), H, W, logits.data());
     ts[r] = (prof_now() - f0) * 1e3;
   }
   std::sort(ts.begin(), ts.end());
@@ -70,11 +106,11 @@ int main(int argc, char** argv) {
   fclose(fo);
   const double t_write = (prof_now() - w0) * 1e3;
 
-  fprintf(stderr, "# H=%d W=%d bands=%d classes=%d reps=%d\n", H, W, m->n_bands, m->n_classes, reps);
+  A::banner(m, H, W, reps);
   fprintf(stderr, "# blob load : %9.3f ms\n", t_load * 1e3);
   fprintf(stderr, "# forward   : %9.3f ms  (median; min %.3f, max %.3f)\n", med, tmin, tmax);
   fprintf(stderr, "# out write : %9.3f ms\n", t_write);
   prof_report(stderr);
-  bnn_free(m);
+  A::release(m);
   return 0;
 }

@@ -142,6 +142,31 @@ inline void real_conv_masks(const int8_t* wsign, int cout, int cin, uint64_t* ou
           out[((size_t)(co / 16) * cp + ci) * 3 + t / 4] |= 1ull << (16 * (t % 4) + co % 16);
 }
 
+// 1x1 stem weights (v2 models; signs +1, -1 or 0): 64-bit lane masks
+// [group of four input channels q][16-channel group g][2]; bit 16k + i of
+// mask 0 is set iff w[16g + i][4q + k] > 0, of mask 1 iff it is nonzero.
+// Channels past cout or cin, and the groups that pad the group count to a
+// multiple of the groups per wave, leave their bits 0.
+inline int stem_groups_padded(int cout) {
+  const int ngrp = (cout + 15) / 16, G = ngrp < 4 ? ngrp : 4;
+  return (ngrp + G - 1) / G * G;
+}
+inline size_t real_stem_masks_len(int cout, int cin) { return (size_t)2 * stem_groups_padded(cout) * ((cin + 3) / 4); }
+inline void real_stem_masks(const int8_t* wsign, int cout, int cin, uint64_t* out) {
+  const int ngp = stem_groups_padded(cout);
+  for (size_t i = 0; i < real_stem_masks_len(cout, cin); ++i) out[i] = 0;
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci) {
+      const int8_t w = wsign[(size_t)co * cin + ci];
+      const size_t at = ((size_t)(ci / 4) * ngp + co / 16) * 2;
+      const uint64_t bit = 1ull << (16 * (ci % 4) + co % 16);
+      if (w > 0) out[at] |= bit;
+      if (w != 0) out[at + 1] |= bit;
+    }
+}
+// the 1x1 real conv + real fold (v2 stem): wm = real_stem_masks, w unused
+hipError_t launch_stem(const RealArgs& a, hipStream_t s);
+
 // Launchers return hipSuccess or the first launch error.  mt = micro-tile
 // side (1 or 2), cog = output channels per work-item (8/16/32).
 hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,

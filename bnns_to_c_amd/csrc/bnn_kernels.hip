@@ -445,6 +445,169 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
 }
 
 // ------------------------------------------------------------------------
+// 1x1 real-input stem on the matrix cores (v2 models)
+// ------------------------------------------------------------------------
+// out[co][p] = alpha[co] * (sum over ci from 0 in order of w[co][ci] * x[ci][p])
+// (csrc/bnn_conv_realin.c:140-155), then the real fold, as bits.  One
+// v_mfma_f32_16x16x1_4b_f32 per (ci, 16-channel group) advances 16 channels
+// x 64 pixels by one exact fma step (w is +1, -1 or 0, so w*x is exact and
+// fma(w, x, acc) rounds as acc + w*x does).  A wave owns 64 consecutive
+// pixels (lane l = pixel p0 + l: each ci is one coalesced 256-byte load) and
+// G channel groups; with CBSZ = 2 one weight register holds the signs of four
+// input channels (lanes 16k..16k+15 = channel 4q+k), built from two lane
+// masks (positive, nonzero).  D register r of lane l holds pixel
+// p0 + 16*(r/4) + l%16, channel 16g + 4*(l/16) + r%4.
+constexpr int kStemQuads = 4;  // quads of input channels in flight per lane
+
+template <int G, int T>
+__device__ __forceinline__ void stem_step(f32x16 (&acc)[G], const float (&wq)[G], float xv) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(wq[g], xv, acc[g], 2, T, 0);
+}
+
+struct alignas(16) StemMask {
+  uint64_t pos, nz;
+};
+
+// weights of quad q: masks [nq][ngp] (real_stem_masks), this wave's G groups
+template <int G>
+__device__ __forceinline__ void stem_weights(const uint64_t* __restrict__ wm, int q, int ngp, int g0,
+                                             float (&wq)[G]) {
+  const StemMask* m = reinterpret_cast<const StemMask*>(wm) + (size_t)q * ngp + g0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const StemMask mm = m[g];
+    const float sg = __builtin_amdgcn_inverse_ballot_w64(mm.pos) ? 1.0f : -1.0f;
+    wq[g] = __builtin_amdgcn_inverse_ballot_w64(mm.nz) ? sg : 0.0f;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void k_stem_mfma(const RealArgs a, uint32_t xbytes, int ngp) {
+  const int lane = threadIdx.x & 63;
+  const int ny = ngp / G;  // channel-group blocks per pixel tile
+  const long tile = (long)(blockIdx.x / ny) * 4 + (threadIdx.x >> 6);
+  const int g0 = (int)(blockIdx.x % ny) * G;
+  const int HW = a.H * a.W;
+  const long npix = (long)a.N * HW;
+  const long q = tile * 64 + lane;  // this lane's pixel in [N][H*W]
+  const bool live = q < npix;
+  const int n = live ? (int)(q / HW) : 0;
+  const int p = live ? (int)(q - (long)n * HW) : 0;
+  const int py = p / a.W, px = p - py * a.W;
+  const InGeom ig = in_geom(a, n);
+  const bool inside = live && py < ig.ylim && px < ig.xlim;
+  const uint32_t voff = inside ? (uint32_t)(ig.base + (size_t)py * ig.rstride + px) * 4u : 0x80000000u;
+  const uint32_t cbytes = (uint32_t)(ig.cstride * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
+
+  f32x16 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[g][r] = 0.0f;
+
+  // Channel c sits in slot c % 16 of xr; a slot is refilled (16 channels
+  // ahead) right after its step has read it.  Loads run unguarded: a
+  // channel at or past cin is the next image's data or past the buffer
+  // (read as 0), and only the guarded tail quad can meet it.
+  constexpr int kAhead = 4 * kStemQuads;
+  float xr[kAhead];
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) xr[k] = ld_f32(rs, voff, (uint32_t)k * cbytes);
+  const int qf = a.cin >> 2, rem = a.cin & 3;
+  auto quad = [&](auto hc, int qq) {
+    constexpr int h = decltype(hc)::value;
+    float wq[G];
+    stem_weights<G>(a.wm, qq, ngp, g0, wq);
+    stem_step<G, 0>(acc, wq, xr[4 * h + 0]);
+    stem_step<G, 1>(acc, wq, xr[4 * h + 1]);
+    stem_step<G, 2>(acc, wq, xr[4 * h + 2]);
+    stem_step<G, 3>(acc, wq, xr[4 * h + 3]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xr[4 * h + k] = ld_f32(rs, voff, (uint32_t)(4 * qq + k + kAhead) * cbytes);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto tail = [&](auto hc, int qq) {
+    constexpr int h = decltype(hc)::value;
+    float wq[G];
+    stem_weights<G>(a.wm, qq, ngp, g0, wq);
+    stem_step<G, 0>(acc, wq, xr[4 * h]);
+    if (rem > 1) stem_step<G, 1>(acc, wq, xr[4 * h + 1]);
+    if (rem > 2) stem_step<G, 2>(acc, wq, xr[4 * h + 2]);
+  };
+  int qi = 0;
+#pragma unroll 1
+  for (; qi + kStemQuads <= qf; qi += kStemQuads) {
+    quad(std::integral_constant<int, 0>{}, qi);
+    quad(std::integral_constant<int, 1>{}, qi + 1);
+    quad(std::integral_constant<int, 2>{}, qi + 2);
+    quad(std::integral_constant<int, 3>{}, qi + 3);
+  }
+  // the last qf % 4 full quads, then the partial quad (cin % 4 channels)
+  auto finish = [&](auto hc) {
+    constexpr int h = decltype(hc)::value;
+    if (qi + h < qf) quad(hc, qi + h);
+    else if (qi + h == qf && rem) tail(hc, qi + h);
+  };
+  finish(std::integral_constant<int, 0>{});
+  finish(std::integral_constant<int, 1>{});
+  finish(std::integral_constant<int, 2>{});
+  finish(std::integral_constant<int, 3>{});
+
+  // alpha, the real fold (csrc/bnn_fold.c:62-77, A*x+B fused as in the
+  // reference build), bits gathered across the four lane groups
+  const int cwo = (a.cout + 31) >> 5;
+  const int ngrp = (a.cout + 15) >> 4;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int gg = g0 + g;
+    if (gg >= ngrp) break;
+    const int cq = gg * 16 + 4 * (lane >> 4);
+    uint32_t w01 = 0, w23 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int co = cq + k;
+      const int cc = min(co, a.cout - 1);
+      const float al = a.alpha[cc];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float o = __fmul_rn(al, acc[g][4 * b + k]);
+        const long qp = tile * 64 + 16 * b + (lane & 15);
+        if (a.f32 && qp < npix && co < a.cout) {
+          const long nn = qp / HW;
+          a.f32[((size_t)nn * a.cout + co) * HW + (qp - nn * HW)] = o;
+        }
+        if (a.out) {
+          float z = __fmaf_rn(a.A[cc], o, a.B[cc]);
+          if (z < 0.0f) z = __fmul_rn(a.slope[cc], z);
+          const float rr = __fadd_rn(z, a.rsign[cc]);
+          const uint32_t bit = (rr > 0.0f && co < a.cout) ? 1u : 0u;
+          const int sh = 16 * (b & 1) + 4 * (lane >> 4) + k;
+          if (b < 2) w01 |= bit << sh;
+          else w23 |= bit << sh;
+        }
+      }
+    }
+    if (!a.out) continue;
+    w01 |= (uint32_t)__shfl_xor((int)w01, 16);
+    w01 |= (uint32_t)__shfl_xor((int)w01, 32);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 16);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 32);
+    // lane group b stores pixel p0 + 16b + l%16: 16 bits at bit 16*(gg%2)
+    // of word gg/2; the last group of an odd count writes its whole word
+    const int b = lane >> 4;
+    const uint32_t word = ((b < 2 ? w01 : w23) >> (16 * (b & 1))) & 0xFFFFu;
+    const long qp = tile * 64 + 16 * b + (lane & 15);
+    if (qp >= npix) continue;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + (size_t)qp * cwo) + gg * 2;
+    if ((gg & 1) == 0 && gg == ngrp - 1) *reinterpret_cast<uint32_t*>(dst) = word;
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+  }
+}
+
+// ------------------------------------------------------------------------
 // binary conv with fused epilogues
 // ------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
@@ -988,6 +1151,30 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s) {
     BNN_RG(1) BNN_RG(2) BNN_RG(3) BNN_RG(4) BNN_RG(5) BNN_RG(6) BNN_RG(7) BNN_RG(8)
 #undef BNN_RG
     default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int stem_groups_per_wave(int cout) { return std::min(4, (cout + 15) / 16); }
+
+hipError_t launch_stem(const RealArgs& a, hipStream_t s) {
+  if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
+  const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
+  // offsets stay below 2^31 even for the channels read ahead past cin, so
+  // a lane outside the image (base offset 2^31) always reads past the buffer
+  const size_t cstride = a.pcols > 0 ? (size_t)a.sH * a.sW : (size_t)a.H * a.W;
+  if (xbytes + (size_t)(4 * kStemQuads + 4) * 4 * cstride >= 0x80000000ull || !a.wm || a.cin < 1)
+    return hipErrorInvalidValue;
+  const long npix = (long)a.N * a.H * a.W;
+  const long blocks_px = (npix + 255) / 256;
+  const int G = stem_groups_per_wave(a.cout);
+  const int ngp = stem_groups_padded(a.cout);
+  const unsigned grid = (unsigned)(blocks_px * (ngp / G));
+  switch (G) {
+    case 1: hipLaunchKernelGGL(k_stem_mfma<1>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
+    case 2: hipLaunchKernelGGL(k_stem_mfma<2>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
+    case 3: hipLaunchKernelGGL(k_stem_mfma<3>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
+    default: hipLaunchKernelGGL(k_stem_mfma<4>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
   }
   return hipGetLastError();
 }

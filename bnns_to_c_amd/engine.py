@@ -1,8 +1,11 @@
-"""ctypes bindings for libbnn_hip.so, the gfx950 engine (include/bnn_model.h).
+"""ctypes bindings for libbnn_hip.so, the gfx950 engine (include/bnn_model.h,
+include/bnn_model_stem.h).
 
 This is the Python mirror of the reference's C interface for the v1 path:
 `Engine.load` / `forward` / `free` wrap bnn_load / bnn_forward / bnn_free
-(csrc/bnn_model.h:57-60) and the kernel functions keep the reference's
+(csrc/bnn_model.h:57-60), `StemEngine` the v2 spectral-stem model's
+bnn_stem_load / bnn_stem_forward / bnn_stem_free
+(csrc/bnn_model_stem.h:61-64), and the kernel functions keep the reference's
 names, argument order and batch-1 layouts (csrc/bnn_model.h:7-23), exactly as
 the reference's ctypes harnesses bind them (python/verify/bconv_harness.py:36-47,
 forward_driver.py:55-66).  Every call runs on the GPU.  There is no CPU
@@ -24,7 +27,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libbnn_hip.so")
 CLI_PATH = os.path.join(LIB_DIR, "bnn_infer")
+CLI_STEM_PATH = os.path.join(LIB_DIR, "bnn_infer_stem")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "bnn_model.h")
+HEADER_STEM = os.path.join(os.path.dirname(HERE), "include", "bnn_model_stem.h")
 
 BNN_OK, BNN_EBLOB, BNN_EARG, BNN_EHIP = 0, 1, 2, 3
 
@@ -71,6 +76,18 @@ def lib() -> C.CDLL:
     L.bnn_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
     L.bnn_stream.argtypes = [_vp]
     L.bnn_stream.restype = _vp
+    # v2 (spectral stem): the same signatures on a StemModel*
+    L.bnn_stem_blob_check.argtypes = [C.c_char_p]
+    L.bnn_stem_load_status.argtypes = [C.c_char_p, C.POINTER(_vp)]
+    L.bnn_stem_free.argtypes = [_vp]
+    L.bnn_stem_forward.argtypes = [_vp, _f32, _ci, _ci, _f32]
+    L.bnn_stem_forward_batch.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32]
+    L.bnn_stem_forward_device.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
+    L.bnn_stem_forward_debug.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32, STAGE_CB, _vp]
+    L.bnn_stem_forward_patched.argtypes = [_vp, _f32, _ci, _ci, _f32, _ci]
+    L.bnn_stem_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
+    L.bnn_stem_stream.argtypes = [_vp]
+    L.bnn_stem_stream.restype = _vp
     L.bnn_prof_enable.argtypes = [_ci]
     L.bnn_prof_count.restype = _ci
     L.bnn_prof_get.argtypes = [_ci, C.c_char_p, _ci, C.c_char_p, _ci, C.POINTER(C.c_double),
@@ -112,12 +129,17 @@ def _p(a: np.ndarray, t):
 
 
 def blob_check(path: str) -> None:
-    """Parse and validate a blob on the host only; raises BnnError."""
+    """Parse and validate a v1 blob on the host only; raises BnnError."""
     _check(lib().bnn_blob_check(path.encode()))
 
 
+def stem_blob_check(path: str) -> None:
+    """Parse and validate a v2 (spectral-stem) blob on the host only."""
+    _check(lib().bnn_stem_blob_check(path.encode()))
+
+
 def header_symbols(path: str = HEADER):
-    """Function names declared in include/bnn_model.h."""
+    """Function names declared in a header (default include/bnn_model.h)."""
     import re
     txt = open(path).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
@@ -128,19 +150,23 @@ def header_symbols(path: str = HEADER):
 
 
 class Engine:
-    """A loaded model on the GPU (the reference's Model*)."""
+    """A loaded v1 model on the GPU (the reference's Model*)."""
+
+    _api = "bnn_"  # entry-point prefix: bnn_load_status, bnn_forward_batch, ...
 
     def __init__(self, path: str):
-        L = lib()
         h = _vp()
-        _check(L.bnn_load_status(path.encode(), C.byref(h)))
+        _check(self._fn("load_status")(path.encode(), C.byref(h)))
         self.h = h
         hdr = (C.c_int * 5).from_address(h.value)
         self.version, self.base, self.n_bands, self.n_classes, self.upsampler = list(hdr)
 
+    def _fn(self, name: str):
+        return getattr(lib(), self._api + name)
+
     def close(self) -> None:
         if getattr(self, "h", None):
-            lib().bnn_free(self.h)
+            self._fn("free")(self.h)
             self.h = None
 
     def __del__(self):
@@ -157,13 +183,13 @@ class Engine:
         x = np.ascontiguousarray(x, np.float32)
         N, nb, H, W = x.shape
         out = np.empty((N, self.n_classes, H, W), np.float32)
-        _check(lib().bnn_forward_batch(self.h, _p(x, _f32), N, H, W, _p(out, _f32)))
+        _check(self._fn("forward_batch")(self.h, _p(x, _f32), N, H, W, _p(out, _f32)))
         return out
 
     def forward_device(self, d_in: int, N: int, H: int, W: int, d_out: int,
                        stream: Optional[int] = None) -> None:
-        _check(lib().bnn_forward_device(self.h, _vp(d_in), N, H, W, _vp(d_out),
-                                        _vp(stream or None)))
+        _check(self._fn("forward_device")(self.h, _vp(d_in), N, H, W, _vp(d_out),
+                                          _vp(stream or None)))
 
     def forward_patched(self, cube: np.ndarray, P: int = 32) -> np.ndarray:
         """Scene [n_bands, H, W] -> logit map [n_classes, H, W] by independent
@@ -171,20 +197,21 @@ class Engine:
         cube = np.ascontiguousarray(cube, np.float32)
         nb, H, W = cube.shape
         out = np.empty((self.n_classes, H, W), np.float32)
-        _check(lib().bnn_forward_patched(self.h, _p(cube, _f32), H, W, _p(out, _f32), P))
+        _check(self._fn("forward_patched")(self.h, _p(cube, _f32), H, W, _p(out, _f32), P))
         return out
 
     def forward_patched_device(self, d_cube: int, H: int, W: int, d_map: int, P: int = 32,
                                stream: Optional[int] = None) -> None:
-        _check(lib().bnn_forward_patched_device(self.h, _vp(d_cube), H, W, _vp(d_map), P,
-                                                _vp(stream or None)))
+        _check(self._fn("forward_patched_device")(self.h, _vp(d_cube), H, W, _vp(d_map), P,
+                                                  _vp(stream or None)))
 
     def stream(self) -> int:
-        return lib().bnn_stream(self.h)
+        return self._fn("stream")(self.h)
 
     def forward_debug(self, x: np.ndarray):
         """Forward with every intermediate stage returned as numpy arrays
-        (binary stages as int8 +-1 [N,C,H,W], P as int32, enc1.conv1 as f32)."""
+        (binary stages as int8 +-1 [N,C,H,W], P as int32, the first real
+        conv's output -- enc1.conv1, or stem.conv for v2 -- as f32)."""
         x = np.ascontiguousarray(x, np.float32)
         N, nb, H, W = x.shape
         out = np.empty((N, self.n_classes, H, W), np.float32)
@@ -196,9 +223,23 @@ class Engine:
             arr = np.ctypeslib.as_array(C.cast(data, C.POINTER(ct)), shape=(cnt,))
             got[name.decode()] = arr.copy().reshape(n, c, h, w)
 
-        _check(lib().bnn_forward_debug(self.h, _p(x, _f32), N, H, W, _p(out, _f32),
-                                       STAGE_CB(cb), None))
+        _check(self._fn("forward_debug")(self.h, _p(x, _f32), N, H, W, _p(out, _f32),
+                                         STAGE_CB(cb), None))
         return out, got
+
+
+class StemEngine(Engine):
+    """A loaded v2 spectral-stem model on the GPU (the reference's
+    StemModel*, csrc/bnn_model_stem.h:44-64); the same methods as Engine."""
+
+    _api = "bnn_stem_"
+
+    def __init__(self, path: str):
+        super().__init__(path)
+        # has_stem, n_stem_layers, then the stem ConvS (8-byte aligned) at 32
+        ints = (C.c_int * 10).from_address(self.h.value)
+        self.has_stem, self.n_stem_layers = ints[5], ints[6]
+        self.stem_channels = ints[9]
 
 
 # ---------------------------------------------------------------- profiler --

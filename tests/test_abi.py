@@ -1,6 +1,7 @@
 """libbnn_hip.so loads without a GPU and exports every entry point that
-include/bnn_model.h and include/bnn_prof.h declare; host-only pieces of the
-engine are checked here against the checker."""
+include/bnn_model.h, include/bnn_model_stem.h and include/bnn_prof.h
+declare; host-only pieces of the engine are checked here against the
+checker."""
 import ctypes
 import os
 import subprocess
@@ -16,8 +17,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def test_library_exports_header_symbols():
     lib = E.lib()
-    names = set(E.header_symbols()) | set(E.header_symbols(os.path.join(ROOT, "include", "bnn_prof.h")))
-    assert {"bnn_load", "bnn_forward", "bnn_free", "bconv_dispatch", "head_1x1", "prof_report"} <= names
+    names = (set(E.header_symbols()) | set(E.header_symbols(E.HEADER_STEM))
+             | set(E.header_symbols(os.path.join(ROOT, "include", "bnn_prof.h"))))
+    assert {"bnn_load", "bnn_forward", "bnn_free", "bconv_dispatch", "head_1x1", "prof_report",
+            "bnn_stem_load", "bnn_stem_forward", "bnn_stem_free"} <= names
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
     out = subprocess.run(["nm", "-D", "--defined-only", E.LIB_PATH], capture_output=True, text=True).stdout
@@ -33,9 +36,11 @@ def test_library_built_for_gfx950():
 
 
 def test_header_compiles_as_c(tmp_path):
+    # both model headers together, as a caller of both engines includes them
     src = tmp_path / "t.c"
-    src.write_text('#include "bnn_model.h"\n#include "bnn_prof.h"\n'
-                   "int main(void){ Model *m = 0; (void)m; return sizeof(Conv) > 0 ? 0 : 1; }\n")
+    src.write_text('#include "bnn_model.h"\n#include "bnn_model_stem.h"\n#include "bnn_prof.h"\n'
+                   "int main(void){ Model *m = 0; StemModel *s = 0; (void)m; (void)s;\n"
+                   "  return sizeof(Conv) == sizeof(ConvS) && sizeof(Act) == sizeof(ActS) ? 0 : 1; }\n")
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
                     "-c", str(src), "-o", str(tmp_path / "t.o")], check=True)
 
@@ -46,6 +51,22 @@ def test_model_struct_prefix_matches_reference():
         _fields_ = [("i", ctypes.c_int * 8), ("p", ctypes.c_void_p * 3)]
 
     assert ctypes.sizeof(Conv) == 56
+
+
+def test_stem_model_layout_matches_reference(tmp_path):
+    """StemModel keeps csrc/bnn_model_stem.h:44-59's field order (main_stem.c
+    reads n_bands, n_classes and stem_conv.Cout), with the device pointer
+    last; the offsets the Python binding reads are the C compiler's."""
+    src = tmp_path / "o.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "bnn_model_stem.h"\n'
+                   "int main(void){ printf(\"%zu %zu %zu %zu %zu\\n\", offsetof(StemModel, n_bands),"
+                   " offsetof(StemModel, has_stem), offsetof(StemModel, stem_conv.Cout),"
+                   " offsetof(StemModel, head_bias), offsetof(StemModel, dev)); return 0; }\n")
+    exe = tmp_path / "o"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    off = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()]
+    assert off[:3] == [8, 20, 36]          # the Python binding reads ints 2, 5 and 9
+    assert off[4] == off[3] + 8            # dev is the one field past the reference's
 
 
 def test_fold_canon_matches_rules(orc):

@@ -157,3 +157,63 @@ def test_v2_roundtrip_and_header():
     bad[24:28] = (0).to_bytes(4, "little")          # has_stem = 0
     with pytest.raises(B.BlobError, match="has_stem"):
         B.from_bytes(bytes(bad))
+
+
+def test_engines_keep_their_versions(tmp_path):
+    """each loader takes its own version only, with the reference's message
+    for a v1 blob given to the v2 loader (csrc/bnn_model_stem.c:85-86)"""
+    from bnns_to_c_amd import engine
+    v1 = tmp_path / "v1.blob"
+    v1.write_bytes(B.to_bytes(synth.make_blob(seed=0, base=8)))
+    v2 = tmp_path / "v2.blob"
+    v2.write_bytes(B.to_bytes(synth.make_blob_v2(seed=1, base=8)))
+    engine.blob_check(str(v1))
+    engine.stem_blob_check(str(v2))
+    with pytest.raises(engine.BnnError, match="unsupported blob version 2.*bnn_stem_load"):
+        engine.blob_check(str(v2))
+    with pytest.raises(engine.BnnError, match="expected v2 blob, got v1"):
+        engine.stem_blob_check(str(v1))
+
+
+def _stem_corruptions():
+    data = B.to_bytes(synth.make_blob_v2(seed=2, base=8, stem=16))
+    out = [("n_stem_layers=1 supported", data[:28] + struct.pack("<i", 2) + data[32:]),
+           ("n_stem_layers=1 supported", data[:24] + struct.pack("<i", 0) + data[28:]),
+           ("short read", data[:40]),
+           ("trailing bytes", data + b"\0"),
+           ("bad conv tag", data[:32] + struct.pack("<i", 7) + data[36:])]
+    # stem conv record: <7i> + 16*120 signs + 16 alphas; its act record follows
+    a0 = 32 + 28 + 16 * 120 + 16 * 4
+    out.append(("bad act tag", data[:a0] + struct.pack("<i", 1) + data[a0 + 4:]))
+    # stem geometry the forward does not run: a 3x3 stem, pad 1
+    b = synth.make_blob_v2(seed=2, base=8, stem=16)
+    b.stem_conv = synth._real_conv(np.random.default_rng(1), 120, 16, k=3)
+    out.append(("stem does not chain", B.to_bytes(b)))
+    pad = bytearray(data)
+    pad[52:56] = struct.pack("<i", 1)
+    out.append(("stem does not chain", bytes(pad)))
+    return out
+
+
+@pytest.mark.parametrize("msg,data", _stem_corruptions(), ids=lambda v: v if isinstance(v, str) else "")
+def test_engine_stem_blob_check_rejects(msg, data, tmp_path):
+    from bnns_to_c_amd import engine
+    p = tmp_path / "bad.blob"
+    p.write_bytes(data)
+    with pytest.raises(engine.BnnError, match=msg):
+        engine.stem_blob_check(str(p))
+
+
+def test_engine_stem_rejects_broken_chain(tmp_path):
+    from bnns_to_c_amd import engine
+    b = synth.make_blob_v2(seed=3, base=8, stem=24)
+    b.enc_conv1[0] = synth._real_conv(np.random.default_rng(0), 24, 8)   # enc1.conv1 must be binary
+    p = tmp_path / "chain.blob"
+    p.write_bytes(B.to_bytes(b))
+    with pytest.raises(engine.BnnError, match="enc1.conv1 does not chain"):
+        engine.stem_blob_check(str(p))
+    b = synth.make_blob_v2(seed=3, base=8, stem=24)
+    b.stem_act = synth._int_act(np.random.default_rng(0), 24, 120, False)   # the stem fold is real
+    p.write_bytes(B.to_bytes(b))
+    with pytest.raises(engine.BnnError, match="stem does not chain"):
+        engine.stem_blob_check(str(p))
