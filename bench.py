@@ -17,6 +17,9 @@ timed between device synchronisations.  Prints ONE JSON line on stdout:
                 32x32, batch 1024 (the benchmark's fused-kernel config)
   scene         benchmark config 3: a 956x684x120 scene by 32x32 patches,
                 device-resident and from host memory (PCIe included)
+  v2_stem       the v2 spectral-stem model (16-channel 1x1 stem, then the
+                binary body) at the same batch: patches/s, and its stem
+                kernel's HBM rate against the 8 TB/s peak
   cpu_baseline  the reference C CLI (oracle/_ref/bnn_infer, built from the
                 reference sources) timed on this host: median of reps of one
                 patch, like csrc/main.c:55-61; falls back to the checker
@@ -247,6 +250,40 @@ def main() -> int:
         f"({cube.nbytes / scene_host_ms / 1e6:.1f} GB/s of input)")
     del d_cube, d_map
 
+    # the v2 spectral-stem model (csrc/bnn_model_stem.c): 16-channel stem
+    # (the reference exporter's default), base 16, same batch and input
+    bs = synth.make_blob_v2(seed=0, base=16, stem=16)
+    stem_path = os.path.join(td, "bench_stem.blob")
+    blob.write(bs, stem_path)
+    seng = engine.StemEngine(stem_path)
+
+    def sstep():
+        seng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+
+    for _ in range(args.warmup):
+        sstep()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        sstep()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    v2_ms = e0.elapsed_time(e1) / args.steps
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(args.steps):
+        sstep()
+    torch.cuda.synchronize()
+    engine.prof_enable(False)
+    stem_ms = [ms for lab, op, ms, work in engine.prof_records() if lab == "stem.conv"]
+    stem_ms = sum(stem_ms) / len(stem_ms)
+    # algorithmic bytes: every input float once, one 32-bit word of stem bits per pixel out
+    stem_bytes = N * bs.n_bands * H * W * 4 + N * H * W * 4
+    stem_rate = stem_bytes / (stem_ms / 1e3)
+    log(f"v2 stem model: {v2_ms:.4f} ms/step, {N / v2_ms * 1e3:,.0f} patches/s; stem kernel "
+        f"{stem_ms * 1e3:.1f} us, {stem_rate / 1e9:.0f} GB/s ({stem_rate / PEAK_HBM:.3f} of HBM peak)")
+    seng.close()
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -286,6 +323,10 @@ def main() -> int:
                   "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
                   "host_ms": round(scene_host_ms, 3),
                   "host_note": "host cube in, host map out: strips through pinned buffers over PCIe"},
+        "v2_stem": {"config": "v2 spectral-stem model, 16-channel 1x1 stem, base 16, 32x32x120, batch 1024",
+                    "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),
+                    "stem_kernel_us": round(stem_ms * 1e3, 2), "stem_bytes": stem_bytes,
+                    "stem_hbm_GB_s": round(stem_rate / 1e9, 1), "stem_frac": round(stem_rate / PEAK_HBM, 4)},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

@@ -454,20 +454,20 @@ int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
 
 void release(BnnDevice* D) {
   if (!D) return;
-  if (D->stream) hipStreamSynchronize(D->stream);
-  for (void* p : D->allocs) hipFree(p);
+  if (D->stream) (void)hipStreamSynchronize(D->stream);
+  for (void* p : D->allocs) (void)hipFree(p);
   D->allocs.clear();
-  if (D->ws.base) hipFree(D->ws.base);
-  if (D->stage_in) hipFree(D->stage_in);
-  if (D->stage_out) hipFree(D->stage_out);
-  if (D->copy) hipStreamSynchronize(D->copy);
+  if (D->ws.base) (void)hipFree(D->ws.base);
+  if (D->stage_in) (void)hipFree(D->stage_in);
+  if (D->stage_out) (void)hipFree(D->stage_out);
+  if (D->copy) (void)hipStreamSynchronize(D->copy);
   for (int k = 0; k < 2; ++k) {
-    if (D->pin[k]) hipHostFree(D->pin[k]);
-    if (D->ev_copied[k]) hipEventDestroy(D->ev_copied[k]);
-    if (D->ev_free[k]) hipEventDestroy(D->ev_free[k]);
+    if (D->pin[k]) (void)hipHostFree(D->pin[k]);
+    if (D->ev_copied[k]) (void)hipEventDestroy(D->ev_copied[k]);
+    if (D->ev_free[k]) (void)hipEventDestroy(D->ev_free[k]);
   }
-  if (D->copy) hipStreamDestroy(D->copy);
-  if (D->stream) hipStreamDestroy(D->stream);
+  if (D->copy) (void)hipStreamDestroy(D->copy);
+  if (D->stream) (void)hipStreamDestroy(D->stream);
   D->stream = nullptr;
 }
 
@@ -512,7 +512,7 @@ void level_dims(int H, int W, int* hs, int* wsz) {
 int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
   if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
   // a forward may still be in flight on a caller's stream
-  if (w.base) { HIP_TRY(hipDeviceSynchronize()); hipFree(w.base); w.base = nullptr; }
+  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; }
   int hs[5], ws[5];
   level_dims(H, W, hs, ws);
   std::vector<std::pair<uint32_t**, size_t>> plan;
@@ -716,7 +716,7 @@ int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_
       prof_add(ops[i].label, ops[i].optype, ops[i].oe, ops[i].taps, ms * 1e-3);
     }
   }
-  for (hipEvent_t e : evs) hipEventDestroy(e);
+  for (hipEvent_t e : evs) (void)hipEventDestroy(e);
   return rc;
 }
 
@@ -761,7 +761,7 @@ int run_scene_rows(const Model* m, const float* d_cube, int H, int W, float* d_m
       prof_add(ops[i].label, ops[i].optype, ops[i].oe, ops[i].taps, ms * 1e-3);
     }
   }
-  for (hipEvent_t e : evs) hipEventDestroy(e);
+  for (hipEvent_t e : evs) (void)hipEventDestroy(e);
   return rc;
 }
 
@@ -784,7 +784,7 @@ int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, 
   if (D->pin_cap < strip_bytes) {
     HIP_TRY(hipDeviceSynchronize());
     for (int k = 0; k < 2; ++k) {
-      if (D->pin[k]) hipHostFree(D->pin[k]);
+      if (D->pin[k]) (void)hipHostFree(D->pin[k]);
       D->pin[k] = nullptr;
     }
     D->pin_cap = 0;
@@ -828,7 +828,7 @@ int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, 
 
 int grow(float** p, size_t* cap, size_t bytes) {
   if (*cap >= bytes) return BNN_OK;
-  if (*p) { HIP_TRY(hipDeviceSynchronize()); hipFree(*p); }
+  if (*p) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(*p); }
   *p = nullptr;
   *cap = 0;
   HIP_TRY(hipMalloc((void**)p, bytes));
@@ -963,7 +963,7 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
     tmp.push_back(p);
     return p;
   };
-  auto cleanup = [&]() { for (void* p : tmp) hipFree(p); };
+  auto cleanup = [&]() { for (void* p : tmp) (void)hipFree(p); };
   d.conv1 = (float*)alloc((size_t)N * D->rcout * H * W * 4);
   for (size_t i = 0; i < pinfo.size(); ++i)
     d.P[i] = (int32_t*)alloc((size_t)N * pinfo[i].c * hs[pinfo[i].lvl] * ws[pinfo[i].lvl] * 4);

@@ -74,7 +74,7 @@ int main(int argc, char** argv) {
   std::vector<float> input(n_in);
   if (strcmp(argv[2], "rand") == 0) {
     srand(1234);
-    for (long i = 0; i < n_in; ++i) input[i] = (float)rand() / RAND_MAX * 2.0f - 1.0f;
+    for (long i = 0; i < n_in; ++i) input[i] = (float)rand() / (float)RAND_MAX * 2.0f - 1.0f;  // as csrc/main.c: RAND_MAX taken as float
   } else {
     FILE* fi = fopen(argv[2], "rb");
     if (!fi || fread(input.data(), sizeof(float), n_in, fi) != (size_t)n_in) {

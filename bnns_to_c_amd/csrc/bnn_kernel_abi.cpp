@@ -34,7 +34,7 @@ void check(hipError_t e, const char* what) {
 struct Buf {
   void* p = nullptr;
   explicit Buf(size_t bytes) { check(hipMalloc(&p, bytes ? bytes : 4), "hipMalloc"); }
-  ~Buf() { hipFree(p); }
+  ~Buf() { (void)hipFree(p); }
   template <class T>
   T* as() const { return (T*)p; }
 };

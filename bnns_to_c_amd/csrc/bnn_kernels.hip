@@ -24,6 +24,16 @@
 
 #include "bnn_kernels.h"
 
+// Multi-dword raw buffer loads, declared on the LLVM intrinsics themselves:
+// clang's __builtin_amdgcn_raw_buffer_load_b64 / _b128 keep only the first
+// dword on this toolchain (the other elements of the result repeat it).
+typedef float stem_f32x2 __attribute__((ext_vector_type(2)));
+typedef float stem_f32x4 __attribute__((ext_vector_type(4)));
+extern "C" __device__ stem_f32x2 raw_load_f32x2(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.ptr.buffer.load.v2f32");
+extern "C" __device__ stem_f32x4 raw_load_f32x4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+
 namespace bnn {
 namespace {
 
@@ -449,20 +459,58 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
 // ------------------------------------------------------------------------
 // out[co][p] = alpha[co] * (sum over ci from 0 in order of w[co][ci] * x[ci][p])
 // (csrc/bnn_conv_realin.c:140-155), then the real fold, as bits.  One
-// v_mfma_f32_16x16x1_4b_f32 per (ci, 16-channel group) advances 16 channels
-// x 64 pixels by one exact fma step (w is +1, -1 or 0, so w*x is exact and
-// fma(w, x, acc) rounds as acc + w*x does).  A wave owns 64 consecutive
-// pixels (lane l = pixel p0 + l: each ci is one coalesced 256-byte load) and
-// G channel groups; with CBSZ = 2 one weight register holds the signs of four
+// v_mfma_f32_16x16x1_4b_f32 per (ci, 16-channel group, pixel set) advances
+// 16 channels x 64 pixels by one exact fma step (w is +1, -1 or 0, so w*x is
+// exact and fma(w, x, acc) rounds as acc + w*x does).  A wave owns 64*PX
+// consecutive pixels: lane l loads pixels PX*l .. PX*l+PX-1 of each input
+// channel with one PX-dword load (the wave reads 256*PX contiguous bytes),
+// and MFMA pass p takes component p, so its B block b, column j is pixel
+// PX*(16b+j)+p.  With CBSZ = 2 one weight register holds the signs of four
 // input channels (lanes 16k..16k+15 = channel 4q+k), built from two lane
-// masks (positive, nonzero).  D register r of lane l holds pixel
-// p0 + 16*(r/4) + l%16, channel 16g + 4*(l/16) + r%4.
-constexpr int kStemQuads = 4;  // quads of input channels in flight per lane
+// masks (positive, nonzero).  D register r of lane l in pass p holds pixel
+// PX*(16*(r/4) + l%16) + p, channel 16g + 4*(l/16) + r%4.
 
-template <int G, int T>
-__device__ __forceinline__ void stem_step(f32x16 (&acc)[G], const float (&wq)[G], float xv) {
+template <int PX>
+struct StemVec;
+template <>
+struct StemVec<1> {
+  float v[1];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    v[0] = ld_f32(rs, voff, soff);
+  }
+};
+template <>
+struct StemVec<2> {
+  float v[2];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    const stem_f32x2 r = raw_load_f32x2(rs, (int)voff, (int)soff, 0);
+    v[0] = r[0];
+    v[1] = r[1];
+  }
+};
+template <>
+struct StemVec<4> {
+  float v[4];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    const stem_f32x4 r = raw_load_f32x4(rs, (int)voff, (int)soff, 0);
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(wq[g], xv, acc[g], 2, T, 0);
+    for (int i = 0; i < 4; ++i) v[i] = r[i];
+  }
+};
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>)
+template <class F, int... H>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, H...>) {
+  (f(std::integral_constant<int, H>{}), ...);
+}
+
+template <int G, int PX, int T>
+__device__ __forceinline__ void stem_step(f32x16 (&acc)[G][PX], const float (&wq)[G], const StemVec<PX>& xv) {
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int p = 0; p < PX; ++p)
+      acc[g][p] = __builtin_amdgcn_mfma_f32_16x16x1f32(wq[g], xv.v[p], acc[g][p], 2, T, 0);
 }
 
 struct alignas(16) StemMask {
@@ -482,128 +530,143 @@ __device__ __forceinline__ void stem_weights(const uint64_t* __restrict__ wm, in
   }
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void k_stem_mfma(const RealArgs a, uint32_t xbytes, int ngp) {
+// G channel groups per wave, PX pixels per lane, NQ quads of input channels
+// in flight per lane, registers sized for OCC waves per SIMD; DUMP also
+// stores the conv output as floats (a.f32).  The host guarantees that a
+// lane's PX pixels lie in one row of one patch and inside or outside the
+// input together.
+template <int G, int PX, int NQ, int OCC, bool DUMP>
+__global__ __launch_bounds__(256, OCC) void k_stem_mfma(const RealArgs a, uint32_t xbytes, int ngp) {
   const int lane = threadIdx.x & 63;
   const int ny = ngp / G;  // channel-group blocks per pixel tile
   const long tile = (long)(blockIdx.x / ny) * 4 + (threadIdx.x >> 6);
   const int g0 = (int)(blockIdx.x % ny) * G;
   const int HW = a.H * a.W;
   const long npix = (long)a.N * HW;
-  const long q = tile * 64 + lane;  // this lane's pixel in [N][H*W]
+  const long t0 = tile * 64 * PX;   // first pixel of the wave
+  const long q = t0 + PX * lane;    // this lane's first pixel in [N][H*W]
   const bool live = q < npix;
   const int n = live ? (int)(q / HW) : 0;
-  const int p = live ? (int)(q - (long)n * HW) : 0;
-  const int py = p / a.W, px = p - py * a.W;
+  const int pp = live ? (int)(q - (long)n * HW) : 0;
+  const int py = pp / a.W, px = pp - py * a.W;
   const InGeom ig = in_geom(a, n);
   const bool inside = live && py < ig.ylim && px < ig.xlim;
   const uint32_t voff = inside ? (uint32_t)(ig.base + (size_t)py * ig.rstride + px) * 4u : 0x80000000u;
   const uint32_t cbytes = (uint32_t)(ig.cstride * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
 
-  f32x16 acc[G];
+  f32x16 acc[G][PX];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[g][r] = 0.0f;
-
-  // Channel c sits in slot c % 16 of xr; a slot is refilled (16 channels
-  // ahead) right after its step has read it.  Loads run unguarded: a
-  // channel at or past cin is the next image's data or past the buffer
-  // (read as 0), and only the guarded tail quad can meet it.
-  constexpr int kAhead = 4 * kStemQuads;
-  float xr[kAhead];
+    for (int p = 0; p < PX; ++p)
 #pragma unroll
-  for (int k = 0; k < kAhead; ++k) xr[k] = ld_f32(rs, voff, (uint32_t)k * cbytes);
+      for (int r = 0; r < 16; ++r) acc[g][p][r] = 0.0f;
+
+  // Channel c sits in slot c % (4*NQ) of xr; a slot is refilled (4*NQ
+  // channels ahead) right after its step has read it.  Loads run unguarded:
+  // a channel at or past cin is the next image's data or past the buffer
+  // (read as 0), and only the guarded tail quad can meet it.
+  constexpr int kAhead = 4 * NQ;
+  StemVec<PX> xr[kAhead];
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) xr[k].load(rs, voff, (uint32_t)k * cbytes);
   const int qf = a.cin >> 2, rem = a.cin & 3;
   auto quad = [&](auto hc, int qq) {
     constexpr int h = decltype(hc)::value;
     float wq[G];
     stem_weights<G>(a.wm, qq, ngp, g0, wq);
-    stem_step<G, 0>(acc, wq, xr[4 * h + 0]);
-    stem_step<G, 1>(acc, wq, xr[4 * h + 1]);
-    stem_step<G, 2>(acc, wq, xr[4 * h + 2]);
-    stem_step<G, 3>(acc, wq, xr[4 * h + 3]);
+    stem_step<G, PX, 0>(acc, wq, xr[4 * h + 0]);
+    stem_step<G, PX, 1>(acc, wq, xr[4 * h + 1]);
+    stem_step<G, PX, 2>(acc, wq, xr[4 * h + 2]);
+    stem_step<G, PX, 3>(acc, wq, xr[4 * h + 3]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) xr[4 * h + k] = ld_f32(rs, voff, (uint32_t)(4 * qq + k + kAhead) * cbytes);
+    for (int k = 0; k < 4; ++k) xr[4 * h + k].load(rs, voff, (uint32_t)(4 * qq + k + kAhead) * cbytes);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto tail = [&](auto hc, int qq) {
     constexpr int h = decltype(hc)::value;
     float wq[G];
     stem_weights<G>(a.wm, qq, ngp, g0, wq);
-    stem_step<G, 0>(acc, wq, xr[4 * h]);
-    if (rem > 1) stem_step<G, 1>(acc, wq, xr[4 * h + 1]);
-    if (rem > 2) stem_step<G, 2>(acc, wq, xr[4 * h + 2]);
+    stem_step<G, PX, 0>(acc, wq, xr[4 * h]);
+    if (rem > 1) stem_step<G, PX, 1>(acc, wq, xr[4 * h + 1]);
+    if (rem > 2) stem_step<G, PX, 2>(acc, wq, xr[4 * h + 2]);
   };
   int qi = 0;
 #pragma unroll 1
-  for (; qi + kStemQuads <= qf; qi += kStemQuads) {
-    quad(std::integral_constant<int, 0>{}, qi);
-    quad(std::integral_constant<int, 1>{}, qi + 1);
-    quad(std::integral_constant<int, 2>{}, qi + 2);
-    quad(std::integral_constant<int, 3>{}, qi + 3);
-  }
-  // the last qf % 4 full quads, then the partial quad (cin % 4 channels)
-  auto finish = [&](auto hc) {
-    constexpr int h = decltype(hc)::value;
-    if (qi + h < qf) quad(hc, qi + h);
-    else if (qi + h == qf && rem) tail(hc, qi + h);
-  };
-  finish(std::integral_constant<int, 0>{});
-  finish(std::integral_constant<int, 1>{});
-  finish(std::integral_constant<int, 2>{});
-  finish(std::integral_constant<int, 3>{});
+  for (; qi + NQ <= qf; qi += NQ)
+    static_for([&](auto hc) { quad(hc, qi + decltype(hc)::value); }, std::make_integer_sequence<int, NQ>{});
+  // the last qf % NQ full quads, then the partial quad (cin % 4 channels)
+  static_for(
+      [&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        if (qi + h < qf) quad(hc, qi + h);
+        else if (qi + h == qf && rem) tail(hc, qi + h);
+      },
+      std::make_integer_sequence<int, NQ>{});
 
   // alpha, the real fold (csrc/bnn_fold.c:62-77, A*x+B fused as in the
   // reference build), bits gathered across the four lane groups
   const int cwo = (a.cout + 31) >> 5;
   const int ngrp = (a.cout + 15) >> 4;
+  constexpr int NW = 2 * PX;  // 32-bit words of bits per lane and group
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int gg = g0 + g;
     if (gg >= ngrp) break;
     const int cq = gg * 16 + 4 * (lane >> 4);
-    uint32_t w01 = 0, w23 = 0;
+    // pixel (b, p) = PX*(16b + l%16) + p: 16 bits at 16*((b*PX+p) % 2) of word (b*PX+p) / 2
+    uint32_t wb[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) wb[i] = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int co = cq + k;
       const int cc = min(co, a.cout - 1);
       const float al = a.alpha[cc];
+      const float fA = a.A[cc], fB = a.B[cc], fs = a.slope[cc], fr = a.rsign[cc];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float o = __fmul_rn(al, acc[g][4 * b + k]);
-        const long qp = tile * 64 + 16 * b + (lane & 15);
-        if (a.f32 && qp < npix && co < a.cout) {
-          const long nn = qp / HW;
-          a.f32[((size_t)nn * a.cout + co) * HW + (qp - nn * HW)] = o;
-        }
-        if (a.out) {
-          float z = __fmaf_rn(a.A[cc], o, a.B[cc]);
-          if (z < 0.0f) z = __fmul_rn(a.slope[cc], z);
-          const float rr = __fadd_rn(z, a.rsign[cc]);
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int p = 0; p < PX; ++p) {
+          const float o = __fmul_rn(al, acc[g][p][4 * b + k]);
+          const long qp = t0 + PX * (16 * b + (lane & 15)) + p;
+          if (DUMP && qp < npix && co < a.cout) {
+            const long nn = qp / HW;
+            a.f32[((size_t)nn * a.cout + co) * HW + (qp - nn * HW)] = o;
+          }
+          float z = __fmaf_rn(fA, o, fB);
+          if (z < 0.0f) z = __fmul_rn(fs, z);
+          const float rr = __fadd_rn(z, fr);
           const uint32_t bit = (rr > 0.0f && co < a.cout) ? 1u : 0u;
-          const int sh = 16 * (b & 1) + 4 * (lane >> 4) + k;
-          if (b < 2) w01 |= bit << sh;
-          else w23 |= bit << sh;
+          const int i = b * PX + p;
+          wb[i / 2] |= bit << (16 * (i % 2) + 4 * (lane >> 4) + k);
         }
-      }
     }
     if (!a.out) continue;
-    w01 |= (uint32_t)__shfl_xor((int)w01, 16);
-    w01 |= (uint32_t)__shfl_xor((int)w01, 32);
-    w23 |= (uint32_t)__shfl_xor((int)w23, 16);
-    w23 |= (uint32_t)__shfl_xor((int)w23, 32);
-    // lane group b stores pixel p0 + 16b + l%16: 16 bits at bit 16*(gg%2)
-    // of word gg/2; the last group of an odd count writes its whole word
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      wb[i] |= (uint32_t)__shfl_xor((int)wb[i], 16);
+      wb[i] |= (uint32_t)__shfl_xor((int)wb[i], 32);
+    }
+    // lane group b stores pixels PX*(16b + l%16) + p: 16 bits at bit
+    // 16*(gg%2) of word gg/2; the last group of an odd count writes its whole word
     const int b = lane >> 4;
-    const uint32_t word = ((b < 2 ? w01 : w23) >> (16 * (b & 1))) & 0xFFFFu;
-    const long qp = tile * 64 + 16 * b + (lane & 15);
-    if (qp >= npix) continue;
-    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + (size_t)qp * cwo) + gg * 2;
-    if ((gg & 1) == 0 && gg == ngrp - 1) *reinterpret_cast<uint32_t*>(dst) = word;
-    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+#pragma unroll
+    for (int p = 0; p < PX; ++p) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int i = bb * PX + p;
+        if (b == bb) word = (wb[i / 2] >> (16 * (i % 2))) & 0xFFFFu;
+      }
+      const long qp = t0 + PX * (16 * b + (lane & 15)) + p;
+      if (qp >= npix) continue;
+      uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + (size_t)qp * cwo) + gg * 2;
+      if ((gg & 1) == 0 && gg == ngrp - 1) *reinterpret_cast<uint32_t*>(dst) = word;
+      else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+    }
   }
 }
 
@@ -1157,24 +1220,55 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s) {
 
 int stem_groups_per_wave(int cout) { return std::min(4, (cout + 15) / 16); }
 
+#ifndef BNN_STEM_NQ4
+#define BNN_STEM_NQ4 1  // quads in flight at 4 pixels per lane
+#endif
+#ifndef BNN_STEM_OCC4
+#define BNN_STEM_OCC4 4  // waves per SIMD at 4 pixels per lane
+#endif
+#ifndef BNN_STEM_PX1
+#define BNN_STEM_PX1 2  // pixels per lane with one channel group per wave
+#endif
+#ifndef BNN_STEM_PX2
+#define BNN_STEM_PX2 1  // pixels per lane with two channel groups per wave
+#endif
+
+template <int G, int PX>
+void launch_stem_t(const RealArgs& a, uint32_t xbytes, int ngp, hipStream_t s) {
+  constexpr int NQ = PX == 4 ? BNN_STEM_NQ4 : 4;
+  constexpr int OCC = G * PX == 1 ? 5 : PX == 4 ? BNN_STEM_OCC4 : 3;
+  constexpr int OCCD = OCC < 3 ? OCC : 3;  // the debug variant's float stores need registers
+  const long npix = (long)a.N * a.H * a.W;
+  const dim3 grid((unsigned)((npix + 256 * PX - 1) / (256 * PX) * (ngp / G)));
+  if (a.f32) hipLaunchKernelGGL((k_stem_mfma<G, PX, NQ, OCCD, true>), grid, dim3(256), 0, s, a, xbytes, ngp);
+  else hipLaunchKernelGGL((k_stem_mfma<G, PX, NQ, OCC, false>), grid, dim3(256), 0, s, a, xbytes, ngp);
+}
+
 hipError_t launch_stem(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   // offsets stay below 2^31 even for the channels read ahead past cin, so
   // a lane outside the image (base offset 2^31) always reads past the buffer
   const size_t cstride = a.pcols > 0 ? (size_t)a.sH * a.sW : (size_t)a.H * a.W;
-  if (xbytes + (size_t)(4 * kStemQuads + 4) * 4 * cstride >= 0x80000000ull || !a.wm || a.cin < 1)
+  if (xbytes + (size_t)(4 * 4 + 4) * 4 * cstride >= 0x80000000ull || !a.wm || a.cin < 1)
     return hipErrorInvalidValue;
-  const long npix = (long)a.N * a.H * a.W;
-  const long blocks_px = (npix + 255) / 256;
   const int G = stem_groups_per_wave(a.cout);
   const int ngp = stem_groups_padded(a.cout);
-  const unsigned grid = (unsigned)(blocks_px * (ngp / G));
-  switch (G) {
-    case 1: hipLaunchKernelGGL(k_stem_mfma<1>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
-    case 2: hipLaunchKernelGGL(k_stem_mfma<2>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
-    case 3: hipLaunchKernelGGL(k_stem_mfma<3>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
-    default: hipLaunchKernelGGL(k_stem_mfma<4>, dim3(grid), dim3(256), 0, s, a, (uint32_t)xbytes, ngp); break;
+  // pixels per lane: a lane's pixels must share a patch row and lie inside
+  // or outside the input together (patch widths and, for scenes, the scene
+  // width are multiples of PX)
+  auto fits = [&](int px) { return a.W % px == 0 && (a.pcols == 0 || a.sW % px == 0); };
+  int PX = G == 1 ? BNN_STEM_PX1 : G == 2 ? BNN_STEM_PX2 : 1;
+  while (PX > 1 && !fits(PX)) PX /= 2;
+  const uint32_t xb = (uint32_t)xbytes;
+  switch (G * 8 + PX) {
+    case 1 * 8 + 4: launch_stem_t<1, 4>(a, xb, ngp, s); break;
+    case 1 * 8 + 2: launch_stem_t<1, 2>(a, xb, ngp, s); break;
+    case 1 * 8 + 1: launch_stem_t<1, 1>(a, xb, ngp, s); break;
+    case 2 * 8 + 2: launch_stem_t<2, 2>(a, xb, ngp, s); break;
+    case 2 * 8 + 1: launch_stem_t<2, 1>(a, xb, ngp, s); break;
+    case 3 * 8 + 1: launch_stem_t<3, 1>(a, xb, ngp, s); break;
+    default: launch_stem_t<4, 1>(a, xb, ngp, s); break;
   }
   return hipGetLastError();
 }
