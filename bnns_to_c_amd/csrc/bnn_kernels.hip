@@ -283,17 +283,30 @@ __device__ __forceinline__ void mfma_taps(f32x16 (&acc)[9], const float (&wa)[3]
 #ifndef BNN_MWPE
 #define BNN_MWPE 2
 #endif
-template <int WR, int WC>  // waves along rows / columns: tile (4*WR) x (16*WC)
+// an offset past any input of the matrix-core real conv (inputs are smaller)
+constexpr uint32_t kRealFar = 0x7FFFFFF0u;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// waves along rows / columns: tile (4*WR) x (16*WC); PARTIAL: cin is not a
+// multiple of the chunk size
+template <int WR, int WC, bool PARTIAL>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(BNN_MWPE)))
 void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
-  constexpr int TR = 4 * WR, TC = 16 * WC, NT = 64 * WR * WC;
+  constexpr int TR = 4 * WR, TC = 16 * WC, NW = WR * WC;
   constexpr int CI = kRealMfmaCI;  // input channels per LDS chunk
-  // LDS rows are padded to LC = 16 (mod 32) floats: the four 16-lane rows of
-  // a wave's B read then fall in disjoint banks
-  constexpr int LR = TR + 2, LW = TC + 2, LC = (LW + 15) / 32 * 32 + 16, LPL = LR * LC;
-  constexpr int LE = CI * LR * LW;  // tile elements loaded per chunk
-  constexpr int KL = (LE + NT - 1) / NT;
-  __shared__ float tile[2][CI * LPL];  // [ci][row][col], zero outside the image
+  // A chunk is CI x LR rows of the input tile (LW = TC + 2 columns with the
+  // halo).  Each row is filled by one buffer load that writes LDS (lane l
+  // lands at the load's LDS base + 4*l, so a row takes 64 slots); rows are
+  // LC = 80 floats apart, 16 (mod 32), so the four 16-lane rows of a wave's
+  // B read fall in disjoint banks.
+  constexpr int LR = TR + 2, LW = TC + 2, LC = 80, LPL = LR * LC;
+  static_assert(LW <= 64, "a tile row must fit one 64-lane load");
+  constexpr int NROW = CI * LR;             // row loads per chunk
+  constexpr int KR = NROW / NW;  // row loads per wave
+  static_assert(NROW % NW == 0, "every wave issues the same number of row loads");
+  // Three buffers: chunk ch is read from one while ch+1 has landed in the
+  // next and ch+2 is in flight into the third.
+  __shared__ float tile0[CI * LPL], tile1[CI * LPL], tile2[CI * LPL];  // [ci][row][col]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = (wv / WC) * 4, wc = (wv % WC) * 16;
@@ -305,47 +318,68 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   const int y0 = ty * TR, x0 = tx * TC;
   const int g = blockIdx.y;  // 16-channel group
   const int HW = a.H * a.W;
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
-  // the lane's four output channels (16g + 4*(lane/16) + k) and their alpha
-  // and fold parameters, fetched now so the epilogue does not wait on them
-  // (the parameter arrays are padded to 32 channels)
+  // the lane's four output channels: 16g + 4*(lane/16) + k
   const int cq = g * 16 + 4 * (lane >> 4);
-  float p_al[4], p_A[4], p_B[4], p_sl[4], p_rs[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    p_al[k] = a.alpha[cq + k];
-    if (a.out) {
-      p_A[k] = a.A[cq + k];
-      p_B[k] = a.B[cq + k];
-      p_sl[k] = a.slope[cq + k];
-      p_rs[k] = a.rsign[cq + k];
-    }
-  }
 
-  // this thread's share of every chunk: tile element e = tid + k*NT, its
-  // byte offset in the chunk (or an offset past the buffer, which reads 0,
-  // outside the image) and its LDS slot.  Channels past cin in the last
-  // chunk also read 0: a product w * 0 adds +-0 to a chain that never holds
+  // Row load (ci, r) of chunk ch reads input channel ch*CI + ci, image row
+  // y0 - 1 + r: the lane part of its byte offset is the column, the rest is
+  // scalar.  A column outside the image or past the halo gets the lane
+  // offset kFar, a row outside the image (or a channel past cin in the last
+  // chunk) the scalar offset kFar: with the input under kFar bytes either
+  // sum lies past the buffer (both together stay below 2^32), so those
+  // positions read 0.  A product w * 0 adds +-0 to a chain that never holds
   // -0, which leaves it unchanged, so every chunk runs all CI channels.
   const InGeom ig = in_geom(a, n);
-  uint32_t goff[KL];
-  int lidx[KL];
-#pragma unroll
-  for (int k = 0; k < KL; ++k) {
-    const int e = tid + k * NT;
-    const int cil = e / (LR * LW), rem = e - cil * (LR * LW);
-    const int row = rem / LW, col = rem - row * LW;
-    const int gy = y0 - 1 + row, gx = x0 - 1 + col;
-    const bool ok = e < LE && gy >= 0 && gy < ig.ylim && gx >= 0 && gx < ig.xlim;
-    goff[k] = ok ? (uint32_t)(ig.base + cil * ig.cstride + (size_t)gy * ig.rstride + gx) * 4u : 0x80000000u;
-    lidx[k] = e < LE ? cil * LPL + row * LC + col : 0;
-  }
-  const uint32_t chunk_bytes = (uint32_t)(CI * ig.cstride * 4u);
+  const int gx = x0 - 1 + lane;
+  const uint32_t vo_lane =
+      (lane < LW && gx >= 0 && gx < ig.xlim) ? (uint32_t)(ig.base + (size_t)gx) * 4u : kRealFar;
+  const uint32_t cs4 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ig.cstride * 4u));
+  const uint32_t rs4 = (uint32_t)__builtin_amdgcn_readfirstlane(ig.rstride * 4);
+  // tile rows [rlo, rhi) lie inside the image
+  const int rlo = y0 == 0 ? 1 : 0;
+  const int rhi = min(LR, __builtin_amdgcn_readfirstlane(ig.ylim) - y0 + 1);
   const int nchunk = (a.cin + CI - 1) / CI;
-  // byte offset of element k in chunk ch, 0x80000000 for a channel past cin
-  auto chunk_off = [&](int k, int ch) -> uint32_t {
-    const int cil = (tid + k * NT) / (LR * LW);
-    return ch * CI + cil < a.cin ? goff[k] + (uint32_t)ch * chunk_bytes : 0x80000000u;
+  typedef __attribute__((address_space(3))) float* lds_f32;
+  // the three chunk buffers by compile-time index (distinct variables, so
+  // the compiler can tell a buffer being read from one being filled)
+  auto bufp = [&](auto bc) -> float* {
+    constexpr int B = decltype(bc)::value;
+    if constexpr (B == 0) return tile0;
+    else if constexpr (B == 1) return tile1;
+    else return tile2;
+  };
+  // wave wv fills the KR / LR channels [wv*KR/LR, ...) of the chunk
+  static_assert(KR % LR == 0, "a wave's row loads cover whole channels");
+  // The LDS-writing loads are issued from inline assembly, so the compiler
+  // does not track them: its own wait placement assumes any pending LDS
+  // write may alias any LDS read and would wait for the chunk after next
+  // before reading this one.  The waits for them are explicit (step).
+  const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
+  const u32x4 rsrc = {(uint32_t)xaddr, (uint32_t)(xaddr >> 32) & 0xFFFFu, xbytes, 0x00020000u};
+  auto issue = [&](auto bc, int ch) {
+    // the row arithmetic stays here rather than being hoisted out of the
+    // chunk loop, where its 3 x KR scalars would not fit in registers
+    int cw0 = wv * (KR / LR);
+    asm volatile("" : "+s"(cw0));
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_f32)(bufp(bc)) + (uint32_t)(cw0 * LPL * 4);
+#pragma unroll
+    for (int j = 0; j < KR / LR; ++j) {
+      const int cin_j = ch * CI + cw0 + j;  // input channel of these rows
+      const bool chan_ok = !PARTIAL || cin_j < a.cin;
+      const uint32_t cbase = (uint32_t)cin_j * cs4 + (uint32_t)(y0 - 1) * rs4;
+#pragma unroll
+      for (int r = 0; r < LR; ++r) {
+        const bool ok = chan_ok && r >= rlo && r < rhi;
+        const uint32_t soff = ok ? cbase + (uint32_t)r * rs4 : kRealFar;
+        const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + (uint32_t)((j * LPL + r * LC) * 4)));
+        const uint32_t vl = vo_lane;
+        const u32x4 rd = rsrc;
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                     :
+                     : "s"(m0v), "v"(vl), "s"(rd), "s"(soff)
+                     : "memory");
+      }
+    }
   };
 
   f32x16 acc[9];
@@ -354,29 +388,19 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
-  float pre[KL];
-#pragma unroll
-  for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, chunk_off(k, 0), 0);
-#pragma unroll
-  for (int k = 0; k < KL; ++k)
-    if (tid + k * NT < LE) tile[0][lidx[k]] = pre[k];
-  __syncthreads();
-
-  const uint64_t* wm = a.wm + (size_t)g * nchunk * CI * 3;
+  // the weight masks through the constant address space: the kernel never
+  // writes them, and saying so keeps their loads scalar next to the
+  // LDS-writing buffer loads
+  typedef const __attribute__((address_space(4))) uint64_t* const_u64;
+  const_u64 wm = (const_u64)a.wm + (size_t)g * nchunk * CI * 3;
   const int lb = (wr + (lane >> 4)) * LC + wc + (lane & 15);
-#pragma unroll 1
-  for (int ch = 0; ch < nchunk; ++ch) {
-    const int buf = ch & 1;
-    const bool more = ch + 1 < nchunk;
-    if (more) {
-#pragma unroll
-      for (int k = 0; k < KL; ++k) pre[k] = ld_f32(rs, chunk_off(k, ch + 1), 0);
-    }
+  // One chunk of CI channels on the matrix cores.  The chunk's weight masks
+  // arrive in one scalar batch; channel cl+1's inputs are read while channel
+  // cl's nine products run (the scheduling barriers keep the compiler from
+  // moving the reads next to their use).
+  auto run_chunk = [&](auto bc, int ch) {
     const int ci0 = ch * CI;
-    const float* tb = tile[buf] + lb;
-    // the chunk's weight masks arrive in one scalar batch; channel cl+1's
-    // inputs are read while channel cl's nine products run (the scheduling
-    // barriers keep the compiler from moving the reads next to their use)
+    const float* tb = bufp(bc) + lb;
     uint64_t mk[CI][3];
 #pragma unroll
     for (int cl = 0; cl < CI; ++cl)
@@ -398,12 +422,68 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
       mfma_taps(acc, wa, xb[cl & 1], std::make_integer_sequence<int, 9>{});
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
+  };
+  // The chunk barrier: this wave's own waits (below) make its LDS-writing
+  // loads complete, and every LDS read of the chunk has fed an MFMA before
+  // the barrier, so no memory fence is needed (a fence would wait for the
+  // loads still in flight for the chunk after next); the signal fences keep
+  // the compiler from moving LDS accesses across it.
+  auto chunk_barrier = [] {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  // s_waitcnt with vmcnt <= KR or 0 (expcnt and lgkmcnt left alone)
+  constexpr int kWaitKD = (KR & 15) | ((KR >> 4) << 14) | (7 << 4) | (15 << 8);
+  constexpr int kWait0 = (7 << 4) | (15 << 8);
+  static_assert(KR < 64, "vmcnt holds at most 63");
+  // Chunk ch from buffer B; chunk ch+2, if any, is fetched into buffer
+  // B+2 (mod 3), last read as chunk ch-1, which every wave finished before
+  // the last barrier.  Then this wave's loads of chunk ch+1, issued one step
+  // earlier, are waited for (only the KR loads of chunk ch+2 may remain) and
+  // the barrier makes every wave's loads visible.
+  auto step = [&](auto bc, int ch) {
+    constexpr int B = decltype(bc)::value;
+    const bool ahead = ch + 2 < nchunk;
+    if (ahead) issue(std::integral_constant<int, (B + 2) % 3>{}, ch + 2);
+    run_chunk(bc, ch);
+    if (ahead) __builtin_amdgcn_s_waitcnt(kWaitKD);
+    else __builtin_amdgcn_s_waitcnt(kWait0);
+    chunk_barrier();
+  };
+  issue(std::integral_constant<int, 0>{}, 0);
+  if (nchunk > 1) {
+    issue(std::integral_constant<int, 1>{}, 1);
+    __builtin_amdgcn_s_waitcnt(kWaitKD);
+  } else {
+    __builtin_amdgcn_s_waitcnt(kWait0);
+  }
+  chunk_barrier();
+  // chunk c lives in buffer c % 3
+  int ch = 0;
+#pragma unroll 1
+  for (; ch + 3 <= nchunk; ch += 3) {
+    step(std::integral_constant<int, 0>{}, ch);
+    step(std::integral_constant<int, 1>{}, ch + 1);
+    step(std::integral_constant<int, 2>{}, ch + 2);
+  }
+  if (ch < nchunk) {
+    step(std::integral_constant<int, 0>{}, ch);
+    if (ch + 1 < nchunk) step(std::integral_constant<int, 1>{}, ch + 1);
+  }
+
+  // alpha and fold parameters of the lane's four channels (the arrays are
+  // padded to 32 channels)
+  float p_al[4], p_A[4], p_B[4], p_sl[4], p_rs[4];
 #pragma unroll
-      for (int k = 0; k < KL; ++k)
-        if (tid + k * NT < LE) tile[buf ^ 1][lidx[k]] = pre[k];
+  for (int k = 0; k < 4; ++k) {
+    p_al[k] = a.alpha[cq + k];
+    if (a.out) {
+      p_A[k] = a.A[cq + k];
+      p_B[k] = a.B[cq + k];
+      p_sl[k] = a.slope[cq + k];
+      p_rs[k] = a.rsign[cq + k];
     }
-    __syncthreads();
   }
 
   // taps in row-major order into acc (an out-of-image tap summed zeros to
@@ -1195,10 +1275,16 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s) {
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
   if (a.wm) {
+    if (xbytes >= kRealFar) return hipErrorInvalidValue;
     constexpr int WR = BNN_MWR, WC = BNN_MWC;
     const int tilesH = (a.H + 4 * WR - 1) / (4 * WR), tilesW = (a.W + 16 * WC - 1) / (16 * WC);
     dim3 grid((unsigned)((long)a.N * tilesH * tilesW), (unsigned)((a.cout + 15) / 16));
-    hipLaunchKernelGGL((k_real_mfma<WR, WC>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH, tilesW);
+    if (a.cin % kRealMfmaCI)
+      hipLaunchKernelGGL((k_real_mfma<WR, WC, true>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH,
+                         tilesW);
+    else
+      hipLaunchKernelGGL((k_real_mfma<WR, WC, false>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH,
+                         tilesW);
     return hipGetLastError();
   }
   const int tilesH = (a.H + RT - 1) / RT, tilesW = (a.W + RW - 1) / RW;
