@@ -772,27 +772,42 @@ struct Acc {
 };
 
 // D[p][j] += sum over taps popcount((a ^ w) & m) for one 32-channel word.
+// The weights of JB channels (9 words each, wave-uniform) are fetched as
+// one batch of scalar loads before their products: fetched channel by
+// channel, each would wait for its own load.
+#ifndef BNN_BJB
+#define BNN_BJB 4
+#endif
 template <int MT, int COG>
 __device__ __forceinline__ void accumulate(Acc<MT, COG>& D, const uint32_t (&av)[MT + 2][MT + 2],
                                            const uint32_t (&m)[MT + 2][MT + 2],
                                            const uint32_t* __restrict__ wrow) {
+  constexpr int JB = COG < BNN_BJB ? COG : BNN_BJB;
+  typedef const __attribute__((address_space(4))) uint32_t* const_u32;
+  const const_u32 wr = (const_u32)wrow;
 #pragma unroll
-  for (int j = 0; j < COG; ++j) {
-    uint32_t w9[9];
+  for (int j0 = 0; j0 < COG; j0 += JB) {
+    uint32_t w9[JB][9];
 #pragma unroll
-    for (int t = 0; t < 9; ++t) w9[t] = wrow[j * 9 + t];
+    for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
-    for (int py = 0; py < MT; ++py)
+      for (int t = 0; t < 9; ++t) w9[jj][t] = wr[(j0 + jj) * 9 + t];
 #pragma unroll
-      for (int px = 0; px < MT; ++px) {
-        uint32_t d = D.d[py * MT + px][j];
+    for (int jj = 0; jj < JB; ++jj) {
+      const int j = j0 + jj;
 #pragma unroll
-        for (int ky = 0; ky < 3; ++ky)
+      for (int py = 0; py < MT; ++py)
 #pragma unroll
-          for (int kx = 0; kx < 3; ++kx)
-            d = bcnt_acc((av[py + ky][px + kx] ^ w9[ky * 3 + kx]) & m[py + ky][px + kx], d);
-        D.d[py * MT + px][j] = d;
-      }
+        for (int px = 0; px < MT; ++px) {
+          uint32_t d = D.d[py * MT + px][j];
+#pragma unroll
+          for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx)
+              d = bcnt_acc((av[py + ky][px + kx] ^ w9[jj][ky * 3 + kx]) & m[py + ky][px + kx], d);
+          D.d[py * MT + px][j] = d;
+        }
+    }
   }
 }
 
@@ -805,30 +820,22 @@ __device__ __forceinline__ void load_window(uint32_t (&av)[NP][NP], __amdgpu_buf
     for (int k = 0; k < NP; ++k) av[i][k] = ld_u32(rs, vo[i][k], soff);
 }
 
-// Sum one input segment (cw words per pixel) into D.  Two windows
-// alternate so that the next word's loads are in flight while the current
-// word is consumed.  The loads are unconditional (a conditional load makes
-// the compiler wait for every outstanding load before the next use), so the
-// last pair also fetches the word after the segment: the pixel's next word,
-// the next pixel's first word, or past the end of the buffer, which reads 0.
-// That word is never used.
+// Sum one input segment (cw words per pixel) into D, one word's window at
+// a time: the waves of a launch overlap each other's load latency (measured
+// faster than keeping further words in flight in each wave, which costs
+// registers and, for one-word inputs, wasted loads).
 template <int MT, int COG>
 __device__ __forceinline__ void conv_segment(Acc<MT, COG>& D, __amdgpu_buffer_rsrc_t rs,
                                              const uint32_t (&vo)[MT + 2][MT + 2],
                                              const uint32_t (&m)[MT + 2][MT + 2], int cw,
                                              const uint32_t* __restrict__ wt, int rowstride) {
   constexpr int NP = MT + 2;
-  uint32_t wa[NP][NP], wb[NP][NP];
-  load_window<NP>(wa, rs, vo, 0u);
-  int w = 0;
+  uint32_t win[NP][NP];
 #pragma unroll 1
-  for (; w + 1 < cw; w += 2) {
-    load_window<NP>(wb, rs, vo, (uint32_t)(w + 1) * 4u);
-    accumulate<MT, COG>(D, wa, m, wt + (size_t)w * rowstride);
-    load_window<NP>(wa, rs, vo, (uint32_t)(w + 2) * 4u);
-    accumulate<MT, COG>(D, wb, m, wt + (size_t)(w + 1) * rowstride);
+  for (int w = 0; w < cw; ++w) {
+    load_window<NP>(win, rs, vo, (uint32_t)w * 4u);
+    accumulate<MT, COG>(D, win, m, wt + (size_t)w * rowstride);
   }
-  if (w < cw) accumulate<MT, COG>(D, wa, m, wt + (size_t)w * rowstride);
 }
 
 // Store the COG bits of one channel group.  A group that alone covers its
