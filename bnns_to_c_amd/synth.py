@@ -178,3 +178,51 @@ def make_thresholds(seed: int, c: int, bound: int):
     ty = np.where(rng.random(c) < 0.5, B.RULE_GE, B.RULE_LT).astype(np.int32)
     z = np.zeros(c, np.int32)
     return ty, t, z, z.copy()
+
+
+# ------------------------------------------- trained-parameter generator --
+def make_params(seed: int = 0, base: int = 8, n_bands: int = 120, n_classes: int = 3,
+                stem: int = 0) -> dict:
+    """Float parameters in the layout bnns_to_c_amd.fold reads: N(0,1)
+    conv weights (a few exact zeros), and per chain a BatchNorm, RPReLU
+    move1, PReLU slope and RSign bias drawn so that every rule kind occurs:
+    some negative gammas (lt), negative slopes (bands), offsets large
+    enough for constants.  stem > 0 adds a v2 stem of that many channels."""
+    rng = np.random.default_rng(seed)
+    p = {}
+
+    def conv(name, cin, cout, k=3):
+        w = rng.standard_normal((cout, cin, k, k)).astype(np.float32)
+        w.reshape(-1)[rng.choice(w.size, max(1, w.size // 500), replace=False)] = 0.0
+        p[f"{name}.weight"] = w
+        return float(np.abs(w).mean()) * np.sqrt(cin * k * k)   # typical |alpha * P|
+
+    def act(name, c, spread):
+        g = rng.uniform(0.5, 1.5, c).astype(np.float32)
+        g[rng.random(c) < 0.2] *= -1
+        p[f"{name}.bn.weight"] = g
+        p[f"{name}.bn.bias"] = rng.normal(0, 0.3, c).astype(np.float32)
+        m = rng.normal(0, 0.5 * spread, c).astype(np.float32)
+        m[rng.random(c) < 0.05] = np.float32(5 * spread)            # saturates: a constant
+        p[f"{name}.bn.running_mean"] = m
+        p[f"{name}.bn.running_var"] = rng.uniform(0.5, 2.0, c).astype(np.float32) * np.float32(spread * spread)
+        p[f"{name}.move1"] = rng.normal(0, 0.1, c).astype(np.float32)
+        p[f"{name}.prelu"] = rng.uniform(-0.6, 1.0, c).astype(np.float32)
+        p[f"{name}.rsign"] = rng.normal(0, 0.3, c).astype(np.float32)
+
+    if stem:
+        s = conv("stem.conv", n_bands, stem, k=1)
+        act("stem.act", stem, s)
+    acts = {"conv1": ["act1"], "conv2": ["act2"]}
+    for name, ci, co in topology(base, n_bands):
+        st, cv = name.split(".")
+        st = "bottleneck" if st == "bott" else st
+        if name == "enc1.conv1" and stem:
+            ci = stem
+        s = conv(f"{st}.{cv}", ci, co)
+        names = ["act2_skip", "act2_down"] if st.startswith("enc") and cv == "conv2" else acts[cv]
+        for a in names:
+            act(f"{st}.{a}", co, s)
+    p["outc.weight"] = rng.normal(0, 0.05, (n_classes, base, 1, 1)).astype(np.float32)
+    p["outc.bias"] = rng.normal(0, 0.05, n_classes).astype(np.float32)
+    return p
