@@ -147,6 +147,61 @@ def make_blob_v2(seed: int = 0, base: int = 16, n_bands: int = 120, n_classes: i
     return b
 
 
+def make_blob_react(seed: int = 0, base: int = 16, n_bands: int = 120, n_classes: int = 3,
+                    coverage: bool = False):
+    """A v3 (ReActNet real-highway) blob (python/bnn2c/blob_react.py:8-41).
+    Recipe (recorded with every fixture): binary weights Bernoulli(0.5);
+    enc1.conv1 as the v1 real first conv; proj W ~ N(0, 1/sqrt(Cin)); int
+    epilogues A ~ U(0.5, 1.5)/sqrt(Cin*9) (alpha and the BN scale folded),
+    real epilogue A ~ U(0.5, 1.5); B ~ N(0, 0.3), move1 ~ N(0, 0.1),
+    prelu_w ~ U(-0.25, 0.5); taps rsign ~ N(0, 0.3); head W ~ N(0, 0.1),
+    bias ~ N(0, 0.05).  coverage=True also sets exact zeros: prelu_w = 0
+    (negative t gives -0), A = 0, rsign = 0 and B = -move1 on some channels."""
+    from . import blob_react as R
+    rng = np.random.default_rng(seed)
+
+    def epi(kind, c, cin):
+        A = rng.uniform(0.5, 1.5, c).astype(np.float32)
+        if kind == R.EPI_INT:
+            A = (A / np.float32(np.sqrt(cin * 9))).astype(np.float32)
+        Bv = rng.normal(0, 0.3, c).astype(np.float32)
+        m = rng.normal(0, 0.1, c).astype(np.float32)
+        w = rng.uniform(-0.25, 0.5, c).astype(np.float32)
+        if coverage:
+            w[rng.random(c) < 0.2] = 0.0
+            A[rng.random(c) < 0.1] = 0.0
+            z = rng.random(c) < 0.1
+            Bv[z] = -m[z]
+        return R.Epi(kind, c, A, Bv, m, w)
+
+    def tap(c):
+        r = rng.normal(0, 0.3, c).astype(np.float32)
+        if coverage:
+            r[rng.random(c) < 0.2] = 0.0
+        return R.Tap(c, r)
+
+    b = R.BlobV3(base, n_bands, n_classes)
+    for name, ci, co, kind in R.arch(base):
+        if name == "enc1":
+            ci = n_bands
+        real = name == "enc1"
+        conv1 = _real_conv(rng, ci, co) if real else _bin_conv(rng, ci, co)
+        W = rng.normal(0, 1 / np.sqrt(ci), (co, ci)).astype(np.float32)
+        blk = R.Block(kind == "down", real, None if real else tap(ci), conv1, R.Proj(co, ci, W),
+                      epi(R.EPI_REAL if real else R.EPI_INT, co, ci), tap(co), _bin_conv(rng, co, co),
+                      epi(R.EPI_INT, co, co), epi(R.EPI_INT, co, co) if kind == "down" else None)
+        if name.startswith("enc"):
+            b.enc.append(blk)
+        elif name == "bottleneck":
+            b.bott = blk
+        else:
+            b.dec.append(blk)
+    W = rng.normal(0.0, 0.1, (n_classes, base)).astype(np.float32)
+    bias = rng.normal(0.0, 0.05, n_classes).astype(np.float32)
+    b.head = B.Head(n_classes, base, W, bias)
+    return b
+
+
 def make_input(seed: int, n: int, n_bands: int = 120, h: int = 32, w: int = 32) -> np.ndarray:
     """x ~ N(0,1) float32 [n, n_bands, h, w] ([band,row,col] per patch)."""
     rng = np.random.default_rng(seed)

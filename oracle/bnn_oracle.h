@@ -106,6 +106,48 @@ void orc_head(const float *a, const float *Wt, const float *bias, float *logits,
 void orc_up_cat(const int8_t *skip, int sC, int sH, int sW, const int8_t *x,
                 int xC, int hH, int hW, int8_t *out);
 
+/* ---- v3 (ReActNet real highway; bnn_oracle_react.c) ----
+ * Records of csrc/bnn_model_react.h:57-88; dec[0..3] = dec4..dec1. */
+typedef struct { int c; float *rsign; } orr_tap_rec;
+typedef struct { int cout, cin; float *W; } orr_proj_rec;
+typedef struct { int kind, c; float *A, *B, *move1, *prelu_w; } orr_epi_rec;
+typedef struct {
+    int is_down, input_real;
+    orr_tap_rec tap1, tap2;
+    orc_conv c1, c2;
+    orr_proj_rec p1;
+    orr_epi_rec e1, ea, eb;       /* ea: skip (down) or epi2 (plain); eb: pooled down */
+} orr_block;
+typedef struct {
+    int version, base, n_bands, n_classes, upsampler;
+    orr_block enc[4], bott, dec[4];
+    int head_cout, head_cin;
+    float *head_w, *head_b;
+} orr_model;
+
+int  orr_parse(const uint8_t *buf, size_t len, orr_model **out, char *err, int errlen);
+void orr_free(orr_model *m);
+/* Stages (dtype as orc_forward): enc1.u1.proj, enc1.u1.conv, enc1.h1;
+ * X.u1.proj, X.u1.tap, X.u1.P, X.h1 (X = enc2..4, bott, dec4..1);
+ * X.u2.tap, X.u2.P; encK.skip, encK.pool.P, encK.pool.h, encK.down;
+ * bott.h2, decK.cat, decK.h2; logits. */
+int  orr_forward(const orr_model *m, const float *in, int H, int W, float *logits,
+                 orc_stage_cb cb, void *ctx);
+int  orr_forward_patched(const orr_model *m, const float *in, int H, int W, float *logits, int P);
+int  orr_forward_batch_par(const orr_model *m, const float *in, int N, int H, int W, float *logits);
+void orr_proj(const float *x, const float *Wm, float *out, int cin, int HW, int cout);
+void orr_conv3(const float *x, const int8_t *wsign, const float *alpha, float *out,
+               int cin, int H, int W, int cout);
+void orr_epi_int(const int32_t *P, const float *res, float *out, int C, int HW,
+                 const float *A, const float *B, const float *move1, const float *prelu_w);
+void orr_epi_real(const float *x, const float *res, float *out, int C, int HW,
+                  const float *A, const float *B, const float *move1, const float *prelu_w);
+void orr_tap(const float *x, int8_t *out, int C, int HW, const float *rsign);
+void orr_maxpool_real(const float *x, float *out, int C, int H, int W);
+void orr_up_cat(const float *skip, int sC, int sH, int sW, const float *x, int xC, int hH, int hW,
+                float *out);
+void orr_head(const float *a, const float *Wm, const float *bias, float *out, int cin, int HW, int cout);
+
 #ifdef __cplusplus
 }
 #endif

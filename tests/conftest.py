@@ -40,6 +40,21 @@ def ref():
 
 
 @pytest.fixture(scope="session")
+def rorc():
+    from oracle.oracle import ReactOracle, build
+    build()
+    return ReactOracle()
+
+
+@pytest.fixture(scope="session")
+def rref():
+    from oracle.oracle import RefReact, react_ref_available
+    if not react_ref_available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    return RefReact()
+
+
+@pytest.fixture(scope="session")
 def golden():
     with open(os.path.join(GOLDEN, "golden.json")) as f:
         meta = json.load(f)

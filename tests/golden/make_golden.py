@@ -18,8 +18,16 @@ an H x W) it records:
     stage hashes of the chained kernels (stem 1x1 conv, real fold, then a
     binary enc1), and the output of `bnn_infer_stem`.
 
+  * for v3 (ReActNet) blobs: logits from bnn_forward_react, stage hashes of
+    the reference's v3 kernels (react_proj_blk, react_conv3_blk, react_tap,
+    bconv_blk_b4p4_i16, react_epilogue_*, maxpool_P_i16, maxpool_real_v2,
+    head_1x1_v2) chained as csrc/bnn_model_react.c:190-274, 395-438 chains
+    them, and the output of `bnn_infer_react` on an input file, streamed and
+    patch-wise.
+
 Stage hashes are over the C-order bytes of [C,H,W] arrays: int8 for binary
-activations, int32 for P, float32 for enc1.conv1 and logits.
+activations, int32 for P, float32 for enc1.conv1 and logits (v3: float32
+for every highway stage, int32 for P although the reference stores int16).
 """
 from __future__ import annotations
 
@@ -37,7 +45,8 @@ sys.path.insert(0, ROOT)
 
 from bnns_to_c_amd import blob as B  # noqa: E402
 from bnns_to_c_amd import synth  # noqa: E402
-from oracle.oracle import REF_CLI, REF_CLI_STEM, RefC  # noqa: E402
+from bnns_to_c_amd import blob_react as R  # noqa: E402
+from oracle.oracle import REACT_REF_CLI, REF_CLI, REF_CLI_STEM, RefC, RefReact  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
@@ -58,6 +67,16 @@ STEM_CASES = [
     ("stem24_base16_s3_30x34", 3, 16, 24, False, 112, 1, 30, 34),
 ]
 STEM_CLI_CASES = [("stem16_base16_s1_32x32", 1, 16, 16, False, 32, 32)]
+# v3 (ReActNet): (name, blob seed, base, coverage, input seed, N, H, W)
+REACT_CASES = [
+    ("react16_s0_32x32", 0, 16, False, 120, 2, 32, 32),
+    ("react8_cov_s1_odd17x23", 1, 8, True, 121, 2, 17, 23),
+    ("react16_cov_s2_32x32", 2, 16, True, 122, 1, 32, 32),
+    ("react32_s3_16x16", 3, 32, False, 123, 1, 16, 16),
+]
+# (name, blob seed, base, input seed, H, W, patch size or 0 for the whole image)
+REACT_CLI_CASES = [("react8_s4_36x52_file", 4, 8, 124, 36, 52, 0),
+                   ("react16_s5_40x56_patch16", 5, 16, 125, 40, 56, 16)]
 
 
 def sha(a: np.ndarray) -> str:
@@ -131,6 +150,81 @@ def ref_chain(ref: RefC, b: B.BlobV1, x: np.ndarray):
     return st
 
 
+def up_cat_f(skip: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """csrc/bnn_model_react.c:280-298: the float concat, 0.0 where the up part is absent."""
+    sC, sH, sW = skip.shape
+    xC, hH, hW = x.shape
+    out = np.zeros((sC + xC, sH, sW), np.float32)
+    out[:sC] = skip
+    uH, uW = 2 * hH, 2 * hW
+    oh, ow = max(sH - uH, 0) // 2, max(sW - uW, 0) // 2
+    up = np.repeat(np.repeat(x, 2, axis=1), 2, axis=2)[:, :min(uH, sH), :min(uW, sW)]
+    out[sC:, oh:oh + up.shape[1], ow:ow + up.shape[2]] = up
+    return out
+
+
+def react_chain(ref: RefReact, b: R.BlobV3, x: np.ndarray):
+    """Every stage of one v3 patch through the reference's v3 kernels."""
+    st = {}
+
+    def epi(acc, res, e):
+        return ref.epi(acc, res, e.A, e.B, e.move1, e.prelu_w)
+
+    def unit1(k, xin, nm):
+        res = ref.proj(xin, k.proj1.W)
+        st[f"{nm}.u1.proj"] = res
+        a = ref.tap(xin, k.tap1.rsign)
+        st[f"{nm}.u1.tap"] = a
+        P = ref.bconv(a, k.conv1.packed, k.conv1.cout)
+        st[f"{nm}.u1.P"] = P.astype(np.int32)
+        h = epi(P, res, k.epi1)
+        st[f"{nm}.h1"] = h
+        return h
+
+    def unit2_P(k, h1, nm):
+        a = ref.tap(h1, k.tap2.rsign)
+        st[f"{nm}.u2.tap"] = a
+        P = ref.bconv(a, k.conv2.packed, k.conv2.cout)
+        st[f"{nm}.u2.P"] = P.astype(np.int32)
+        return P
+
+    h = x
+    skips = []
+    for i, k in enumerate(b.enc):
+        nm = f"enc{i + 1}"
+        if k.input_real:
+            res = ref.proj(h, k.proj1.W)
+            st["enc1.u1.proj"] = res
+            c = ref.conv3(h, k.conv1.wsign, k.conv1.alpha)
+            st["enc1.u1.conv"] = c
+            h1 = epi(c, res, k.epi1)
+            st["enc1.h1"] = h1
+        else:
+            h1 = unit1(k, h, nm)
+        P = unit2_P(k, h1, nm)
+        sk = epi(P, h1, k.epi_a)
+        st[f"{nm}.skip"] = sk
+        skips.append(sk)
+        Pd = ref.maxpool_P(P)
+        st[f"{nm}.pool.P"] = Pd.astype(np.int32)
+        hd = ref.maxpool_real(h1)
+        st[f"{nm}.pool.h"] = hd
+        h = epi(Pd, hd, k.epi_b)
+        st[f"{nm}.down"] = h
+    h1 = unit1(b.bott, h, "bott")
+    h = epi(unit2_P(b.bott, h1, "bott"), h1, b.bott.epi_a)
+    st["bott.h2"] = h
+    for j, k in enumerate(b.dec):
+        nm = f"dec{4 - j}"
+        cat = up_cat_f(skips[3 - j], h)
+        st[f"{nm}.cat"] = cat
+        h1 = unit1(k, cat, nm)
+        h = epi(unit2_P(k, h1, nm), h1, k.epi_a)
+        st[f"{nm}.h2"] = h
+    st["logits"] = ref.head(h, b.head.W, b.head.bias)
+    return st
+
+
 def main() -> None:
     ref = RefC()
     meta = {"generator": "tests/golden/make_golden.py",
@@ -199,6 +293,40 @@ def main() -> None:
             o = np.fromfile(out, np.float32).reshape(-1, H, W)
             meta["stem_cli"][name] = {"blob_seed": seed, "base": base, "stem": stem, "coverage": cov,
                                       "H": H, "W": W, "sha256": sha(o)}
+            arrays[f"{name}__cli"] = o
+        rref = RefReact()
+        meta["react_cases"], meta["react_cli"] = {}, {}
+        for name, seed, base, cov, iseed, N, H, W in REACT_CASES:
+            b = synth.make_blob_react(seed=seed, base=base, coverage=cov)
+            data = R.to_bytes(b)
+            path = os.path.join(td, name + ".blob")
+            open(path, "wb").write(data)
+            x = synth.make_input(iseed, N, 120, H, W)
+            h, _, ncls = rref.load(path)
+            logits = np.stack([rref.forward(h, x[n], ncls) for n in range(N)])
+            rref.free(h)
+            stages = []
+            for n in range(N):
+                st = react_chain(rref, b, x[n])
+                assert np.array_equal(st["logits"].view(np.uint32), logits[n].view(np.uint32)), \
+                    f"{name}: chained reference kernels differ from reference bnn_forward_react"
+                stages.append({k: sha(v) for k, v in st.items()})
+            meta["react_cases"][name] = {"blob_seed": seed, "base": base, "coverage": cov, "input_seed": iseed,
+                                         "N": N, "H": H, "W": W, "blob_sha256": hashlib.sha256(data).hexdigest(),
+                                         "input_sha256": sha(x), "stages": stages}
+            arrays[f"{name}__logits"] = logits
+        for name, seed, base, iseed, H, W, P in REACT_CLI_CASES:
+            b = synth.make_blob_react(seed=seed, base=base)
+            path = os.path.join(td, name + "_cli.blob")
+            open(path, "wb").write(R.to_bytes(b))
+            xin = os.path.join(td, name + "_in.bin")
+            synth.make_input(iseed, 1, 120, H, W)[0].tofile(xin)
+            out = os.path.join(td, name + "_cli.bin")
+            spec = f"patch{P}:{xin}" if P else xin
+            subprocess.run([REACT_REF_CLI, path, spec, out, str(H), str(W)], check=True, capture_output=True)
+            o = np.fromfile(out, np.float32).reshape(-1, H, W)
+            meta["react_cli"][name] = {"blob_seed": seed, "base": base, "input_seed": iseed, "H": H, "W": W,
+                                       "patch": P, "sha256": sha(o)}
             arrays[f"{name}__cli"] = o
     with open(os.path.join(OUT, "golden.json"), "w") as f:
         json.dump(meta, f, indent=1, sort_keys=True)
