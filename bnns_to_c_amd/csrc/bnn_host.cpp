@@ -22,6 +22,7 @@
 #include <thread>
 #include <vector>
 
+#include "bnn_host_internal.h"
 #include "bnn_kernels.h"
 #include "bnn_model.h"
 #include "bnn_model_stem.h"
@@ -32,7 +33,10 @@ using namespace bnn;
 // ------------------------------------------------------------------ errors
 namespace {
 thread_local std::string g_err;
+bool g_prof_on = false;
+}  // namespace
 
+namespace bnn {
 int set_err(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -43,18 +47,34 @@ int set_err(int code, const char* fmt, ...) {
   return code;
 }
 
-#define HIP_TRY(expr)                                                                  \
-  do {                                                                                 \
-    hipError_t e_ = (expr);                                                            \
-    if (e_ != hipSuccess)                                                              \
-      return set_err(BNN_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
-                     __LINE__);                                                        \
-  } while (0)
-
 [[noreturn]] void die() {
   fprintf(stderr, "%s\n", g_err.c_str());
   exit(1);
 }
+
+bool prof_enabled() { return g_prof_on; }
+
+std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int taps, int cs) {
+  const int nw = (cin * taps + 63) / 64;
+  const int cw0 = words(cs ? cs : cin), cw1 = cs ? words(cin - cs) : 0;
+  const int coutp = pad32(cout);
+  std::vector<uint32_t> wt((size_t)(cw0 + cw1) * coutp * taps, 0u);
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci) {
+      int w, b;
+      if (!cs || ci < cs) { w = ci >> 5; b = ci & 31; }
+      else { w = cw0 + ((ci - cs) >> 5); b = (ci - cs) & 31; }
+      for (int t = 0; t < taps; ++t) {
+        const int k = ci * taps + t;
+        if ((kbits[(size_t)co * nw + (k >> 6)] >> (k & 63)) & 1ull)
+          wt[((size_t)w * coutp + co) * taps + t] |= 1u << b;
+      }
+    }
+  return wt;
+}
+}  // namespace bnn
+
+namespace {
 
 // ------------------------------------------------------------ blob reader
 struct Reader {
@@ -282,30 +302,6 @@ int validate(const Model* m, const StemPart* st = nullptr) {
 }
 
 // --------------------------------------------------------- host repacking
-inline int words(int c) { return (c + 31) >> 5; }
-inline int pad32(int c) { return (c + 31) & ~31; }
-
-// kidx sign bits (bit k = ci*9 + t) -> [cw0+cw1][coutp][9] uint32 with channel
-// ci placed at word ci>>5 of the first segment (ci < cs) or at word
-// cw0 + ((ci-cs)>>5) of the second (the upsampled half of a concat).
-std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int taps, int cs) {
-  const int nw = (cin * taps + 63) / 64;
-  const int cw0 = words(cs ? cs : cin), cw1 = cs ? words(cin - cs) : 0;
-  const int coutp = pad32(cout);
-  std::vector<uint32_t> wt((size_t)(cw0 + cw1) * coutp * taps, 0u);
-  for (int co = 0; co < cout; ++co)
-    for (int ci = 0; ci < cin; ++ci) {
-      int w, b;
-      if (!cs || ci < cs) { w = ci >> 5; b = ci & 31; }
-      else { w = cw0 + ((ci - cs) >> 5); b = (ci - cs) & 31; }
-      for (int t = 0; t < taps; ++t) {
-        const int k = ci * taps + t;
-        if ((kbits[(size_t)co * nw + (k >> 6)] >> (k & 63)) & 1ull)
-          wt[((size_t)w * coutp + co) * taps + t] |= 1u << b;
-      }
-    }
-  return wt;
-}
 
 struct FoldHost {
   std::vector<int32_t> lo;
@@ -547,7 +543,6 @@ struct ProfRec {
   double oe, taps, sec;
 };
 std::vector<ProfRec> g_prof;
-bool g_prof_on = false;
 
 // work-item shape: pool epilogue needs 2x2 blocks, the head one pixel; the
 // channel group shrinks until the launch has ~4 waves per SIMD
@@ -628,6 +623,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
                    uint32_t* out, uint32_t* out2, float* logits, const char* label) -> int {
     BconvArgs a{};
     a.in0 = in0; a.in1 = in1; a.cw0 = L.cw0; a.cw1 = L.cw1;
+    a.padoff = 0x80000000u;  // uncovered concat positions read 0 bits
     a.N = N; a.H = hs[lvl]; a.W = wsz[lvl]; a.cin = L.cin; a.cout = L.cout;
     if (in1) {
       a.h1 = hs[lvl1]; a.w1 = wsz[lvl1];

@@ -1,5 +1,6 @@
 // bnn_kernel_abi.cpp - the reference's batch-1 kernel entry points
-// (csrc/bnn_model.h:7-23, csrc/bnn_conv.c:50,80) backed by the GPU.
+// (csrc/bnn_model.h:7-23, csrc/bnn_conv.c:50,80, and the v3 kernels of
+// csrc/bnn_model_react.h:18-53) backed by the GPU.
 //
 // Same names, argument order and layouts as the reference, host pointers in
 // and out, synchronous.  Each call stages its arrays through device memory,
@@ -18,6 +19,7 @@
 
 #include "bnn_kernels.h"
 #include "bnn_model.h"
+#include "bnn_model_react.h"
 
 using namespace bnn;
 
@@ -215,6 +217,142 @@ void head_1x1(const float* a, const float* Wt, const float* bias, float* logits,
   check(launch_head(da->as<float>(), dw->as<float>(), db->as<float>(), dO.as<float>(), Cin, (int)hw, Cout, 0),
         "head");
   down(logits, dO, (size_t)Cout * hw * 4);
+}
+
+// ---------------------------------------------------------------- v3 ----
+// csrc/bnn_react_ops.c:36-70 (form 0) and csrc/bnn_react_epi.c:11-77 (form 1)
+static void react_epi(const void* acc, int kind, size_t esz, const float* res, float* out, int C, int H, int W,
+                      const float* A, const float* B, const float* move1, const float* prelu_w, int form) {
+  const size_t n = (size_t)C * H * W;
+  if (!n) return;
+  std::unique_ptr<Buf> dacc(up(acc, n * esz)), dres(up(res, n * 4)), dA(up(A, C * 4)), dB(up(B, C * 4)),
+      dm(up(move1, C * 4)), dw(up(prelu_w, C * 4));
+  Buf dO(n * 4);
+  check(launch_react_epi(dacc->p, kind, dres->as<float>(), dO.as<float>(), C, (long)H * W, dA->as<float>(),
+                         dB->as<float>(), dm->as<float>(), dw->as<float>(), form, 0),
+        "react_epilogue");
+  down(out, dO, n * 4);
+}
+
+void react_epilogue_int(const int32_t* P, const float* res, float* out, int C, int H, int W, const float* A,
+                        const float* B, const float* move1, const float* prelu_w) {
+  react_epi(P, 0, 4, res, out, C, H, W, A, B, move1, prelu_w, 0);
+}
+void react_epilogue_real(const float* cin, const float* res, float* out, int C, int H, int W, const float* A,
+                         const float* B, const float* move1, const float* prelu_w) {
+  react_epi(cin, 2, 4, res, out, C, H, W, A, B, move1, prelu_w, 0);
+}
+void react_epilogue_int_v2(const int32_t* P, const float* res, float* out, int C, int H, int W, const float* A,
+                           const float* B, const float* move1, const float* prelu_w) {
+  react_epi(P, 0, 4, res, out, C, H, W, A, B, move1, prelu_w, 1);
+}
+void react_epilogue_int_i16(const int16_t* P, const float* res, float* out, int C, int H, int W, const float* A,
+                            const float* B, const float* move1, const float* prelu_w) {
+  react_epi(P, 1, 2, res, out, C, H, W, A, B, move1, prelu_w, 1);
+}
+void react_epilogue_real_v2(const float* cin, const float* res, float* out, int C, int H, int W, const float* A,
+                            const float* B, const float* move1, const float* prelu_w) {
+  react_epi(cin, 2, 4, res, out, C, H, W, A, B, move1, prelu_w, 1);
+}
+
+void react_tap(const float* x, int8_t* out, int C, int H, int W, const float* rsign) {
+  const size_t n = (size_t)C * H * W;
+  if (!n) return;
+  std::unique_ptr<Buf> dx(up(x, n * 4)), dr(up(rsign, C * 4));
+  Buf dO(n);
+  check(launch_react_tap(dx->as<float>(), dO.as<int8_t>(), C, (long)H * W, dr->as<float>(), 0), "react_tap");
+  down(out, dO, n);
+}
+
+void maxpool_real(const float* x, float* out, int C, int H, int W, int k, int stride) {
+  if (k <= 0 || stride <= 0 || H < k || W < k || C <= 0) return;
+  const int Ho = (H - k) / stride + 1, Wo = (W - k) / stride + 1;
+  std::unique_ptr<Buf> dx(up(x, (size_t)C * H * W * 4));
+  Buf dO((size_t)C * Ho * Wo * 4);
+  check(launch_maxpool_real(dx->as<float>(), dO.as<float>(), C, H, W, k, stride, 0), "maxpool_real");
+  down(out, dO, (size_t)C * Ho * Wo * 4);
+}
+// 2x2 / stride 2 only; any other window leaves out untouched (csrc/bnn_react_opt.c:48)
+void maxpool_real_v2(const float* x, float* out, int C, int H, int W, int k, int stride) {
+  if (k != 2 || stride != 2) return;
+  maxpool_real(x, out, C, H, W, 2, 2);
+}
+void maxpool_P_v2(const int32_t* x, int32_t* out, int C, int H, int W, int k, int stride) {
+  if (k != 2 || stride != 2) return;
+  maxpool_P(x, out, C, H, W, 2, 2);
+}
+void maxpool_P_i16(const int16_t* x, int16_t* out, int C, int H, int W, int k, int stride) {
+  if (k != 2 || stride != 2 || H < 2 || W < 2 || C <= 0) return;
+  const int Ho = H / 2, Wo = W / 2;
+  std::vector<int32_t> xi((size_t)C * H * W), oi((size_t)C * Ho * Wo);
+  for (size_t i = 0; i < xi.size(); ++i) xi[i] = x[i];
+  maxpool_P(xi.data(), oi.data(), C, H, W, 2, 2);
+  for (size_t i = 0; i < oi.size(); ++i) out[i] = (int16_t)oi[i];
+}
+
+// one chain over ci from 0 per output: react_proj_blk for Cout % 8 == 0
+// (csrc/bnn_realin_blk.h:39-83, which exits otherwise), react_proj_1x1
+// (csrc/bnn_react_ops.c:117-133) for any Cout; both on the matrix cores
+static void proj_gpu(const float* x, const float* Wm, float* out, int Cin, int H, int W, int Cout) {
+  const size_t hw = (size_t)H * W;
+  if (!hw || Cout <= 0) return;
+  std::vector<float> lanes(react_pw_lanes_len(Cout, Cin));
+  react_pw_lanes(Wm, Cout, Cin, lanes.data());
+  std::unique_ptr<Buf> dx(up(x, (size_t)Cin * hw * 4)), dw(up(lanes.data(), lanes.size() * 4));
+  Buf dO((size_t)Cout * hw * 4);
+  ProjArgs p{};
+  p.x0 = dx->as<float>(); p.c0 = Cin; p.cin = Cin; p.cout = Cout;
+  p.N = 1; p.H = H; p.W = W; p.w = dw->as<float>(); p.out = dO.as<float>();
+  check(launch_proj(p, 0), "react_proj");
+  down(out, dO, (size_t)Cout * hw * 4);
+}
+void react_proj_1x1(const float* x, const float* Wm, float* out, int Cin, int H, int W, int Cout) {
+  proj_gpu(x, Wm, out, Cin, H, W, Cout);
+}
+void react_proj_blk(const float* x, const float* Wm, float* out, int Cin, int H, int W, int Cout) {
+  if (Cout % 8) {
+    fprintf(stderr, "proj_blk: Cout %% CB != 0\n");
+    exit(1);
+  }
+  proj_gpu(x, Wm, out, Cin, H, W, Cout);
+}
+
+void react_conv3_blk(const float* x, const int8_t* wsign, const float* alpha, float* out, int Cin, int H, int W,
+                     int Cout) {
+  if (Cout % 8) {
+    fprintf(stderr, "conv3_blk: Cout %% CB != 0\n");
+    exit(1);
+  }
+  const size_t hw = (size_t)H * W;
+  if (!hw || Cout <= 0) return;
+  std::unique_ptr<Buf> dx(up(x, (size_t)Cin * hw * 4)), dw(up(wsign, (size_t)Cout * Cin * 9)),
+      da(up(alpha, (size_t)Cout * 4));
+  Buf dO((size_t)Cout * hw * 4);
+  check(launch_conv3_chain(dx->as<float>(), dw->as<int8_t>(), da->as<float>(), dO.as<float>(), Cin, H, W, Cout, 0),
+        "react_conv3");
+  down(out, dO, (size_t)Cout * hw * 4);
+}
+
+// the register-tiled binary convs give the integers of every other bconv
+// kernel (csrc/bnn_bconv_blk.h:30-156), int16 storage included
+void bconv_blk_b4p4(const int8_t* a, const uint64_t* packed_w, int32_t* P, int Cin, int H, int W, int Cout, int kh,
+                    int kw, int pad, int stride) {
+  bconv_gpu(a, packed_w, P, Cin, H, W, Cout, kh, kw, pad, stride);
+}
+void bconv_blk_b4p4_i16(const int8_t* a, const uint64_t* packed_w, int16_t* P, int Cin, int H, int W, int Cout,
+                        int kh, int kw, int pad, int stride) {
+  const int Ho = out_dim(H, kh, pad, stride), Wo = out_dim(W, kw, pad, stride);
+  if (Ho <= 0 || Wo <= 0 || Cout <= 0) return;
+  std::vector<int32_t> Pi((size_t)Cout * Ho * Wo);
+  bconv_gpu(a, packed_w, Pi.data(), Cin, H, W, Cout, kh, kw, pad, stride);
+  for (size_t i = 0; i < Pi.size(); ++i) P[i] = (int16_t)Pi[i];
+}
+
+// bias, then channels in order, one fused step each: the same arithmetic as
+// head_1x1 (csrc/bnn_react_opt.c:33-41 on x86)
+void head_1x1_v2(const float* a, const float* Wt, const float* bias, float* logits, int Cin, int H, int W_,
+                 int Cout) {
+  head_1x1(a, Wt, bias, logits, Cin, H, W_, Cout);
 }
 
 }  // extern "C"

@@ -20,6 +20,11 @@ enum Epi : int {
   EPI_POOL = 1,  // rule on P (skip) + 2x2 max of P -> second rule (down)
   EPI_HEAD = 2,  // rule on P -> +-1 -> fp32 1x1 head -> logits
   EPI_P = 3,     // raw int32 P [N][Cout][H][W]
+  // v3 (ReActNet real highway): h = RPReLU(A*P + (B + move1) + res) as
+  // float planes, and the bits of the next tap on h
+  EPI_RX = 4,      // h and its tap bits
+  EPI_RXPOOL = 5,  // skip h (+ bits) and the pooled down h (+ bits)
+  EPI_RXHEAD = 6,  // h, then the fp32 1x1 head -> logits
 };
 
 // One modular interval per channel: bit = (uint32)(P - lo) < wid.  Covers
@@ -70,6 +75,18 @@ struct BconvArgs {
   const float* hb;      // head bias [ncls]
   int ncls;
   int sH, sW, pcols, prow0;  // scene mode (pcols > 0), as in RealArgs
+  // in1 byte offset read where the upsample does not cover an in-image
+  // position: 0x80000000 (past the buffer: reads 0 bits, v1's zero-filled
+  // concat) or the offset of the pad pixel that holds the tap bits of 0.0
+  // (v3's zero-filled float concat)
+  uint32_t padoff;
+  // v3 epilogues.  Float planes: element (c, n, y, x) at c*N*H*W + (n*H + y)*W + x.
+  const float* res;     // shortcut planes [cout] at this resolution
+  float* hout;          // h planes (EPI_RXHEAD: optional)
+  const float *eA, *eB, *eW;   // A, B + move1, PReLU weight; padded to 32
+  const float* trs;     // rsign of the tap on h -> out bits (+ the pad pixel at N*H*W), or null
+  const float *dA, *dB, *dW, *drs;  // EPI_RXPOOL: the pooled-down epilogue and its tap -> out2
+  float* dout;          // EPI_RXPOOL: pooled h planes at (H/2, W/2)
 };
 
 struct RealArgs {
@@ -88,6 +105,13 @@ struct RealArgs {
   // patches, pcols per row, patch n at row prow0 + n / pcols, column
   // n % pcols; a patch's rows and columns past the cube read 0
   int sH, sW, pcols, prow0;
+  // v3 enc1 unit 1 (launch_react_in): the conv chain runs over ci outermost,
+  // taps inside; a 1x1 projection chain runs beside it; the epilogue is
+  // h = RPReLU(A*(alpha*acc) + B + proj) with A, B (= B + move1), slope
+  // (= PReLU weight) and rsign (= the next tap's bias) above
+  const float* pw;      // projection weights [ceil(cout/16)][chunk][4][64], see react_proj_lanes
+  float* hout;          // h planes [cout][N*H*W]
+  float* f32b;          // projection output [N][cout][H][W]; may be null
 };
 
 // Real-conv work split: output channels per lane group and output rows per
@@ -166,6 +190,58 @@ inline void real_stem_masks(const int8_t* wsign, int cout, int cin, uint64_t* ou
 }
 // the 1x1 real conv + real fold (v2 stem): wm = real_stem_masks, w unused
 hipError_t launch_stem(const RealArgs& a, hipStream_t s);
+
+// v3 enc1 projection weights for the matrix-core kernel: per 16-channel
+// group g and input chunk ch (kRealMfmaCI = 8 channels) four 64-float rows;
+// row r < 2, lane l holds W[16g + l%16][8ch + 4r + l/16] (0 past cout/cin),
+// rows 2 and 3 are 0 (one row per wave of the work group).
+inline size_t react_proj_lanes_len(int cout, int cin) {
+  return (size_t)((cout + 15) / 16) * (real_conv_cin_pad(cin) / kRealMfmaCI) * 4 * 64;
+}
+inline void react_proj_lanes(const float* W, int cout, int cin, float* out) {
+  const int nch = real_conv_cin_pad(cin) / kRealMfmaCI;
+  for (size_t i = 0; i < react_proj_lanes_len(cout, cin); ++i) out[i] = 0.0f;
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci) {
+      const int g = co / 16, ch = ci / kRealMfmaCI, r = (ci % kRealMfmaCI) / 4, l = 16 * (ci % 4) + co % 16;
+      out[(((size_t)g * nch + ch) * 4 + r) * 64 + l] = W[(size_t)co * cin + ci];
+    }
+}
+// v3 enc1 unit 1: 3x3 conv (lane masks) + projection + epilogue -> h planes and tap bits
+hipError_t launch_react_in(const RealArgs& a, hipStream_t s);
+
+// v3 1x1 projection of binary blocks (no bias), on the matrix cores:
+// out[co][q] = chain over ci from 0 of W[co][ci] * x[ci][q] over the planes
+// of x (q = (n*H + y)*W + x).  With x1 set, channels >= c0 come from the
+// nearest-2x upsample of x1 (planes at h1 x w1) placed at (oh, ow); positions
+// it does not cover read 0.  Weights as react_pw_lanes lays them out.
+struct ProjArgs {
+  const float* x0;      // planes [c0][N*H*W]
+  const float* x1;      // planes [cin-c0][N*h1*w1], or null
+  int c0, cin, cout;
+  int N, H, W, h1, w1, oh, ow, uh, uw;
+  const float* w;       // react_pw_lanes layout
+  float* out;           // planes [cout][N*H*W]
+};
+// [ceil(cout/16)][ceil(cin/4)][64]: lane l of quad q holds W[16g + l%16][4q + l/16]
+inline size_t react_pw_lanes_len(int cout, int cin) { return (size_t)((cout + 15) / 16) * ((cin + 3) / 4) * 64; }
+inline void react_pw_lanes(const float* W, int cout, int cin, float* out) {
+  const int nq = (cin + 3) / 4;
+  for (size_t i = 0; i < react_pw_lanes_len(cout, cin); ++i) out[i] = 0.0f;
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci)
+      out[(((size_t)(co / 16) * nq + ci / 4) * 64) + 16 * (ci % 4) + co % 16] = W[(size_t)co * cin + ci];
+}
+hipError_t launch_proj(const ProjArgs& a, hipStream_t s);
+
+// v3 batch-1 kernel ABI helpers (one thread per output element)
+hipError_t launch_react_epi(const void* acc, int kind, const float* res, float* out, int C, long HW,
+                            const float* A, const float* B, const float* move1, const float* prelu_w, int form,
+                            hipStream_t s);
+hipError_t launch_react_tap(const float* x, int8_t* out, int C, long HW, const float* rsign, hipStream_t s);
+hipError_t launch_maxpool_real(const float* x, float* out, int C, int H, int W, int k, int stride, hipStream_t s);
+hipError_t launch_conv3_chain(const float* x, const int8_t* wsign, const float* alpha, float* out, int cin, int H,
+                              int W, int cout, hipStream_t s);
 
 // Launchers return hipSuccess or the first launch error.  mt = micro-tile
 // side (1 or 2), cog = output channels per work-item (8/16/32).

@@ -279,6 +279,17 @@ __device__ __forceinline__ void mfma_taps(f32x16 (&acc)[9], const float (&wa)[3]
                                           std::integer_sequence<int, T...>) {
   (mfma_tap<T>(acc, wa, xb), ...);
 }
+// v3 order: the nine taps of one input channel as consecutive steps of one
+// chain (csrc/bnn_realin_blk.h:111-125)
+template <int T>
+__device__ __forceinline__ void mfma_chain_tap(f32x16& acc, const float (&wa)[3], const float (&xb)[9]) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x1f32(wa[T >> 2], xb[T], acc, 2, T & 3, 0);
+}
+template <int... T>
+__device__ __forceinline__ void mfma_chain(f32x16& acc, const float (&wa)[3], const float (&xb)[9],
+                                           std::integer_sequence<int, T...>) {
+  (mfma_chain_tap<T>(acc, wa, xb), ...);
+}
 
 #ifndef BNN_MWPE
 #define BNN_MWPE 2
@@ -288,8 +299,15 @@ constexpr uint32_t kRealFar = 0x7FFFFFF0u;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // waves along rows / columns: tile (4*WR) x (16*WC); PARTIAL: cin is not a
-// multiple of the chunk size
-template <int WR, int WC, bool PARTIAL>
+// multiple of the chunk size.  RX: the v3 (ReActNet) enc1 unit 1 -- one
+// conv chain per output over ci outermost and taps inside
+// (csrc/bnn_realin_blk.h:111-125), a 1x1 projection chain on the centre tap
+// with real weights (csrc/bnn_realin_blk.h:59-70), and the epilogue
+// h = RPReLU(fma(A, alpha*acc, B + move1) + proj) written as float planes
+// with the bits of the next tap on h (csrc/bnn_react_epi.c:57-77,
+// bnn_react_ops.c:75-85).  The projection weights of a chunk ride along
+// with its input rows: one more LDS-writing load per wave.
+template <int WR, int WC, bool PARTIAL, bool RX>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(BNN_MWPE)))
 void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   constexpr int TR = 4 * WR, TC = 16 * WC, NW = WR * WC;
@@ -304,9 +322,13 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   constexpr int NROW = CI * LR;             // row loads per chunk
   constexpr int KR = NROW / NW;  // row loads per wave
   static_assert(NROW % NW == 0, "every wave issues the same number of row loads");
+  static_assert(!RX || NW == 4, "the projection rows of a chunk are one per wave of four");
+  constexpr int KL = KR + (RX ? 1 : 0);  // LDS-writing loads per wave and chunk
   // Three buffers: chunk ch is read from one while ch+1 has landed in the
   // next and ch+2 is in flight into the third.
   __shared__ float tile0[CI * LPL], tile1[CI * LPL], tile2[CI * LPL];  // [ci][row][col]
+  constexpr int WL = RX ? 4 * 64 : 1;  // projection rows of a chunk (RX)
+  __shared__ float wl0[WL], wl1[WL], wl2[WL];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = (wv / WC) * 4, wc = (wv % WC) * 16;
@@ -348,6 +370,12 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
     else if constexpr (B == 1) return tile1;
     else return tile2;
   };
+  auto wlp = [&](auto bc) -> float* {
+    constexpr int B = decltype(bc)::value;
+    if constexpr (B == 0) return wl0;
+    else if constexpr (B == 1) return wl1;
+    else return wl2;
+  };
   // wave wv fills the KR / LR channels [wv*KR/LR, ...) of the chunk
   static_assert(KR % LR == 0, "a wave's row loads cover whole channels");
   // The LDS-writing loads are issued from inline assembly, so the compiler
@@ -356,6 +384,9 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   // before reading this one.  The waits for them are explicit (step).
   const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
   const u32x4 rsrc = {(uint32_t)xaddr, (uint32_t)(xaddr >> 32) & 0xFFFFu, xbytes, 0x00020000u};
+  const uint64_t paddr = RX ? (uint64_t)(uintptr_t)a.pw : 0;
+  const u32x4 psrc = {(uint32_t)paddr, (uint32_t)(paddr >> 32) & 0xFFFFu,
+                      RX ? (uint32_t)(gridDim.y * nchunk * 4 * 64 * 4) : 0u, 0x00020000u};
   auto issue = [&](auto bc, int ch) {
     // the row arithmetic stays here rather than being hoisted out of the
     // chunk loop, where its 3 x KR scalars would not fit in registers
@@ -380,11 +411,25 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
                      : "memory");
       }
     }
+    if constexpr (RX) {
+      // this wave's projection row of the chunk (lane l -> slot 64*wv + l)
+      const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)((uint32_t)(uintptr_t)(lds_f32)(wlp(bc)) + (uint32_t)(wv * 256)));
+      const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)((((uint32_t)g * nchunk + ch) * 4 + wv) * 256u));
+      const uint32_t vl = (uint32_t)lane * 4u;
+      const u32x4 rd = psrc;
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                   :
+                   : "s"(m0v), "v"(vl), "s"(rd), "s"(soff)
+                   : "memory");
+    }
   };
 
-  f32x16 acc[9];
+  // RX: acc[0] the conv chain, acc[1] the projection chain
+  constexpr int NACC = RX ? 2 : 9;
+  f32x16 acc[NACC];
 #pragma unroll
-  for (int t = 0; t < 9; ++t)
+  for (int t = 0; t < NACC; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
@@ -419,7 +464,27 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
         for (int t = 0; t < 9; ++t) xb[(cl + 1) & 1][t] = tb[(cl + 1) * LPL + (t / 3) * LC + t % 3];
       }
       __builtin_amdgcn_sched_barrier(0);
-      mfma_taps(acc, wa, xb[cl & 1], std::make_integer_sequence<int, 9>{});
+      if constexpr (RX) {
+        // the projection step (weights of channels 4q..4q+3 in one
+        // register, block cl%4 broadcast) sits inside the conv chain, whose
+        // steps wait on each other
+        const float pa = wlp(bc)[(cl >> 2) * 64 + lane];
+        mfma_chain(acc[0], wa, xb[cl & 1], std::make_integer_sequence<int, 4>{});
+        // (the broadcast block must be a literal; the switch folds once unrolled)
+        switch (cl & 3) {
+          case 0: acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(pa, xb[cl & 1][4], acc[1], 2, 0, 0); break;
+          case 1: acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(pa, xb[cl & 1][4], acc[1], 2, 1, 0); break;
+          case 2: acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(pa, xb[cl & 1][4], acc[1], 2, 2, 0); break;
+          default: acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(pa, xb[cl & 1][4], acc[1], 2, 3, 0); break;
+        }
+        mfma_chain_tap<4>(acc[0], wa, xb[cl & 1]);
+        mfma_chain_tap<5>(acc[0], wa, xb[cl & 1]);
+        mfma_chain_tap<6>(acc[0], wa, xb[cl & 1]);
+        mfma_chain_tap<7>(acc[0], wa, xb[cl & 1]);
+        mfma_chain_tap<8>(acc[0], wa, xb[cl & 1]);
+      } else {
+        mfma_taps(acc, wa, xb[cl & 1], std::make_integer_sequence<int, 9>{});
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -433,14 +498,14 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
-  // s_waitcnt with vmcnt <= KR or 0 (expcnt and lgkmcnt left alone)
-  constexpr int kWaitKD = (KR & 15) | ((KR >> 4) << 14) | (7 << 4) | (15 << 8);
+  // s_waitcnt with vmcnt <= KL or 0 (expcnt and lgkmcnt left alone)
+  constexpr int kWaitKD = (KL & 15) | ((KL >> 4) << 14) | (7 << 4) | (15 << 8);
   constexpr int kWait0 = (7 << 4) | (15 << 8);
-  static_assert(KR < 64, "vmcnt holds at most 63");
+  static_assert(KL < 64, "vmcnt holds at most 63");
   // Chunk ch from buffer B; chunk ch+2, if any, is fetched into buffer
   // B+2 (mod 3), last read as chunk ch-1, which every wave finished before
   // the last barrier.  Then this wave's loads of chunk ch+1, issued one step
-  // earlier, are waited for (only the KR loads of chunk ch+2 may remain) and
+  // earlier, are waited for (only the KL loads of chunk ch+2 may remain) and
   // the barrier makes every wave's loads visible.
   auto step = [&](auto bc, int ch) {
     constexpr int B = decltype(bc)::value;
@@ -475,6 +540,52 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   // alpha and fold parameters of the lane's four channels (the arrays are
   // padded to 32 channels)
   float p_al[4], p_A[4], p_B[4], p_sl[4], p_rs[4];
+  if constexpr (RX) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      p_al[k] = a.alpha[cq + k];
+      p_A[k] = a.A[cq + k];
+      p_B[k] = a.B[cq + k];
+      p_sl[k] = a.slope[cq + k];
+      p_rs[k] = a.rsign[cq + k];
+    }
+    const int xo = x0 + wc + (lane & 15);
+    const size_t plane = (size_t)a.N * HW;
+    uint32_t w01 = 0, w23 = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int k = r & 3, b = r >> 2;
+      const int y = y0 + wr + b;
+      const int co = cq + k;
+      const bool in = y < a.H && xo < a.W && co < a.cout;
+      const float c = __fmul_rn(p_al[k], acc[0][r]);
+      const float res = acc[1][r];
+      const size_t at = ((size_t)n * a.cout + co) * HW + (size_t)y * a.W + xo;
+      if (a.f32 && in) a.f32[at] = c;
+      if (a.f32b && in) a.f32b[at] = res;
+      const float t = __fadd_rn(__fmaf_rn(p_A[k], c, p_B[k]), res);
+      const float h = t >= 0.0f ? t : __fmul_rn(p_sl[k], t);
+      if (in) a.hout[(size_t)co * plane + ((size_t)n * a.H + y) * a.W + xo] = h;
+      const uint32_t bit = (__fadd_rn(h, p_rs[k]) > 0.0f && co < a.cout) ? 1u : 0u;
+      const int sh = 16 * (b & 1) + 4 * (lane >> 4) + k;
+      if (b < 2) w01 |= bit << sh;
+      else w23 |= bit << sh;
+    }
+    if (!a.out) return;
+    w01 |= (uint32_t)__shfl_xor((int)w01, 16);
+    w01 |= (uint32_t)__shfl_xor((int)w01, 32);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 16);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 32);
+    const int q = lane >> 4;
+    const uint32_t word = ((q < 2 ? w01 : w23) >> (16 * (q & 1))) & 0xFFFFu;
+    const int y = y0 + wr + q;
+    if (y >= a.H || xo >= a.W) return;
+    const int cwo = (a.cout + 31) >> 5;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)y * a.W + xo) * cwo) + g * 2;
+    if ((g & 1) == 0 && g == (int)gridDim.y - 1) *reinterpret_cast<uint32_t*>(dst) = word;
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     p_al[k] = a.alpha[cq + k];
@@ -910,10 +1021,11 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
   conv_segment<MT, COG>(D, make_rsrc(a.in0, bytes0), vo, m, a.cw0, a.wt + (size_t)co0 * 9, coutp * 9);
   if (a.cw1 > 0) {
     // nearest 2x of the low-res tensor placed at (oh, ow); in-image positions
-    // it does not cover read as 0 bits (the reference's zero-filled concat,
-    // whose 0 entries its XNOR kernels treat as -1: csrc/bnn_model.c:130-148,
-    // csrc/bnn_conv.c:123, 162).  They are given an offset past the end of
-    // the buffer, where buffer loads return 0.
+    // it does not cover read at padoff: v1, past the end of the buffer, where
+    // buffer loads return 0 bits (the reference's zero-filled concat, whose 0
+    // entries its XNOR kernels treat as -1: csrc/bnn_model.c:130-148,
+    // csrc/bnn_conv.c:123, 162); v3, the pad pixel holding the tap bits of
+    // the concat's 0.0 (csrc/bnn_model_react.c:280-298).
     const uint32_t cw4 = (uint32_t)a.cw1 * 4u;
     uint32_t lr[NP], lc[NP];
     bool rcov[NP], ccov[NP];
@@ -928,7 +1040,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
 #pragma unroll
     for (int i = 0; i < NP; ++i)
 #pragma unroll
-      for (int k = 0; k < NP; ++k) vo[i][k] = (rcov[i] && ccov[k]) ? lr[i] + lc[k] : 0x80000000u;
+      for (int k = 0; k < NP; ++k) vo[i][k] = (rcov[i] && ccov[k]) ? lr[i] + lc[k] : a.padoff;
     conv_segment<MT, COG>(D, make_rsrc(a.in1, bytes1), vo, m, a.cw1,
                           a.wt + ((size_t)a.cw0 * coutp + co0) * 9, coutp * 9);
   }
@@ -965,6 +1077,102 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
 
   // bytes of the pixel's words the last channel group zero-fills
   const int zero_end = blockIdx.y == gridDim.y - 1 ? a.cwo * 4 : 0;
+
+  if constexpr (EPI == EPI_RX || EPI == EPI_RXPOOL || EPI == EPI_RXHEAD) {
+    // h = RPReLU(fma(A, P, B + move1) + res): the fused step and the two
+    // separately rounded operations of csrc/bnn_react_epi.c:34-55 as the
+    // reference build contracts them; tap bit = h + rsign > 0
+    // (csrc/bnn_react_ops.c:75-85)
+    const size_t plane = (size_t)a.N * HW;
+    const float *eA = a.eA + co0, *eB = a.eB + co0, *eW = a.eW + co0;
+    const float* trs = a.trs ? a.trs + co0 : nullptr;
+    auto rx = [](int32_t P, float A, float Bm, float w, float res) {
+      const float t = __fadd_rn(__fmaf_rn(A, (float)P, Bm), res);
+      return t >= 0.0f ? t : __fmul_rn(w, t);
+    };
+    float hr[MT * MT][COG];  // the shortcut at each pixel (EPI_RXPOOL pools it)
+    uint32_t bits[MT * MT];
+#pragma unroll
+    for (int p = 0; p < MT * MT; ++p) bits[p] = 0;
+#pragma unroll
+    for (int py = 0; py < MT; ++py)
+#pragma unroll
+      for (int px = 0; px < MT; ++px) {
+        const int p = py * MT + px;
+        const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
+#pragma unroll
+        for (int j = 0; j < COG; ++j) {
+          hr[p][j] = 0.0f;
+          if (!inimg[p] || co0 + j >= a.cout) continue;
+          hr[p][j] = a.res[(size_t)(co0 + j) * plane + pix];
+          const float h = rx(Pof(p, j), eA[j], eB[j], eW[j], hr[p][j]);
+          if (a.hout) a.hout[(size_t)(co0 + j) * plane + pix] = h;
+          if (trs && __fadd_rn(h, trs[j]) > 0.0f) bits[p] |= 1u << j;
+          if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h;
+        }
+        if (trs && a.out && inimg[p])
+          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, a.cout, bits[p],
+                          zero_end);
+      }
+    // the pad pixel after the last one: the tap bits of 0.0, read by a
+    // concat where its upsample does not cover (csrc/bnn_model_react.c:282)
+    if (EPI == EPI_RX && trs && a.out && tile == 0 && threadIdx.x == 0) {
+      uint32_t pb = 0;
+#pragma unroll
+      for (int j = 0; j < COG; ++j)
+        if (co0 + j < a.cout && __fadd_rn(0.0f, trs[j]) > 0.0f) pb |= 1u << j;
+      store_bits<COG>(a.out, plane, a.cwo, co0, a.cout, pb, zero_end);
+    }
+    if constexpr (EPI == EPI_RXPOOL) {
+      // 2x2 floor-mode max of P (csrc/bnn_react_opt.c:71-82) and of the
+      // highway read (0,0), (0,1), (1,0), (1,1), first of equals kept
+      // (csrc/bnn_react_opt.c:61-66); then the down epilogue on both
+      const bool pooled = y0 + 1 < a.H && x0 + 1 < a.W;
+      if (!pooled) return;
+      const int Hh = a.H >> 1, Wh = a.W >> 1;
+      const size_t hplane = (size_t)a.N * Hh * Wh, dp = ((size_t)n * Hh + ty) * Wh + tx;
+      const float* drs = a.drs ? a.drs + co0 : nullptr;
+      uint32_t b2 = 0;
+#pragma unroll
+      for (int j = 0; j < COG; ++j) {
+        if (co0 + j >= a.cout) continue;
+        int32_t pm = Pof(0, j);
+        float hm = hr[0][j];
+#pragma unroll
+        for (int p = 1; p < 4; ++p) {
+          pm = max(pm, Pof(p, j));
+          if (hr[p][j] > hm) hm = hr[p][j];
+        }
+        if (DUMP) a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
+        const float d = rx(pm, a.dA[co0 + j], a.dB[co0 + j], a.dW[co0 + j], hm);
+        a.dout[(size_t)(co0 + j) * hplane + dp] = d;
+        if (drs && __fadd_rn(d, drs[j]) > 0.0f) b2 |= 1u << j;
+      }
+      if (drs && a.out2) store_bits<COG>(a.out2, dp, a.cwo, co0, a.cout, b2, zero_end);
+    }
+    if constexpr (EPI == EPI_RXHEAD) {
+      // bias, then channels in order, one fused step each
+      // (csrc/bnn_react_opt.c:33-41); one group holds every channel
+      const int pix = y0 * a.W + x0;
+      size_t lbase = (size_t)n * a.ncls * HW + pix, lstride = HW;
+      if (a.pcols > 0) {
+        const int pr = a.prow0 + (int)n / a.pcols, pc = (int)n % a.pcols;
+        const int sy = pr * a.H + y0, sx = pc * a.W + x0;
+        if (sy >= a.sH || sx >= a.sW) return;
+        lbase = (size_t)sy * a.sW + sx;
+        lstride = (size_t)a.sH * a.sW;
+      }
+#pragma unroll 1
+      for (int o = 0; o < a.ncls; ++o) {
+        float accf = a.hb[o];
+#pragma unroll
+        for (int j = 0; j < COG; ++j)
+          if (j < a.cout) accf = __fmaf_rn(a.hw[o * a.cout + j], hr[0][j], accf);
+        a.logits[lbase + (size_t)o * lstride] = accf;
+      }
+    }
+    return;
+  }
   const int32_t* lo1 = a.f1.lo + co0;
   const uint32_t* wd1 = a.f1.wid + co0;
   uint32_t bits[MT * MT];
@@ -1054,6 +1262,155 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       a.logits[lbase + (size_t)o * lstride] = accf;
     }
   }
+}
+
+// ------------------------------------------------------------------------
+// v3 1x1 projection (real weights, no bias) on the matrix cores
+// ------------------------------------------------------------------------
+// out[co][q] = chain over ci from 0 of fma(W[co][ci], x[ci][q], acc) from +0
+// (csrc/bnn_realin_blk.h:59-70): each K = 1 MFMA step is that fma, exactly.
+// A wave owns 64 consecutive plane positions q0 + l (B block l/16, column
+// l%16) and G groups of 16 output channels.  Per four input channels one
+// A register per group holds their weights (lanes 16k + i = W[16g + i][4c + k],
+// block k broadcast by CBSZ = 2, ABID = k).  The concat of a decoder reads
+// channels past c0 from the nearest-2x upsample of x1; positions it does not
+// cover, and channels past cin, read 0, which leaves the chain unchanged
+// (w*0 is +-0 and the chain never holds -0).
+template <int G, int K>
+__device__ __forceinline__ void proj_step(f32x16 (&acc)[G], const float (&wa)[G], const float (&xb)[4]) {
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) acc[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(wa[gi], xb[K], acc[gi], 2, K, 0);
+}
+template <int G, int... K>
+__device__ __forceinline__ void proj_steps(f32x16 (&acc)[G], const float (&wa)[G], const float (&xb)[4],
+                                           std::integer_sequence<int, K...>) {
+  (proj_step<G, K>(acc, wa, xb), ...);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long HW = (long)a.H * a.W, nq = (long)a.N * HW;
+  const long q0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64;
+  if (q0 >= nq) return;  // whole waves
+  const long q = q0 + lane;
+  const bool qok = q < nq;
+  const int ngrp = (a.cout + 15) / 16, nquad = (a.cin + 3) / 4;
+  const int g0 = blockIdx.y * G;
+  const size_t plane1 = (size_t)a.N * a.h1 * a.w1;
+  size_t off1 = 0;
+  bool cov = false;
+  if (a.x1 && qok) {
+    const long n = q / HW, rem = q - n * HW;
+    const int y = (int)(rem / a.W), x = (int)(rem - (long)y * a.W);
+    const int uy = y - a.oh, ux = x - a.ow;
+    cov = (unsigned)uy < (unsigned)a.uh && (unsigned)ux < (unsigned)a.uw;
+    if (cov) off1 = ((size_t)n * a.h1 + (uy >> 1)) * a.w1 + (ux >> 1);
+  }
+  f32x16 acc[G];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[gi][r] = 0.0f;
+  const float* wq = a.w + (size_t)g0 * nquad * 64 + lane;
+#pragma unroll 2
+  for (int c4 = 0; c4 < nquad; ++c4) {
+    float wa[G], xb[4];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) wa[gi] = g0 + gi < ngrp ? wq[((size_t)gi * nquad + c4) * 64] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ci = 4 * c4 + k;
+      float v = 0.0f;
+      if (qok && ci < a.cin) {
+        if (ci < a.c0) v = a.x0[(size_t)ci * nq + q];
+        else if (cov) v = a.x1[(size_t)(ci - a.c0) * plane1 + off1];
+      }
+      xb[k] = v;
+    }
+    proj_steps<G>(acc, wa, xb, std::make_integer_sequence<int, 4>{});
+  }
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int co = 16 * (g0 + gi) + 4 * (lane >> 4) + (r & 3);
+      const long qq = q0 + 16 * (r >> 2) + (lane & 15);
+      if (co < a.cout && qq < nq) a.out[(size_t)co * nq + qq] = acc[gi][r];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------
+// simple kernels for the v3 batch-1 kernel ABI
+// ------------------------------------------------------------------------
+// t = A*acc + B + res + move1 (form 0: csrc/bnn_react_ops.c:47, contracted to
+// fma(A, acc, B) then two adds) or A*acc + (B + move1) + res (form 1:
+// csrc/bnn_react_epi.c:30,53,75, fma(A, acc, B + move1) then one add);
+// out = t >= 0 ? t : prelu_w * t.  acc: 0 int32, 1 int16, 2 float.
+__global__ void k_react_epi(const void* __restrict__ acc, int kind, const float* __restrict__ res,
+                            float* __restrict__ out, int C, long HW, const float* __restrict__ A,
+                            const float* __restrict__ B, const float* __restrict__ m,
+                            const float* __restrict__ w, int form) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)C * HW) return;
+  const int c = (int)(i / HW);
+  const float v = kind == 0 ? (float)((const int32_t*)acc)[i]
+                  : kind == 1 ? (float)((const int16_t*)acc)[i]
+                              : ((const float*)acc)[i];
+  float t;
+  if (form == 0) t = __fadd_rn(__fadd_rn(__fmaf_rn(A[c], v, B[c]), res[i]), m[c]);
+  else t = __fadd_rn(__fmaf_rn(A[c], v, __fadd_rn(B[c], m[c])), res[i]);
+  out[i] = t >= 0.0f ? t : __fmul_rn(w[c], t);
+}
+
+// sign(x + rsign) as +-1 (csrc/bnn_react_ops.c:75-85)
+__global__ void k_react_tap(const float* __restrict__ x, int8_t* __restrict__ out, int C, long HW,
+                            const float* __restrict__ rsign) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)C * HW) return;
+  out[i] = __fadd_rn(x[i], rsign[i / HW]) > 0.0f ? 1 : -1;
+}
+
+// k x k / stride max from -inf, window row-major, first of equals kept
+// (csrc/bnn_react_ops.c:89-107)
+__global__ void k_maxpool_real(const float* __restrict__ x, float* __restrict__ out, int C, int H, int W, int k,
+                               int stride) {
+  const int Ho = (H - k) / stride + 1, Wo = (W - k) / stride + 1;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)C * Ho * Wo) return;
+  const int c = (int)(i / ((long)Ho * Wo)), r = (int)(i % ((long)Ho * Wo)), oy = r / Wo, ox = r % Wo;
+  float mx = -__builtin_inff();
+  for (int ky = 0; ky < k; ++ky)
+    for (int kx = 0; kx < k; ++kx) {
+      const float v = x[((size_t)c * H + oy * stride + ky) * W + ox * stride + kx];
+      if (v > mx) mx = v;
+    }
+  out[i] = mx;
+}
+
+// 3x3 / pad 1 / stride 1, +-1 (or any int8) weights: per output one chain,
+// input channels outermost, taps row-major inside, taps outside the image
+// skipped, then alpha * acc (csrc/bnn_realin_blk.h:111-147)
+__global__ void k_conv3_chain(const float* __restrict__ x, const int8_t* __restrict__ wsign,
+                              const float* __restrict__ alpha, float* __restrict__ out, int cin, int H, int W,
+                              int cout) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)cout * H * W) return;
+  const int co = (int)(i / ((long)H * W)), r = (int)(i % ((long)H * W)), oy = r / W, ox = r % W;
+  float acc = 0.0f;
+  for (int ci = 0; ci < cin; ++ci)
+    for (int ky = 0; ky < 3; ++ky) {
+      const int iy = oy + ky - 1;
+      if (iy < 0 || iy >= H) continue;
+      for (int kx = 0; kx < 3; ++kx) {
+        const int ix = ox + kx - 1;
+        if (ix < 0 || ix >= W) continue;
+        acc = __fmaf_rn((float)wsign[((size_t)co * cin + ci) * 9 + ky * 3 + kx],
+                        x[((size_t)ci * H + iy) * W + ix], acc);
+      }
+    }
+  out[i] = __fmul_rn(alpha[co], acc);
 }
 
 // ------------------------------------------------------------------------
@@ -1223,7 +1580,10 @@ hipError_t go_bconv(BconvArgs a, hipStream_t s) {
   a.dtw = make_fastdiv(tW);
   const int groups = (a.cout + COG - 1) / COG;
   const uint32_t b0 = (uint32_t)((size_t)a.N * a.H * a.W * a.cw0 * 4);
-  const uint32_t b1 = a.in1 ? (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4) : 0u;
+  // a pad pixel (v3) lies right after the low-res tensor
+  const uint32_t b1 = a.in1 ? (uint32_t)((size_t)(a.N * a.h1 * a.w1 + (a.padoff != 0x80000000u ? 1 : 0)) *
+                                         a.cw1 * 4)
+                            : 0u;
   hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for((long)ntiles), groups), dim3(kBlock), 0, s,
                      a, b0, b1);
   return hipGetLastError();
@@ -1248,7 +1608,9 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   if (a.N <= 0 || a.H <= 0 || a.W <= 0) return hipSuccess;
   // byte offsets are 32-bit and 0x80000000 marks "reads 0": tensors stay below 2 GiB
   if ((size_t)a.N * a.H * a.W * (a.cw0 > 0 ? a.cw0 : 1) * 4 >= 0x80000000ull) return hipErrorInvalidValue;
-  if (a.in1 && (size_t)a.N * a.h1 * a.w1 * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
+  if (a.in1 && (size_t)(a.N * a.h1 * a.w1 + 1) * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
+  if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4))
+    return hipErrorInvalidValue;
   switch (epi) {
     case EPI_FOLD:
       if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);
@@ -1265,6 +1627,20 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
     case EPI_P:
       if (mt == 1) return go_bconv_cog<1, EPI_P, false>(a, cog, s);
       if (mt == 2) return go_bconv_cog<2, EPI_P, false>(a, cog, s);
+      break;
+    case EPI_RX:
+      if (!a.res || !a.eA) break;
+      if (mt == 1) return dump ? go_bconv_cog<1, EPI_RX, true>(a, cog, s) : go_bconv_cog<1, EPI_RX, false>(a, cog, s);
+      break;
+    case EPI_RXPOOL:
+      if (!a.res || !a.eA || !a.dA || !a.dout) break;
+      if (mt == 2) return dump ? go_bconv_cog<2, EPI_RXPOOL, true>(a, cog, s)
+                               : go_bconv_cog<2, EPI_RXPOOL, false>(a, cog, s);
+      break;
+    case EPI_RXHEAD:
+      if (mt != 1 || !a.res || !a.eA || a.cout > cog) break;
+      if (cog == 16) return dump ? go_bconv<1, 16, EPI_RXHEAD, true>(a, s) : go_bconv<1, 16, EPI_RXHEAD, false>(a, s);
+      if (cog == 32) return dump ? go_bconv<1, 32, EPI_RXHEAD, true>(a, s) : go_bconv<1, 32, EPI_RXHEAD, false>(a, s);
       break;
   }
   return hipErrorInvalidValue;
@@ -1287,11 +1663,11 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s) {
     const int tilesH = (a.H + 4 * WR - 1) / (4 * WR), tilesW = (a.W + 16 * WC - 1) / (16 * WC);
     dim3 grid((unsigned)((long)a.N * tilesH * tilesW), (unsigned)((a.cout + 15) / 16));
     if (a.cin % kRealMfmaCI)
-      hipLaunchKernelGGL((k_real_mfma<WR, WC, true>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH,
-                         tilesW);
+      hipLaunchKernelGGL((k_real_mfma<WR, WC, true, false>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes,
+                         tilesH, tilesW);
     else
-      hipLaunchKernelGGL((k_real_mfma<WR, WC, false>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes, tilesH,
-                         tilesW);
+      hipLaunchKernelGGL((k_real_mfma<WR, WC, false, false>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes,
+                         tilesH, tilesW);
     return hipGetLastError();
   }
   const int tilesH = (a.H + RT - 1) / RT, tilesW = (a.W + RW - 1) / RW;
@@ -1308,6 +1684,78 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s) {
 #undef BNN_RG
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_proj(const ProjArgs& a, hipStream_t s) {
+  const long nq = (long)a.N * a.H * a.W;
+  if (nq <= 0 || a.cout <= 0) return hipSuccess;
+  if (!a.x0 || !a.w || !a.out || a.c0 < 0 || a.c0 > a.cin || (a.c0 < a.cin && !a.x1)) return hipErrorInvalidValue;
+  const int ngrp = (a.cout + 15) / 16;
+  const long waves = (nq + 63) / 64;
+  // groups per wave: all of them while the launch still has ~2048 waves
+  // (each output is a chain of cin dependent steps, so deep layers with few
+  // positions need the groups spread over waves)
+  int G = 8;
+  while (G > 1 && (G / 2 >= ngrp || waves * ((ngrp + G - 1) / G) < 2048)) G /= 2;
+  dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((ngrp + G - 1) / G));
+  switch (G) {
+    case 1: hipLaunchKernelGGL(k_proj<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(k_proj<2>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(k_proj<4>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(k_proj<8>, grid, dim3(256), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_react_epi(const void* acc, int kind, const float* res, float* out, int C, long HW,
+                            const float* A, const float* B, const float* move1, const float* prelu_w, int form,
+                            hipStream_t s) {
+  const long n = (long)C * HW;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_react_epi, dim3(blocks_for(n)), dim3(kBlock), 0, s, acc, kind, res, out, C, HW, A, B, move1,
+                     prelu_w, form);
+  return hipGetLastError();
+}
+
+hipError_t launch_react_tap(const float* x, int8_t* out, int C, long HW, const float* rsign, hipStream_t s) {
+  const long n = (long)C * HW;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_react_tap, dim3(blocks_for(n)), dim3(kBlock), 0, s, x, out, C, HW, rsign);
+  return hipGetLastError();
+}
+
+hipError_t launch_maxpool_real(const float* x, float* out, int C, int H, int W, int k, int stride, hipStream_t s) {
+  if (k <= 0 || stride <= 0 || H < k || W < k) return hipSuccess;
+  const long n = (long)C * ((H - k) / stride + 1) * ((W - k) / stride + 1);
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_maxpool_real, dim3(blocks_for(n)), dim3(kBlock), 0, s, x, out, C, H, W, k, stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv3_chain(const float* x, const int8_t* wsign, const float* alpha, float* out, int cin, int H,
+                              int W, int cout, hipStream_t s) {
+  const long n = (long)cout * H * W;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_conv3_chain, dim3(blocks_for(n)), dim3(kBlock), 0, s, x, wsign, alpha, out, cin, H, W,
+                     cout);
+  return hipGetLastError();
+}
+
+hipError_t launch_react_in(const RealArgs& a, hipStream_t s) {
+  if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
+  if (!a.wm || !a.pw || !a.hout) return hipErrorInvalidValue;
+  const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
+  if (xbytes >= kRealFar) return hipErrorInvalidValue;
+  constexpr int WR = BNN_MWR, WC = BNN_MWC;
+  const int tilesH = (a.H + 4 * WR - 1) / (4 * WR), tilesW = (a.W + 16 * WC - 1) / (16 * WC);
+  dim3 grid((unsigned)((long)a.N * tilesH * tilesW), (unsigned)((a.cout + 15) / 16));
+  if (a.cin % kRealMfmaCI)
+    hipLaunchKernelGGL((k_real_mfma<WR, WC, true, true>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes,
+                       tilesH, tilesW);
+  else
+    hipLaunchKernelGGL((k_real_mfma<WR, WC, false, true>), grid, dim3(64 * WR * WC), 0, s, a, (uint32_t)xbytes,
+                       tilesH, tilesW);
   return hipGetLastError();
 }
 

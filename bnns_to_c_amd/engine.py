@@ -30,6 +30,8 @@ CLI_PATH = os.path.join(LIB_DIR, "bnn_infer")
 CLI_STEM_PATH = os.path.join(LIB_DIR, "bnn_infer_stem")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "bnn_model.h")
 HEADER_STEM = os.path.join(os.path.dirname(HERE), "include", "bnn_model_stem.h")
+HEADER_REACT = os.path.join(os.path.dirname(HERE), "include", "bnn_model_react.h")
+CLI_REACT_PATH = os.path.join(LIB_DIR, "bnn_infer_react")
 
 BNN_OK, BNN_EBLOB, BNN_EARG, BNN_EHIP = 0, 1, 2, 3
 
@@ -88,6 +90,18 @@ def lib() -> C.CDLL:
     L.bnn_stem_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
     L.bnn_stem_stream.argtypes = [_vp]
     L.bnn_stem_stream.restype = _vp
+    # v3 (ReActNet real highway), include/bnn_model_react.h
+    L.bnn_react_blob_check.argtypes = [C.c_char_p]
+    L.bnn_react_load_status.argtypes = [C.c_char_p, C.POINTER(_vp)]
+    L.bnn_free_react.argtypes = [_vp]
+    L.bnn_forward_react.argtypes = [_vp, _f32, _ci, _ci, _f32]
+    L.bnn_react_forward_batch.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32]
+    L.bnn_react_forward_device.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
+    L.bnn_react_forward_debug.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32, STAGE_CB, _vp]
+    L.bnn_react_forward_patched.argtypes = [_vp, _f32, _ci, _ci, _f32, _ci]
+    L.bnn_react_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
+    L.bnn_react_stream.argtypes = [_vp]
+    L.bnn_react_stream.restype = _vp
     L.bnn_prof_enable.argtypes = [_ci]
     L.bnn_prof_count.restype = _ci
     L.bnn_prof_get.argtypes = [_ci, C.c_char_p, _ci, C.c_char_p, _ci, C.POINTER(C.c_double),
@@ -240,6 +254,24 @@ class StemEngine(Engine):
         ints = (C.c_int * 10).from_address(self.h.value)
         self.has_stem, self.n_stem_layers = ints[5], ints[6]
         self.stem_channels = ints[9]
+
+
+class ReactEngine(Engine):
+    """A loaded v3 (ReActNet real-highway) model on the GPU (the reference's
+    ModelR*, csrc/bnn_model_react.h:82-98); the same methods as Engine.
+    forward_debug returns the stages include/bnn_model_react.h lists."""
+
+    _api = "bnn_react_"
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().bnn_free_react(self.h)
+            self.h = None
+
+
+def react_blob_check(path: str) -> None:
+    """Parse and validate a v3 (ReActNet) blob on the host only."""
+    _check(lib().bnn_react_blob_check(path.encode()))
 
 
 # ---------------------------------------------------------------- profiler --

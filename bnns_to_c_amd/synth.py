@@ -208,6 +208,27 @@ def make_input(seed: int, n: int, n_bands: int = 120, h: int = 32, w: int = 32) 
     return rng.standard_normal((n, n_bands, h, w), dtype=np.float32)
 
 
+def react_rand_cube(n_bands: int, h: int, w: int) -> np.ndarray:
+    """The v3 CLI's "rand" cube [n_bands, h, w]: xorshift64 (13, 7, 17) from
+    88172645463325252, two uniforms ((s >> 11) + 0.5) / 2^53 per value and
+    Box-Muller sqrt(-2 ln u0) cos(2 pi u1) in double, rounded to float
+    (csrc/main_react.c:28-40).  Python's math module calls the same libm."""
+    import math
+    n = n_bands * h * w
+    out = np.empty(n, np.float32)
+    s = 88172645463325252
+    m64 = (1 << 64) - 1
+    for i in range(n):
+        u = []
+        for _ in range(2):
+            s ^= (s << 13) & m64
+            s ^= s >> 7
+            s ^= (s << 17) & m64
+            u.append(((s >> 11) + 0.5) / 9007199254740992.0)
+        out[i] = math.sqrt(-2.0 * math.log(u[0])) * math.cos(6.283185307179586 * u[1])
+    return out.reshape(n_bands, h, w)
+
+
 # ------------------------------------------------- isolated-kernel configs --
 def make_bits(seed: int, n: int, h: int, w: int, c: int) -> np.ndarray:
     """Bernoulli(0.5) +-1 activations int8 [n, c, h, w]."""

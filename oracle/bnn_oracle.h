@@ -142,6 +142,8 @@ void orr_epi_int(const int32_t *P, const float *res, float *out, int C, int HW,
                  const float *A, const float *B, const float *move1, const float *prelu_w);
 void orr_epi_real(const float *x, const float *res, float *out, int C, int HW,
                   const float *A, const float *B, const float *move1, const float *prelu_w);
+void orr_epi_plain(const void *acc, int is_int, const float *res, float *out, int C, int HW,
+                   const float *A, const float *B, const float *move1, const float *prelu_w);
 void orr_tap(const float *x, int8_t *out, int C, int HW, const float *rsign);
 void orr_maxpool_real(const float *x, float *out, int C, int H, int W);
 void orr_up_cat(const float *skip, int sC, int sH, int sW, const float *x, int xC, int hH, int hW,

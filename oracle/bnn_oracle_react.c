@@ -256,6 +256,20 @@ void orr_epi_real(const float *x, const float *res, float *out, int C, int HW,
     }
 }
 
+/* the first epilogue form, which the forward does not call: t = A*acc + B +
+ * res + move1 in that order, the first product and add fused
+ * (csrc/bnn_react_ops.c:36-70); acc int32 (is_int) or float */
+void orr_epi_plain(const void *acc, int is_int, const float *res, float *out, int C, int HW,
+                   const float *A, const float *B, const float *move1, const float *prelu_w) {
+    for (int c = 0; c < C; ++c)
+        for (long p = 0; p < HW; ++p) {
+            const size_t i = (size_t)c * HW + p;
+            const float v = is_int ? (float)((const int32_t *)acc)[i] : ((const float *)acc)[i];
+            const float t = (fmaf(A[c], v, B[c]) + res[i]) + move1[c];
+            out[i] = t >= 0.0f ? t : prelu_w[c] * t;
+        }
+}
+
 /* sign(x + rsign) as +-1, x + rsign == 0 -> -1 (csrc/bnn_react_ops.c:75-85) */
 void orr_tap(const float *x, int8_t *out, int C, int HW, const float *rsign) {
     for (int c = 0; c < C; ++c)

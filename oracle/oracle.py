@@ -361,6 +361,7 @@ class ReactOracle:
         L.orr_epi_int.argtypes = [_i32, _f32, _f32, _ci, _ci, _f32, _f32, _f32, _f32]
         L.orr_epi_real.argtypes = [_f32, _f32, _f32, _ci, _ci, _f32, _f32, _f32, _f32]
         L.orr_tap.argtypes = [_f32, _i8, _ci, _ci, _f32]
+        L.orr_epi_plain.argtypes = [C.c_void_p, _ci, _f32, _f32, _ci, _ci, _f32, _f32, _f32, _f32]
         L.orr_maxpool_real.argtypes = [_f32, _f32, _ci, _ci, _ci]
         L.orr_up_cat.argtypes = [_f32, _ci, _ci, _ci, _f32, _ci, _ci, _ci, _f32]
         L.orr_head.argtypes = [_f32, _f32, _f32, _f32, _ci, _ci, _ci]
@@ -401,6 +402,17 @@ class ReactOracle:
         else:
             x = np.ascontiguousarray(acc, np.float32)
             self.lib.orr_epi_real(_p(x, _f32), _p(res, _f32), _p(out, _f32), c, res[0].size, *prm)
+        return out
+
+    def epi_plain(self, acc, res, A, B, move1, prelu_w):
+        """the react_epilogue_int / _real order (t = A*acc + B + res + move1)"""
+        res = np.ascontiguousarray(res, np.float32)
+        is_int = np.asarray(acc).dtype.kind == "i"
+        a = np.ascontiguousarray(acc, np.int32 if is_int else np.float32)
+        out = np.zeros(res.shape, np.float32)
+        prm = [_p(np.ascontiguousarray(v, np.float32), _f32) for v in (A, B, move1, prelu_w)]
+        self.lib.orr_epi_plain(a.ctypes.data, int(is_int), _p(res, _f32), _p(out, _f32), res.shape[0],
+                               res[0].size, *prm)
         return out
 
     def tap(self, x, rsign):
@@ -508,6 +520,8 @@ class RefReact:
         L.react_proj_1x1.argtypes = [_f32, _f32, _f32, _ci, _ci, _ci, _ci]
         L.react_conv3_blk.argtypes = [_f32, _i8, _f32, _f32, _ci, _ci, _ci, _ci]
         L.react_epilogue_int_i16.argtypes = [_i16, _f32, _f32, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
+        L.react_epilogue_int.argtypes = [_i32, _f32, _f32, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
+        L.react_epilogue_real.argtypes = [_f32, _f32, _f32, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
         L.react_epilogue_real_v2.argtypes = [_f32, _f32, _f32, _ci, _ci, _ci, _f32, _f32, _f32, _f32]
         L.react_tap.argtypes = [_f32, _i8, _ci, _ci, _ci, _f32]
         L.maxpool_real_v2.argtypes = [_f32, _f32, _ci, _ci, _ci, _ci, _ci]
@@ -567,6 +581,19 @@ class RefReact:
         else:
             x = np.ascontiguousarray(acc, np.float32)
             self.lib.react_epilogue_real_v2(_p(x, _f32), _p(res, _f32), _p(out, _f32), c, H, W, *prm)
+        return out
+
+    def epi_plain(self, acc, res, A, B, move1, prelu_w):
+        res = np.ascontiguousarray(res, np.float32)
+        c, H, W = res.shape
+        out = np.zeros(res.shape, np.float32)
+        prm = [_p(np.ascontiguousarray(v, np.float32), _f32) for v in (A, B, move1, prelu_w)]
+        if np.asarray(acc).dtype.kind == "i":
+            P = np.ascontiguousarray(acc, np.int32)
+            self.lib.react_epilogue_int(_p(P, _i32), _p(res, _f32), _p(out, _f32), c, H, W, *prm)
+        else:
+            x = np.ascontiguousarray(acc, np.float32)
+            self.lib.react_epilogue_real(_p(x, _f32), _p(res, _f32), _p(out, _f32), c, H, W, *prm)
         return out
 
     def tap(self, x, rsign):

@@ -76,7 +76,8 @@ REACT_CASES = [
 ]
 # (name, blob seed, base, input seed, H, W, patch size or 0 for the whole image)
 REACT_CLI_CASES = [("react8_s4_36x52_file", 4, 8, 124, 36, 52, 0),
-                   ("react16_s5_40x56_patch16", 5, 16, 125, 40, 56, 16)]
+                   ("react16_s5_40x56_patch16", 5, 16, 125, 40, 56, 16),
+                   ("react8_s6_32x48_rand", 6, 8, -1, 32, 48, 0)]   # input seed -1: the CLI's "rand" cube
 
 
 def sha(a: np.ndarray) -> str:
@@ -320,7 +321,10 @@ def main() -> None:
             path = os.path.join(td, name + "_cli.blob")
             open(path, "wb").write(R.to_bytes(b))
             xin = os.path.join(td, name + "_in.bin")
-            synth.make_input(iseed, 1, 120, H, W)[0].tofile(xin)
+            if iseed >= 0:
+                synth.make_input(iseed, 1, 120, H, W)[0].tofile(xin)
+            else:
+                xin = "rand"
             out = os.path.join(td, name + "_cli.bin")
             spec = f"patch{P}:{xin}" if P else xin
             subprocess.run([REACT_REF_CLI, path, spec, out, str(H), str(W)], check=True, capture_output=True)

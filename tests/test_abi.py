@@ -18,9 +18,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def test_library_exports_header_symbols():
     lib = E.lib()
     names = (set(E.header_symbols()) | set(E.header_symbols(E.HEADER_STEM))
+             | set(E.header_symbols(E.HEADER_REACT))
              | set(E.header_symbols(os.path.join(ROOT, "include", "bnn_prof.h"))))
     assert {"bnn_load", "bnn_forward", "bnn_free", "bconv_dispatch", "head_1x1", "prof_report",
-            "bnn_stem_load", "bnn_stem_forward", "bnn_stem_free"} <= names
+            "bnn_stem_load", "bnn_stem_forward", "bnn_stem_free", "bnn_load_react", "bnn_forward_react",
+            "bnn_forward_react_patched", "bnn_free_react", "react_epilogue_int_i16", "react_proj_blk",
+            "bconv_blk_b4p4_i16"} <= names
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
     out = subprocess.run(["nm", "-D", "--defined-only", E.LIB_PATH], capture_output=True, text=True).stdout
@@ -38,8 +41,9 @@ def test_library_built_for_gfx950():
 def test_header_compiles_as_c(tmp_path):
     # both model headers together, as a caller of both engines includes them
     src = tmp_path / "t.c"
-    src.write_text('#include "bnn_model.h"\n#include "bnn_model_stem.h"\n#include "bnn_prof.h"\n'
-                   "int main(void){ Model *m = 0; StemModel *s = 0; (void)m; (void)s;\n"
+    src.write_text('#include "bnn_model.h"\n#include "bnn_model_stem.h"\n#include "bnn_model_react.h"\n'
+                   '#include "bnn_prof.h"\n'
+                   "int main(void){ Model *m = 0; StemModel *s = 0; ModelR *r = 0; (void)m; (void)s; (void)r;\n"
                    "  return sizeof(Conv) == sizeof(ConvS) && sizeof(Act) == sizeof(ActS) ? 0 : 1; }\n")
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
                     "-c", str(src), "-o", str(tmp_path / "t.o")], check=True)
@@ -92,3 +96,39 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run(["python", os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode != 0 and "one GPU" in (r.stderr + r.stdout)
+
+
+def test_react_model_layout_matches_reference(tmp_path):
+    """ModelR keeps csrc/bnn_model_react.h:82-88's field order (main_react.c
+    reads n_bands and n_classes), with the device pointer last; the records
+    keep the reference's sizes."""
+    src = tmp_path / "r.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "bnn_model_react.h"\n'
+                   "int main(void){ printf(\"%zu %zu %zu %zu %zu %zu\\n\", offsetof(ModelR, n_bands),"
+                   " offsetof(ModelR, n_classes), sizeof(ConvR), sizeof(BlockR),"
+                   " offsetof(ModelR, head_bias), offsetof(ModelR, dev)); return 0; }\n")
+    exe = tmp_path / "r"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    off = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()]
+    assert off[:3] == [8, 12, 56]
+    # is_down, input_real, 2 taps, 2 convs, proj, 3 epis (LP64)
+    assert off[3] == 8 + 2 * 16 + 2 * 56 + 16 + 3 * 40
+    assert off[5] == off[4] + 8
+
+
+def test_react_blob_check_host_only(tmp_path):
+    """the v3 blob check parses and validates without a GPU"""
+    from bnns_to_c_amd import blob_react as R
+    b = synth.make_blob_react(seed=1, base=8)
+    p = tmp_path / "m.blob"
+    R.write(b, str(p))
+    E.react_blob_check(str(p))
+    b.dec[3].conv2.pad = 0
+    R.write(b, str(p))
+    with pytest.raises(E.BnnError) as e:
+        E.react_blob_check(str(p))
+    assert "3x3" in str(e.value)
+    p.write_bytes(R.to_bytes(synth.make_blob_react(seed=1, base=8))[:-4])
+    with pytest.raises(E.BnnError) as e:
+        E.react_blob_check(str(p))
+    assert e.value.code == E.BNN_EBLOB
