@@ -20,6 +20,9 @@ timed between device synchronisations.  Prints ONE JSON line on stdout:
   v2_stem       the v2 spectral-stem model (16-channel 1x1 stem, then the
                 binary body) at the same batch: patches/s, and its stem
                 kernel's HBM rate against the 8 TB/s peak
+  v3_react      the v3 ReActNet real-highway model at the same batch:
+                patches/s, per-kernel times, and the enc1 conv + projection
+                kernel's FP32 rate against the matrix peak
   cpu_baseline  the reference C CLI (oracle/_ref/bnn_infer, built from the
                 reference sources) timed on this host: median of reps of one
                 patch, like csrc/main.c:55-61; falls back to the checker
@@ -105,6 +108,32 @@ def cpu_baseline(blob_path: str, budget_s: float) -> dict:
                       f"OMP_NUM_THREADS={cores}"}
 
 
+def cpu_baseline_react(blob_path: str, budget_s: float):
+    """The reference v3 CLI (oracle/_ref/bnn_infer_react, built from its
+    sources) on one 32x32x120 "rand" patch, median of reps
+    (csrc/main_react.c:85-109); None where that build is absent."""
+    from oracle.oracle import REACT_REF_CLI
+    if not os.path.exists(REACT_REF_CLI):
+        return None
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    env = dict(os.environ, OMP_NUM_THREADS=str(cores))
+
+    def run(reps):
+        with tempfile.TemporaryDirectory() as td:
+            r = subprocess.run([REACT_REF_CLI, blob_path, "rand", os.path.join(td, "o.bin"), "32", "32", str(reps)],
+                               capture_output=True, text=True, env=env, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(r.stderr)
+        return float(re.search(r"# forward \S+ reps=\d+\s+median ([\d.]+) ms", r.stdout).group(1))
+    t1 = run(3)
+    reps = max(5, min(2000, int(budget_s * 1000.0 / max(t1, 1e-3))))
+    med = run(reps)
+    return {"value": round(1000.0 / max(med, 1e-3), 2), "unit": "patches/s", "cores": cores, "kind": "reference",
+            "sample": f"reference bnn_infer_react (csrc/main_react.c) built from its sources, one 32x32x120 "
+                      f"patch, median of {reps} reps = {med:.1f} ms/patch (printed to 0.1 ms), "
+                      f"OMP_NUM_THREADS={cores}"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,8 +162,14 @@ def main() -> int:
     eng = engine.Engine(blob_path)
     x = torch.from_numpy(synth.make_input(1, N)).cuda()
     y = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
-    stream = torch.cuda.current_stream()
+    # every engine enqueues on this stream and the timing events are recorded
+    # on it (a handle of 0, torch's default stream, would make the engines
+    # use their own streams, which the events would not order)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     sp = stream.cuda_stream
+    assert sp, "the timing stream must not be the default stream"
+    torch.cuda.synchronize()
 
     def step():
         eng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
@@ -284,6 +319,50 @@ def main() -> int:
         f"{stem_ms * 1e3:.1f} us, {stem_rate / 1e9:.0f} GB/s ({stem_rate / PEAK_HBM:.3f} of HBM peak)")
     seng.close()
 
+    # the v3 ReActNet model (csrc/bnn_model_react.c): float highway, taps,
+    # 1x1 projections, RPReLU epilogues; base 16, same batch and input
+    from bnns_to_c_amd import blob_react
+    br = synth.make_blob_react(seed=0, base=16)
+    react_path = os.path.join(td, "bench_react.blob")
+    blob_react.write(br, react_path)
+    reng = engine.ReactEngine(react_path)
+
+    def rstep():
+        reng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+
+    for _ in range(args.warmup):
+        rstep()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        rstep()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    v3_ms = e0.elapsed_time(e1) / args.steps
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(args.steps):
+        rstep()
+    torch.cuda.synchronize()
+    engine.prof_enable(False)
+    ragg = {}
+    for lab, op, ms, work in engine.prof_records():
+        a = ragg.setdefault(lab, [op, 0.0, 0, work])
+        a[1] += ms
+        a[2] += 1
+    rkern = [{"label": lab, "op": op, "us": round(tot / cnt * 1e3, 2)} for lab, (op, tot, cnt, _) in ragg.items()]
+    in_us = ragg["enc1.u1"][1] / ragg["enc1.u1"][2] * 1e3
+    # enc1 unit 1: the 3x3 conv (1,080 FMAs per output) and the projection
+    # (120 per output), 16 channels x 32 x 32 per patch
+    in_flops = 2.0 * N * br.enc[0].conv1.cout * H * W * br.n_bands * 10
+    in_rate = in_flops / (in_us / 1e6)
+    v3_cpu = None if args.no_cpu else cpu_baseline_react(react_path, args.cpu_budget / 2)
+    log(f"v3 ReActNet model: {v3_ms:.4f} ms/step, {N / v3_ms * 1e3:,.0f} patches/s; enc1 unit-1 kernel "
+        f"{in_us:.1f} us, {in_rate / 1e12:.1f} TFLOP/s ({in_rate / PEAK_FP32_FLOPS:.3f} of peak)")
+    for k in rkern:
+        log(f"  {k['label']:10s} {k['op']:10s} {k['us']:9.1f} us")
+    reng.close()
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -327,6 +406,13 @@ def main() -> int:
                     "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),
                     "stem_kernel_us": round(stem_ms * 1e3, 2), "stem_bytes": stem_bytes,
                     "stem_hbm_GB_s": round(stem_rate / 1e9, 1), "stem_frac": round(stem_rate / PEAK_HBM, 4)},
+        "v3_react": {"config": "v3 ReActNet real-highway model, base 16, 32x32x120, batch 1024",
+                     "ms_per_step": round(v3_ms, 5), "patches_s": round(N / v3_ms * 1e3, 1),
+                     "enc1_kernel_us": round(in_us, 2), "enc1_tflops": round(in_rate / 1e12, 3),
+                     "enc1_frac": round(in_rate / PEAK_FP32_FLOPS, 4),
+                     "enc1_algorithmic": f"{in_flops:.4g} FLOP/launch = 2 x 16 x 1024 px x 120 x (9 + 1) "
+                                         f"x {N} patches",
+                     "kernels": rkern, "cpu_baseline": v3_cpu},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

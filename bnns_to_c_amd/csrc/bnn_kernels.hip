@@ -1084,30 +1084,59 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
     // reference build contracts them; tap bit = h + rsign > 0
     // (csrc/bnn_react_ops.c:75-85)
     const size_t plane = (size_t)a.N * HW;
-    const float *eA = a.eA + co0, *eB = a.eB + co0, *eW = a.eW + co0;
-    const float* trs = a.trs ? a.trs + co0 : nullptr;
+    // the per-channel parameters through the constant address space: the
+    // kernel never writes them, and saying so makes their loads scalar
+    typedef const __attribute__((address_space(4))) float* const_f32;
+    const const_f32 eA = (const_f32)a.eA + co0, eB = (const_f32)a.eB + co0, eW = (const_f32)a.eW + co0;
+    const const_f32 trs = a.trs ? (const_f32)a.trs + co0 : nullptr;
+    // one scalar descriptor per channel plane of `base`, size 0 past cout:
+    // loads there read 0 and stores are dropped
+    auto plane_rsrc = [&](const float* base, int j, size_t psize) {
+      const bool cok = co0 + j < a.cout;
+      const uint64_t b = (uint64_t)(uintptr_t)base + (uint64_t)(cok ? co0 + j : 0) * psize * 4;
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+      const uint32_t bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)(cok ? (uint32_t)psize * 4u : 0u));
+      return make_rsrc((const void*)(uintptr_t)(((uint64_t)hi << 32) | lo), bytes);
+    };
     auto rx = [](int32_t P, float A, float Bm, float w, float res) {
       const float t = __fadd_rn(__fmaf_rn(A, (float)P, Bm), res);
       return t >= 0.0f ? t : __fmul_rn(w, t);
     };
     float hr[MT * MT][COG];  // the shortcut at each pixel (EPI_RXPOOL pools it)
     uint32_t bits[MT * MT];
-#pragma unroll
-    for (int p = 0; p < MT * MT; ++p) bits[p] = 0;
+    // every shortcut value is loaded before the first store: the stores may
+    // alias them as far as the compiler knows, and interleaved they would
+    // wait for one load at a time
 #pragma unroll
     for (int py = 0; py < MT; ++py)
 #pragma unroll
       for (int px = 0; px < MT; ++px) {
         const int p = py * MT + px;
         const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
+        bits[p] = 0;
+        // one descriptor per channel plane (a channel past cout gets size
+        // 0), the pixel's offset past the end when it lies outside the image
+        const uint32_t voff = inimg[p] ? (uint32_t)pix * 4u : 0x80000000u;
+#pragma unroll
+        for (int j = 0; j < COG; ++j) hr[p][j] = ld_f32(plane_rsrc(a.res, j, plane), voff, 0);
+      }
+#pragma unroll
+    for (int py = 0; py < MT; ++py)
+#pragma unroll
+      for (int px = 0; px < MT; ++px) {
+        const int p = py * MT + px;
+        const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
+        // no branches: a pixel outside the image stores past the end (dropped)
+        // and a channel past cout into a zero-sized plane; neither sets a bit
+        const uint32_t voff = inimg[p] ? (uint32_t)pix * 4u : 0x80000000u;
 #pragma unroll
         for (int j = 0; j < COG; ++j) {
-          hr[p][j] = 0.0f;
-          if (!inimg[p] || co0 + j >= a.cout) continue;
-          hr[p][j] = a.res[(size_t)(co0 + j) * plane + pix];
           const float h = rx(Pof(p, j), eA[j], eB[j], eW[j], hr[p][j]);
-          if (a.hout) a.hout[(size_t)(co0 + j) * plane + pix] = h;
-          if (trs && __fadd_rn(h, trs[j]) > 0.0f) bits[p] |= 1u << j;
+          if (a.hout)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h), plane_rsrc(a.hout, j, plane),
+                                                  (int)voff, 0, 0);
+          if (trs && co0 + j < a.cout && __fadd_rn(h, trs[j]) > 0.0f) bits[p] |= 1u << j;
           if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h;
         }
         if (trs && a.out && inimg[p])
@@ -1131,7 +1160,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       if (!pooled) return;
       const int Hh = a.H >> 1, Wh = a.W >> 1;
       const size_t hplane = (size_t)a.N * Hh * Wh, dp = ((size_t)n * Hh + ty) * Wh + tx;
-      const float* drs = a.drs ? a.drs + co0 : nullptr;
+      const const_f32 drs = a.drs ? (const_f32)a.drs + co0 : nullptr;
       uint32_t b2 = 0;
 #pragma unroll
       for (int j = 0; j < COG; ++j) {
@@ -1144,8 +1173,9 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
           if (hr[p][j] > hm) hm = hr[p][j];
         }
         if (DUMP) a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
-        const float d = rx(pm, a.dA[co0 + j], a.dB[co0 + j], a.dW[co0 + j], hm);
-        a.dout[(size_t)(co0 + j) * hplane + dp] = d;
+        const float d = rx(pm, ((const_f32)a.dA)[co0 + j], ((const_f32)a.dB)[co0 + j], ((const_f32)a.dW)[co0 + j], hm);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, d), plane_rsrc(a.dout, j, hplane),
+                                              (int)((uint32_t)dp * 4u), 0, 0);
         if (drs && __fadd_rn(d, drs[j]) > 0.0f) b2 |= 1u << j;
       }
       if (drs && a.out2) store_bits<COG>(a.out2, dp, a.cwo, co0, a.cout, b2, zero_end);
@@ -1287,8 +1317,68 @@ __device__ __forceinline__ void proj_steps(f32x16 (&acc)[G], const float (&wa)[G
   (proj_step<G, K>(acc, wa, xb), ...);
 }
 
+// what a wave of k_proj needs to fetch its inputs: one descriptor per
+// source (the planes of x0, and of x1 for a concat), a channel selected by
+// the scalar offset, the lane's position by the vector offset (0x80000000,
+// past every source, for a lane with nothing to read)
+struct ProjSrc {
+  __amdgpu_buffer_rsrc_t w, r0, r1;
+  uint32_t nq4, pl4;          // bytes per plane of x0 / x1
+  uint32_t voff0, voff1;
+  int nquad, g0, lane;
+};
+
+// U quads of one source: G weight registers and 4 inputs per quad, the
+// inputs of quad c4 at scalar offset so + (4*(c4 - qa) + k) * step.  The
+// offsets advance by additions only (the scalar unit is shared by the CU).
+template <int G, int U>
+__device__ __forceinline__ void proj_load(const ProjSrc& S, __amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so,
+                                          uint32_t step, int c4, float (&wa)[U][G], float (&xb)[U][4]) {
+  uint32_t wso = (uint32_t)((S.g0 * S.nquad + c4) * 256);
+#pragma unroll
+  for (int u = 0; u < U; ++u, wso += 256) {
+    uint32_t g = wso;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi, g += (uint32_t)S.nquad * 256u) wa[u][gi] = ld_f32(S.w, (uint32_t)S.lane * 4u, g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k, so += step) xb[u][k] = ld_f32(rs, vo, so);
+  }
+}
+
+// the chain steps of one batch; quads at or past qb are skipped (uniform)
+template <int G, int U>
+__device__ __forceinline__ void proj_run(f32x16 (&acc)[G], const float (&wa)[U][G], const float (&xb)[U][4], int c4,
+                                         int qb) {
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (c4 + u < qb) proj_steps<G>(acc, wa[u], xb[u], std::make_integer_sequence<int, 4>{});
+}
+
+// quads [qa, qb) of one source, batch b+1 fetched while batch b runs: each
+// output is one chain of cin dependent steps, so a wave's loads must
+// overlap its products
+template <int G, int U>
+__device__ __forceinline__ void proj_range(f32x16 (&acc)[G], const ProjSrc& S, __amdgpu_buffer_rsrc_t rs, uint32_t vo,
+                                           uint32_t so, uint32_t step, int qa, int qb) {
+  if (qa >= qb) return;
+  const uint32_t bstep = step * 4u * U;
+  float wa0[U][G], xb0[U][4], wa1[U][G], xb1[U][4];
+  proj_load<G, U>(S, rs, vo, so, step, qa, wa0, xb0);
+#pragma unroll 1
+  for (int c4 = qa; c4 < qb; c4 += 2 * U) {
+    so += bstep;
+    if (c4 + U < qb) proj_load<G, U>(S, rs, vo, so, step, c4 + U, wa1, xb1);
+    proj_run<G, U>(acc, wa0, xb0, c4, qb);
+    if (c4 + U >= qb) break;
+    so += bstep;
+    if (c4 + 2 * U < qb) proj_load<G, U>(S, rs, vo, so, step, c4 + 2 * U, wa0, xb0);
+    proj_run<G, U>(acc, wa1, xb1, c4 + U, qb);
+  }
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
+  constexpr int U = G <= 2 ? 8 : 4;  // quads per batch (two batches of registers)
   const int lane = threadIdx.x & 63;
   const long HW = (long)a.H * a.W, nq = (long)a.N * HW;
   const long q0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64;
@@ -1296,45 +1386,53 @@ __global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
   const long q = q0 + lane;
   const bool qok = q < nq;
   const int ngrp = (a.cout + 15) / 16, nquad = (a.cin + 3) / 4;
-  const int g0 = blockIdx.y * G;
-  const size_t plane1 = (size_t)a.N * a.h1 * a.w1;
-  size_t off1 = 0;
-  bool cov = false;
+  constexpr uint32_t kFar = 0x80000000u;  // plane sets stay below 2 GiB (launch_proj checks)
+  ProjSrc S;
+  const uint32_t plane1 = (uint32_t)((size_t)a.N * a.h1 * a.w1);
+  S.w = make_rsrc(a.w, (uint32_t)((size_t)ngrp * nquad * 256));
+  S.r0 = make_rsrc(a.x0, (uint32_t)((size_t)a.c0 * nq * 4));
+  S.r1 = make_rsrc(a.x1 ? a.x1 : a.x0, a.x1 ? (uint32_t)((size_t)(a.cin - a.c0) * plane1 * 4) : 0u);
+  S.nq4 = (uint32_t)nq * 4u;
+  S.pl4 = plane1 * 4u;
+  S.voff0 = qok ? (uint32_t)q * 4u : kFar;
+  S.voff1 = kFar;
   if (a.x1 && qok) {
     const long n = q / HW, rem = q - n * HW;
     const int y = (int)(rem / a.W), x = (int)(rem - (long)y * a.W);
     const int uy = y - a.oh, ux = x - a.ow;
-    cov = (unsigned)uy < (unsigned)a.uh && (unsigned)ux < (unsigned)a.uw;
-    if (cov) off1 = ((size_t)n * a.h1 + (uy >> 1)) * a.w1 + (ux >> 1);
+    if ((unsigned)uy < (unsigned)a.uh && (unsigned)ux < (unsigned)a.uw)
+      S.voff1 = (uint32_t)(((size_t)n * a.h1 + (uy >> 1)) * a.w1 + (ux >> 1)) * 4u;
   }
+  S.nquad = nquad; S.g0 = blockIdx.y * G; S.lane = lane;
   f32x16 acc[G];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[gi][r] = 0.0f;
-  const float* wq = a.w + (size_t)g0 * nquad * 64 + lane;
-#pragma unroll 2
-  for (int c4 = 0; c4 < nquad; ++c4) {
-    float wa[G], xb[4];
+  // input channels in order: the quads wholly in x0, the one quad that
+  // crosses into x1 (when c0 is not a multiple of 4), the quads of x1.
+  // Channels past cin lie past their source and read 0.
+  if (!a.x1) {
+    proj_range<G, U>(acc, S, S.r0, S.voff0, 0u, S.nq4, 0, nquad);
+  } else {
+    const int qx = a.c0 / 4;
+    proj_range<G, U>(acc, S, S.r0, S.voff0, 0u, S.nq4, 0, qx);
+    if (a.c0 % 4) {
+      float wa[1][G], xb[1][4];
+      proj_load<G, 1>(S, S.r0, S.voff0, (uint32_t)(4 * qx) * S.nq4, S.nq4, qx, wa, xb);
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) wa[gi] = g0 + gi < ngrp ? wq[((size_t)gi * nquad + c4) * 64] : 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int ci = 4 * c4 + k;
-      float v = 0.0f;
-      if (qok && ci < a.cin) {
-        if (ci < a.c0) v = a.x0[(size_t)ci * nq + q];
-        else if (cov) v = a.x1[(size_t)(ci - a.c0) * plane1 + off1];
-      }
-      xb[k] = v;
+      for (int k = 0; k < 4; ++k)
+        if (4 * qx + k >= a.c0) xb[0][k] = ld_f32(S.r1, S.voff1, (uint32_t)(4 * qx + k - a.c0) * S.pl4);
+      proj_run<G, 1>(acc, wa, xb, qx, nquad);
     }
-    proj_steps<G>(acc, wa, xb, std::make_integer_sequence<int, 4>{});
+    const int qa = (a.c0 + 3) / 4;
+    proj_range<G, U>(acc, S, S.r1, S.voff1, (uint32_t)(4 * qa - a.c0) * S.pl4, S.pl4, qa, nquad);
   }
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int co = 16 * (g0 + gi) + 4 * (lane >> 4) + (r & 3);
+      const int co = 16 * (S.g0 + gi) + 4 * (lane >> 4) + (r & 3);
       const long qq = q0 + 16 * (r >> 2) + (lane & 15);
       if (co < a.cout && qq < nq) a.out[(size_t)co * nq + qq] = acc[gi][r];
     }
@@ -1691,6 +1789,10 @@ hipError_t launch_proj(const ProjArgs& a, hipStream_t s) {
   const long nq = (long)a.N * a.H * a.W;
   if (nq <= 0 || a.cout <= 0) return hipSuccess;
   if (!a.x0 || !a.w || !a.out || a.c0 < 0 || a.c0 > a.cin || (a.c0 < a.cin && !a.x1)) return hipErrorInvalidValue;
+  // 32-bit buffer offsets, 0x80000000 past every source ("reads 0")
+  if ((long)a.c0 * nq * 4 >= 0x80000000l || (a.x1 && (long)(a.cin - a.c0) * a.N * a.h1 * a.w1 * 4 >= 0x80000000l))
+    return hipErrorInvalidValue;
+  if ((long)((a.cout + 15) / 16) * ((a.cin + 3) / 4) * 256 >= 0x80000000l) return hipErrorInvalidValue;
   const int ngrp = (a.cout + 15) / 16;
   const long waves = (nq + 63) / 64;
   // groups per wave: all of them while the launch still has ~2048 waves
