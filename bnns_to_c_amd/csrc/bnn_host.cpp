@@ -331,12 +331,33 @@ FoldHost canon_fold(const Act& a, int coutp) {
   return f;
 }
 
+// Which binary convs run on the int8 matrix cores (same results as the
+// popcount kernel either way).  By default a fold or pool conv with
+// cout % 64 == 0, an image tile that fits (mfma_conv_fits) and at least 4
+// chunks of 64 input channels: measured per layer in whole forwards, the
+// matrix-core kernel is 6-20 % faster there and slower with fewer chunks,
+// where its per-tile staging and epilogue dominate.  BNN_BCONV_MFMA=0 keeps
+// every conv on the popcount kernel, =2 takes the matrix cores wherever
+// they fit (both read when a model or layer is created).
+int mfma_conv_mode() {
+  const char* e = getenv("BNN_BCONV_MFMA");
+  if (e && !strcmp(e, "0")) return 0;
+  if (e && !strcmp(e, "2")) return 2;
+  return 1;
+}
+
 // ------------------------------------------------------------ device model
 struct DevBconv {
   int cin = 0, cout = 0, cs = 0, cw0 = 0, cw1 = 0;
   uint32_t* wt = nullptr;
   FoldDev f1{}, f2{};
+  MfmaConv mc{};  // int8 matrix-core tables when cout % 64 == 0 (mc.w null otherwise)
+  int mfma = 0;   // mfma_conv_mode() at creation
 };
+
+bool use_mfma(const DevBconv& L, int epi, int H, int W) {
+  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || mfma_nchunk(L.cw0, L.cw1) >= 4);
+}
 
 struct Workspace {
   int N = 0, H = 0, W = 0;
@@ -409,6 +430,17 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   const int coutp = pad32(c.Cout);
   if (a1 && (rc = upload_fold(D, &L->f1, *a1, coutp))) return rc;
   if (a2 && (rc = upload_fold(D, &L->f2, *a2, coutp))) return rc;
+  L->mfma = mfma_conv_mode();
+  if (c.Cout % 64 == 0 && L->mfma) {
+    std::vector<int8_t> w8(mfma_w_len(c.Cin, c.Cout, cs));
+    std::vector<int32_t> st(mfma_s_len(c.Cout));
+    mfma_conv_tables(c.packed, c.Cin, c.Cout, cs, w8.data(), st.data());
+    int8_t* dw;
+    int32_t* ds;
+    if ((rc = dev_upload(D, &dw, w8.data(), w8.size()))) return rc;
+    if ((rc = dev_upload(D, &ds, st.data(), st.size()))) return rc;
+    L->mc = MfmaConv{dw, ds, mfma_npair(L->cw0, L->cw1)};
+  }
   return BNN_OK;
 }
 
@@ -641,10 +673,17 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       a.P = dmp->P[pi++];
       if (epi == EPI_POOL) a.P2 = dmp->P2[lvl];
     }
-    int mt, cog;
-    pick_shape(epi, N, a.H, a.W, L.cout, &mt, &cog);
-    HIP_TRY(launch_bconv(a, epi, mt, cog, dump, s));
-    const char* ot = epi == EPI_POOL ? "bconv_pool" : epi == EPI_HEAD ? "bconv_head" : "bconv";
+    const bool mm = use_mfma(L, epi, a.H, a.W);
+    if (mm) {
+      HIP_TRY(launch_bconv_mfma(a, L.mc, epi, dump, s));
+    } else {
+      int mt, cog;
+      pick_shape(epi, N, a.H, a.W, L.cout, &mt, &cog);
+      HIP_TRY(launch_bconv(a, epi, mt, cog, dump, s));
+    }
+    const char* ot = epi == EPI_POOL ? (mm ? "bconv_pool_mfma" : "bconv_pool")
+                     : epi == EPI_HEAD ? "bconv_head"
+                                       : (mm ? "bconv_mfma" : "bconv");
     return mark(label, ot, (double)N * L.cout * a.H * a.W, (double)L.cin * 9);
   };
 
@@ -1310,6 +1349,10 @@ int bnn_layer_fold_pool_device(const BnnConvLayer* L, const uint32_t* d_act, int
   if (!L->L.f1.lo || !L->L.f2.lo) return set_err(BNN_EARG, "layer was created without both rules");
   if (H < 2 || W < 2) return set_err(BNN_EARG, "pool needs H, W >= 2");
   a.out = d_skip; a.out2 = d_down;
+  if (use_mfma(L->L, EPI_POOL, H, W)) {
+    HIP_TRY(launch_bconv_mfma(a, L->L.mc, EPI_POOL, false, (hipStream_t)stream));
+    return BNN_OK;
+  }
   int mt, cog;
   pick_shape(EPI_POOL, N, H, W, a.cout, &mt, &cog);
   HIP_TRY(launch_bconv(a, EPI_POOL, mt, cog, false, (hipStream_t)stream));

@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace bnn {
 
 enum Epi : int {
@@ -247,6 +249,69 @@ hipError_t launch_conv3_chain(const float* x, const int8_t* wsign, const float* 
 // side (1 or 2), cog = output channels per work-item (8/16/32).
 hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
                         hipStream_t s);
+
+// Binary conv on the int8 matrix cores (v_mfma_i32_16x16x64_i8), for
+// cout % 64 == 0 and the EPI_FOLD / EPI_POOL epilogues.  With activation
+// bits alpha in {0,1} (0 for taps outside the image) and weights w in
+// {-1,+1}, D = sum over valid taps of w*alpha and
+//   P = sum over valid taps of w*(2*alpha - 1) = 2*D - S,
+// S = sum of w over the valid taps, which depends only on which taps are
+// valid: 16 border classes (row pattern x column pattern, each of: all
+// valid, first invalid, last invalid, both invalid).  K runs over chunks of
+// two activation words (64 channels) of one input segment, a concat's
+// upsampled segment after the first (an odd segment's last chunk has an
+// empty second word); within a chunk over the 9 taps, and within a tap over
+// the two words: pair (chunk * 9 + tap) * 2 + word, 32 channels each.
+struct MfmaConv {
+  const int8_t* w;      // [coutp][npair][32] int8, +-1, 0 for padded channels and empty words
+  const int32_t* s;     // [16][coutp] S per border class
+  int npair;
+};
+inline int mfma_nchunk(int cw0, int cw1) { return (cw0 + 1) / 2 + (cw1 + 1) / 2; }
+inline int mfma_npair(int cw0, int cw1) { return 18 * mfma_nchunk(cw0, cw1); }
+// kidx sign bits -> the int8 weight table; channel layout as repack_bin
+// (a concat's upsampled channels start at word cw0)
+inline void mfma_conv_tables(const uint64_t* kbits, int cin, int cout, int cs, int8_t* w, int32_t* stab) {
+  const int cw0 = (cs ? cs : cin) / 32 + ((cs ? cs : cin) % 32 != 0);
+  const int cw1 = cs ? (cin - cs + 31) / 32 : 0;
+  const int npair = mfma_npair(cw0, cw1), nc0 = (cw0 + 1) / 2;
+  const int coutp = (cout + 63) / 64 * 64, nw = (cin * 9 + 63) / 64;
+  for (size_t i = 0; i < (size_t)coutp * npair * 32; ++i) w[i] = 0;
+  std::vector<long> T((size_t)coutp * 9, 0);
+  for (int co = 0; co < cout; ++co)
+    for (int ci = 0; ci < cin; ++ci) {
+      int wd, b, c;  // word within its segment, bit, chunk
+      if (!cs || ci < cs) { wd = ci >> 5; b = ci & 31; c = wd >> 1; }
+      else { wd = (ci - cs) >> 5; b = (ci - cs) & 31; c = nc0 + (wd >> 1); }
+      for (int t = 0; t < 9; ++t) {
+        const int k = ci * 9 + t;
+        const int v = ((kbits[(size_t)co * nw + (k >> 6)] >> (k & 63)) & 1ull) ? 1 : -1;
+        const int pr = (c * 9 + t) * 2 + (wd & 1);
+        w[((size_t)co * npair + pr) * 32 + b] = (int8_t)v;
+        T[(size_t)co * 9 + t] += v;
+      }
+    }
+  // valid rows / columns of the 3x3 window for patterns 0..3
+  static const int valid[4][3] = {{1, 1, 1}, {0, 1, 1}, {1, 1, 0}, {0, 1, 0}};
+  for (int rp = 0; rp < 4; ++rp)
+    for (int cp = 0; cp < 4; ++cp)
+      for (int co = 0; co < coutp; ++co) {
+        long sum = 0;
+        for (int ky = 0; ky < 3; ++ky)
+          for (int kx = 0; kx < 3; ++kx)
+            if (valid[rp][ky] && valid[cp][kx]) sum += T[(size_t)co * 9 + ky * 3 + kx];
+        stab[(size_t)(rp * 4 + cp) * coutp + co] = (int32_t)sum;
+      }
+}
+inline size_t mfma_w_len(int cin, int cout, int cs) {
+  const int cw0 = ((cs ? cs : cin) + 31) / 32, cw1 = cs ? (cin - cs + 31) / 32 : 0;
+  return (size_t)(cout + 63) / 64 * 64 * mfma_npair(cw0, cw1) * 32;
+}
+inline size_t mfma_s_len(int cout) { return (size_t)16 * ((cout + 63) / 64 * 64); }
+// Whether launch_bconv_mfma takes a layer of this shape (cout % 64 == 0 and
+// an image narrow enough for its LDS tile).
+bool mfma_conv_fits(int cout, int H, int W, int epi);
+hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& m, int epi, bool dump, hipStream_t s);
 hipError_t launch_real(const RealArgs& a, hipStream_t s);
 
 // Simple kernels behind the reference's batch-1 kernel ABI.

@@ -22,6 +22,7 @@
 // hold -0.
 #include <utility>
 
+#include "bnn_device.h"
 #include "bnn_kernels.h"
 
 // Multi-dword raw buffer loads, declared on the LLVM intrinsics themselves:
@@ -39,17 +40,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// gfx9 buffer descriptor word 3 for raw dword access.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0));
-}
-__device__ __forceinline__ uint32_t ld_u32(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0);
-}
 
 // Where the real conv finds patch n: in a batch [N][cin][H][W], or in one
 // scene cube [cin][sH][sW] cut into H x W patches (pcols per row), where the
@@ -864,10 +854,6 @@ __global__ __launch_bounds__(256, OCC) void k_stem_mfma(const RealArgs a, uint32
 // ------------------------------------------------------------------------
 // binary conv with fused epilogues
 // ------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-  return f.d == 1 ? n : (__umulhi(n, f.mul) >> f.shr);
-}
-
 // acc + popcount(x) as one v_bcnt_u32_b32.  Written as a chain on purpose:
 // left to itself the compiler turns the per-tap sum into popcount-into-zero
 // plus v_add3 trees, a quarter more VALU work for the same count.
