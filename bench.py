@@ -15,6 +15,9 @@ timed between device synchronisations.  Prints ONE JSON line on stdout:
                 counted) against the VALU-popcount roofline
   fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
                 32x32, batch 1024 (the benchmark's fused-kernel config)
+  cfg4          benchmark config 4: 256x256x120 patches, batch 64, base 32;
+                per-kernel times, the int8 matrix-core convs against the
+                dense int8 peak
   scene         benchmark config 3: a 956x684x120 scene by 32x32 patches,
                 device-resident and from host memory (PCIe included)
   v2_stem       the v2 spectral-stem model (16-channel 1x1 stem, then the
@@ -45,6 +48,7 @@ sys.path.insert(0, ROOT)
 # MI355X published peaks
 PEAK_FP32_FLOPS = 157.3e12          # dense FP32 matrix (MFMA); also the packed-vector figure
 PEAK_HBM = 8.0e12
+PEAK_INT8_MACS = 2.5e15             # dense int8 matrix: 5.0 POP/s = 2.5e15 MAC/s
 
 
 def valu_binop_peak() -> float:
@@ -253,6 +257,55 @@ def main() -> int:
         f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
     L.close()
 
+    # benchmark config 4: large tiles, 256 x 256 x 120, batch 64, base 32
+    # (wide layers, 512 channels at the bottleneck); the int8 matrix-core
+    # conv takes the binary convs with at least 4 chunks of 64 input
+    # channels, the popcount kernel the rest
+    b4 = synth.make_blob(seed=0, base=32)
+    p4 = os.path.join(td, "bench_cfg4.blob")
+    blob.write(b4, p4)
+    eng4 = engine.Engine(p4)
+    N4, S4 = 64, 256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    x4 = torch.randn((N4, b4.n_bands, S4, S4), generator=gen, device="cuda", dtype=torch.float32)
+    y4 = torch.empty((N4, b4.n_classes, S4, S4), dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    torch.cuda.synchronize()
+    reps4 = 5
+    e0.record(stream)
+    for _ in range(reps4):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    cfg4_ms = e0.elapsed_time(e1) / reps4
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(reps4):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    torch.cuda.synchronize()
+    engine.prof_enable(False)
+    agg4 = {}
+    for lab, op, ms, work in engine.prof_records():
+        a4 = agg4.setdefault(lab, [op, 0.0, 0, work])
+        a4[1] += ms
+        a4[2] += 1
+    cfg4_kern = []
+    for lab, (op, tot, cnt, work) in agg4.items():
+        us = tot / cnt * 1e3
+        k4 = {"label": lab, "op": op, "us": round(us, 2)}
+        if op.endswith("_mfma"):
+            k4["mac_s"] = round(work / (us / 1e6), 1)  # bit-MACs = int8 MACs
+            k4["frac_int8_peak"] = round(work / (us / 1e6) / PEAK_INT8_MACS, 4)
+        cfg4_kern.append(k4)
+    log(f"cfg4 256x256x120 b{N4} base 32: {cfg4_ms:.3f} ms/step, {N4 / cfg4_ms * 1e3:,.0f} patches/s")
+    for k4 in cfg4_kern:
+        extra = f"  {k4['frac_int8_peak']:.3f} of int8 peak" if "mac_s" in k4 else ""
+        log(f"  {k4['label']:10s} {k4['op']:16s} {k4['us']:9.1f} us{extra}")
+    eng4.close()
+    del x4, y4
+
     # benchmark config 3: a 956 x 684 x 120 scene (N(0,1) plus a per-band
     # offset U(-0.5, 0.5)) cut into 32 x 32 patches, 30 x 22 = 660 with the
     # edge patches zero past the scene; the device call reads the patches
@@ -397,6 +450,10 @@ def main() -> int:
         "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
                        "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
                        "frac": round(pool_rate / valu_binop_peak(), 4)},
+        "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
+                 "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
+                 "kernels": cfg4_kern,
+                 "int8_mfma_rule": "binary convs with >= 4 chunks of 64 input channels and 8 <= W <= 64"},
         "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
                             "past the scene), benchmark config 3",
                   "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
