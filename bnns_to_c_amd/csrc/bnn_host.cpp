@@ -353,6 +353,7 @@ struct DevBconv {
   FoldDev f1{}, f2{};
   MfmaConv mc{};  // int8 matrix-core tables when cout % 64 == 0 (mc.w null otherwise)
   int mfma = 0;   // mfma_conv_mode() at creation
+  int pair = 0;   // cin <= 16, no concat: wt holds tap pairs, 5 words per channel
 };
 
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
@@ -425,6 +426,19 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   L->cw0 = words(cs ? cs : c.Cin);
   L->cw1 = cs ? words(c.Cin - cs) : 0;
   std::vector<uint32_t> wt = repack_bin(c.packed, c.Cin, c.Cout, 9, cs);
+  L->pair = !cs && c.Cin <= 16;
+  if (L->pair) {
+    // taps 2q (low half) and 2q+1 (high half) in one word, tap 8 alone
+    const int coutp = pad32(c.Cout);
+    std::vector<uint32_t> wp((size_t)coutp * 5, 0u);
+    for (int co = 0; co < coutp; ++co)
+      for (int q = 0; q < 5; ++q) {
+        uint32_t v = wt[(size_t)co * 9 + 2 * q];
+        if (2 * q + 1 < 9) v |= wt[(size_t)co * 9 + 2 * q + 1] << 16;
+        wp[(size_t)co * 5 + q] = v;
+      }
+    wt.swap(wp);
+  }
   int rc;
   if ((rc = dev_upload(D, &L->wt, wt.data(), wt.size()))) return rc;
   const int coutp = pad32(c.Cout);
@@ -665,7 +679,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       a.uh = std::min(uH, a.H);
       a.uw = std::min(uW, a.W);
     }
-    a.wt = L.wt; a.f1 = L.f1; a.f2 = L.f2;
+    a.wt = L.wt; a.pair = L.pair; a.f1 = L.f1; a.f2 = L.f2;
     a.out = out; a.out2 = out2; a.cwo = words(L.cout);
     a.logits = logits; a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
     if (sc && epi == EPI_HEAD) { a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0; }
@@ -1324,7 +1338,7 @@ static int layer_args(const BnnConvLayer* L, const uint32_t* d_act, int N, int H
   if (N < 0 || H <= 0 || W <= 0) return set_err(BNN_EARG, "bad shape");
   *a = BconvArgs{};
   a->in0 = d_act; a->cw0 = L->L.cw0; a->N = N; a->H = H; a->W = W;
-  a->cin = L->L.cin; a->cout = L->L.cout; a->wt = L->L.wt; a->f1 = L->L.f1; a->f2 = L->L.f2;
+  a->cin = L->L.cin; a->cout = L->L.cout; a->wt = L->L.wt; a->pair = L->L.pair; a->f1 = L->L.f1; a->f2 = L->L.f2;
   a->cwo = words(L->L.cout);
   return BNN_OK;
 }

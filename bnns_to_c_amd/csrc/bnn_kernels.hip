@@ -908,6 +908,54 @@ __device__ __forceinline__ void accumulate(Acc<MT, COG>& D, const uint32_t (&av)
   }
 }
 
+// The same for an input of at most 16 channels (one word per pixel, the
+// high half zero): the words (and masks) of taps 2p and 2p+1 are packed into
+// one, tap 8 alone, and the weights come packed the same way (5 words per
+// channel), so each output channel takes 5 popcounts instead of 9.
+template <int MT, int COG>
+__device__ __forceinline__ void accumulate_pair(Acc<MT, COG>& D, const uint32_t (&av)[MT + 2][MT + 2],
+                                                const uint32_t (&m)[MT + 2][MT + 2],
+                                                const uint32_t* __restrict__ wrow) {
+  constexpr int JB = COG < BNN_BJB ? COG : BNN_BJB;
+  typedef const __attribute__((address_space(4))) uint32_t* const_u32;
+  const const_u32 wr = (const_u32)wrow;
+  uint32_t c[MT * MT][5], mm[MT * MT][5];
+#pragma unroll
+  for (int py = 0; py < MT; ++py)
+#pragma unroll
+    for (int px = 0; px < MT; ++px)
+#pragma unroll
+      for (int q = 0; q < 5; ++q) {
+        const int t0 = 2 * q, t1 = 2 * q + 1;
+        const uint32_t a0 = av[py + t0 / 3][px + t0 % 3], m0 = m[py + t0 / 3][px + t0 % 3];
+        if (t1 < 9) {
+          const uint32_t a1 = av[py + t1 / 3][px + t1 % 3], m1 = m[py + t1 / 3][px + t1 % 3];
+          c[py * MT + px][q] = a0 | (a1 << 16);
+          mm[py * MT + px][q] = (m0 & 0xFFFFu) | (m1 & 0xFFFF0000u);
+        } else {
+          c[py * MT + px][q] = a0;
+          mm[py * MT + px][q] = m0;
+        }
+      }
+#pragma unroll
+  for (int j0 = 0; j0 < COG; j0 += JB) {
+    uint32_t w5[JB][5];
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+      for (int q = 0; q < 5; ++q) w5[jj][q] = wr[(j0 + jj) * 5 + q];
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+      for (int p = 0; p < MT * MT; ++p) {
+        uint32_t d = D.d[p][j0 + jj];
+#pragma unroll
+        for (int q = 0; q < 5; ++q) d = bcnt_acc((c[p][q] ^ w5[jj][q]) & mm[p][q], d);
+        D.d[p][j0 + jj] = d;
+      }
+  }
+}
+
 template <int NP>
 __device__ __forceinline__ void load_window(uint32_t (&av)[NP][NP], __amdgpu_buffer_rsrc_t rs,
                                             const uint32_t (&vo)[NP][NP], uint32_t soff) {
@@ -1004,7 +1052,13 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
 #pragma unroll
     for (int j = 0; j < COG; ++j) D.d[p][j] = 0;
 
-  conv_segment<MT, COG>(D, make_rsrc(a.in0, bytes0), vo, m, a.cw0, a.wt + (size_t)co0 * 9, coutp * 9);
+  if (a.pair) {
+    uint32_t win[NP][NP];
+    load_window<NP>(win, make_rsrc(a.in0, bytes0), vo, 0u);
+    accumulate_pair<MT, COG>(D, win, m, a.wt + (size_t)co0 * 5);
+  } else {
+    conv_segment<MT, COG>(D, make_rsrc(a.in0, bytes0), vo, m, a.cw0, a.wt + (size_t)co0 * 9, coutp * 9);
+  }
   if (a.cw1 > 0) {
     // nearest 2x of the low-res tensor placed at (oh, ow); in-image positions
     // it does not cover read at padoff: v1, past the end of the buffer, where
@@ -1178,12 +1232,13 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
         lbase = (size_t)sy * a.sW + sx;
         lstride = (size_t)a.sH * a.sW;
       }
+      const const_f32 hw = (const_f32)a.hw, hb = (const_f32)a.hb;
 #pragma unroll 1
       for (int o = 0; o < a.ncls; ++o) {
-        float accf = a.hb[o];
+        float accf = hb[o];
 #pragma unroll
         for (int j = 0; j < COG; ++j)
-          if (j < a.cout) accf = __fmaf_rn(a.hw[o * a.cout + j], hr[0][j], accf);
+          if (j < a.cout) accf = __fmaf_rn(hw[o * a.cout + j], hr[0][j], accf);
         a.logits[lbase + (size_t)o * lstride] = accf;
       }
     }
@@ -1269,12 +1324,16 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       lstride = (size_t)a.sH * a.sW;
     }
     if (!keep) return;
+    // the head through the constant address space: scalar loads that the
+    // logits stores cannot invalidate
+    typedef const __attribute__((address_space(4))) float* const_hf;
+    const const_hf hw = (const_hf)a.hw, hb = (const_hf)a.hb;
 #pragma unroll 1
     for (int o = 0; o < a.ncls; ++o) {
-      float accf = a.hb[o];
+      float accf = hb[o];
 #pragma unroll
       for (int j = 0; j < COG; ++j)
-        if (j < a.cout) accf = __fmaf_rn(a.hw[o * a.cout + j], sg[j], accf);
+        if (j < a.cout) accf = __fmaf_rn(hw[o * a.cout + j], sg[j], accf);
       a.logits[lbase + (size_t)o * lstride] = accf;
     }
   }
@@ -1695,6 +1754,7 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   if (a.in1 && (size_t)(a.N * a.h1 * a.w1 + 1) * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
   if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4))
     return hipErrorInvalidValue;
+  if (a.pair && (a.cin > 16 || a.cw0 != 1 || a.in1)) return hipErrorInvalidValue;  // one half-word input
   switch (epi) {
     case EPI_FOLD:
       if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);
