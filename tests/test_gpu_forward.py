@@ -205,3 +205,26 @@ def test_batch_size_independent(tmp_path, N):
     torch.cuda.synchronize()
     assert _same(dy.cpu().numpy(), small)
     eng.close()
+
+
+def test_cfg4_large_tile_vs_checker(tmp_path, orc, monkeypatch):
+    """Benchmark config 4's shape (256x256x120, base 32, the default choice
+    of conv kernels, matrix cores on the wide layers): every stage of one
+    patch bitwise against the checker, and a batch of 3 whose patches match
+    their single-patch runs."""
+    monkeypatch.delenv("BNN_BCONV_MFMA", raising=False)
+    b = synth.make_blob(seed=4, base=32)
+    eng, _ = _engine(tmp_path, b)
+    model = orc.parse(B.to_bytes(b))
+    x = synth.make_input(104, 3, 120, 256, 256)
+    logits, st = eng.forward_debug(x[:1])
+    want, ref_st = model.forward(x[0], stages=True)
+    for name, arr in st.items():
+        if name != "logits":
+            assert _same(arr[0], ref_st[name]), name
+    assert _same(logits[0], want)
+    batch = eng.forward_batch(x)
+    assert _same(batch[0], want)
+    for n in (1, 2):
+        assert _same(batch[n], eng.forward_batch(x[n:n + 1])[0]), n
+    eng.close()
