@@ -405,13 +405,10 @@ hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& mc, int epi, bo
   const size_t lds = (size_t)2 * ((size_t)T.ps << T.lti);
   // as many blocks as fit on the chip at once (LDS, and three waves per
   // SIMD by registers), each walking items blockIdx.x, + gridDim.x, ...
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
   const size_t per_cu = std::min<size_t>(3, (160 * 1024) / lds);
   const size_t items = ntiles * (size_t)(a.cout / 64);
   if (items >= 0xFFFFFFFFull) return hipErrorInvalidValue;
