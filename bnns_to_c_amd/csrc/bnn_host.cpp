@@ -72,6 +72,18 @@ std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int t
     }
   return wt;
 }
+
+std::vector<uint32_t> pair_taps(const std::vector<uint32_t>& wt, int cout) {
+  const int coutp = pad32(cout);
+  std::vector<uint32_t> wp((size_t)coutp * 5, 0u);
+  for (int co = 0; co < coutp; ++co)
+    for (int q = 0; q < 5; ++q) {
+      uint32_t v = wt[(size_t)co * 9 + 2 * q];
+      if (2 * q + 1 < 9) v |= wt[(size_t)co * 9 + 2 * q + 1] << 16;
+      wp[(size_t)co * 5 + q] = v;
+    }
+  return wp;
+}
 }  // namespace bnn
 
 namespace {
@@ -427,18 +439,7 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   L->cw1 = cs ? words(c.Cin - cs) : 0;
   std::vector<uint32_t> wt = repack_bin(c.packed, c.Cin, c.Cout, 9, cs);
   L->pair = !cs && c.Cin <= 16;
-  if (L->pair) {
-    // taps 2q (low half) and 2q+1 (high half) in one word, tap 8 alone
-    const int coutp = pad32(c.Cout);
-    std::vector<uint32_t> wp((size_t)coutp * 5, 0u);
-    for (int co = 0; co < coutp; ++co)
-      for (int q = 0; q < 5; ++q) {
-        uint32_t v = wt[(size_t)co * 9 + 2 * q];
-        if (2 * q + 1 < 9) v |= wt[(size_t)co * 9 + 2 * q + 1] << 16;
-        wp[(size_t)co * 5 + q] = v;
-      }
-    wt.swap(wp);
-  }
+  if (L->pair) wt = pair_taps(wt, c.Cout);
   int rc;
   if ((rc = dev_upload(D, &L->wt, wt.data(), wt.size()))) return rc;
   const int coutp = pad32(c.Cout);

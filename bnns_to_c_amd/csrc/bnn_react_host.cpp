@@ -230,6 +230,7 @@ struct DevEpi {
 struct DevBlock {
   int cin = 0, cout = 0, cs = 0, cw0 = 0, cw1 = 0;
   uint32_t *w1 = nullptr, *w2 = nullptr;  // binary conv words (w1 unused for enc1)
+  int p1 = 0, p2 = 0;                      // w1 / w2 hold paired taps (inputs of at most 16 channels)
   float* pw = nullptr;                     // projection lanes (binary blocks)
   DevEpi e1, ea, eb;
   float *t1a = nullptr, *t1b = nullptr;    // tap1 rsign: skip part / upsampled part (decoders); t1a only otherwise
@@ -343,6 +344,8 @@ int build_device(ModelR* m) {
     L.cw1 = L.cs ? words(L.cin - L.cs) : 0;
     if (!b.input_real) {
       std::vector<uint32_t> w = repack_bin(b.conv1.packed, L.cin, L.cout, 9, L.cs);
+      L.p1 = !L.cs && L.cin <= 16;
+      if (L.p1) w = pair_taps(w, L.cout);
       if ((rc = dev_upload(D, &L.w1, w.data(), w.size()))) return rc;
       std::vector<float> pw(react_pw_lanes_len(L.cout, L.cin));
       react_pw_lanes(b.proj1.W, L.cout, L.cin, pw.data());
@@ -351,6 +354,8 @@ int build_device(ModelR* m) {
       if (L.cs && (rc = upload_pad(D, &L.t1b, b.tap1.rsign, L.cin - L.cs, L.cs))) return rc;
     }
     std::vector<uint32_t> w2 = repack_bin(b.conv2.packed, b.conv2.Cin, b.conv2.Cout, 9, 0);
+    L.p2 = b.conv2.Cin <= 16;
+    if (L.p2) w2 = pair_taps(w2, b.conv2.Cout);
     if ((rc = dev_upload(D, &L.w2, w2.data(), w2.size()))) return rc;
     if ((rc = upload_pad(D, &L.t2, b.tap2.rsign, b.tap2.C))) return rc;
     if ((rc = upload_epi(D, &L.e1, b.epi1))) return rc;
@@ -496,9 +501,9 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
     a.in0 = in0; a.in1 = in1;
     a.N = N; a.H = hs[lvl]; a.W = wsz[lvl];
     if (u == 1) {
-      a.cin = L.cin; a.cout = L.cout; a.cw0 = L.cw0; a.cw1 = L.cw1; a.wt = L.w1;
+      a.cin = L.cin; a.cout = L.cout; a.cw0 = L.cw0; a.cw1 = L.cw1; a.wt = L.w1; a.pair = L.p1;
     } else {
-      a.cin = b.conv2.Cin; a.cout = b.conv2.Cout; a.cw0 = words(a.cin); a.cw1 = 0; a.wt = L.w2;
+      a.cin = b.conv2.Cin; a.cout = b.conv2.Cout; a.cw0 = words(a.cin); a.cw1 = 0; a.wt = L.w2; a.pair = L.p2;
     }
     a.padoff = 0x80000000u;
     if (in1) {
