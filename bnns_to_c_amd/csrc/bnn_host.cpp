@@ -82,6 +82,7 @@ std::vector<uint32_t> pair_taps(const std::vector<uint32_t>& wt, int cout) {
       if (2 * q + 1 < 9) v |= wt[(size_t)co * 9 + 2 * q + 1] << 16;
       wp[(size_t)co * 5 + q] = v;
     }
+  wp.insert(wp.end(), wt.begin() + (size_t)coutp * 9, wt.end());
   return wp;
 }
 }  // namespace bnn
@@ -438,7 +439,7 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   L->cw0 = words(cs ? cs : c.Cin);
   L->cw1 = cs ? words(c.Cin - cs) : 0;
   std::vector<uint32_t> wt = repack_bin(c.packed, c.Cin, c.Cout, 9, cs);
-  L->pair = !cs && c.Cin <= 16;
+  L->pair = (cs ? cs : c.Cin) <= 16;
   if (L->pair) wt = pair_taps(wt, c.Cout);
   int rc;
   if ((rc = dev_upload(D, &L->wt, wt.data(), wt.size()))) return rc;

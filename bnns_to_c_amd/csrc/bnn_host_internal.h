@@ -32,9 +32,11 @@ inline int pad32(int c) { return (c + 31) & ~31; }
 // cs == 0) or at word cw0 + ((ci-cs)>>5) of the second (the upsampled half
 // of a concat)
 std::vector<uint32_t> repack_bin(const uint64_t* kbits, int cin, int cout, int taps, int cs);
-// A one-word (at most 16 channels) table from repack_bin recast for the
-// popcount kernel's paired taps: word q of a channel holds tap 2q in its low
-// half and tap 2q+1 in its high half (tap 8 alone), 5 words per channel.
+// A repack_bin table whose first segment is one word of at most 16
+// channels, recast for the popcount kernel's paired taps: that segment
+// becomes 5 words per channel, word q holding tap 2q in its low half and tap
+// 2q+1 in its high half (tap 8 alone); a concat's second segment follows
+// unchanged.
 std::vector<uint32_t> pair_taps(const std::vector<uint32_t>& wt, int cout);
 
 }  // namespace bnn

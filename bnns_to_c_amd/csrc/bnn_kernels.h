@@ -65,10 +65,11 @@ struct BconvArgs {
   int cin, cout;        // true channel counts
   uint32_t ntiles;      // N * tiles per patch (set by launch_bconv)
   FastDiv dper, dtw;    // tiles per patch, tiles per row (set by launch_bconv)
-  const uint32_t* wt;   // [cw0+cw1][cout][9], or (pair) [cout][5]
-  // inputs of at most 16 channels (one word, no concat): two taps share a
-  // 32-bit word, tap 2p in the low half, 2p+1 in the high half (tap 8
-  // alone), so 5 popcounts per output channel instead of 9
+  const uint32_t* wt;   // [cw0+cw1][cout][9], or (pair) [cout][5] then [cw1][cout][9]
+  // a first segment (plain input, or a concat's skip part) of at most 16
+  // channels: two taps share a 32-bit word, tap 2p in the low half, 2p+1 in
+  // the high half (tap 8 alone), so 5 popcounts per output channel there
+  // instead of 9
   int pair;
   FoldDev f1, f2;
   uint32_t* out;        // bits [N][H][W][cwo]  (EPI_FOLD/POOL)

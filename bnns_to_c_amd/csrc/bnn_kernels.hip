@@ -1081,8 +1081,10 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
     for (int i = 0; i < NP; ++i)
 #pragma unroll
       for (int k = 0; k < NP; ++k) vo[i][k] = (rcov[i] && ccov[k]) ? lr[i] + lc[k] : a.padoff;
-    conv_segment<MT, COG>(D, make_rsrc(a.in1, bytes1), vo, m, a.cw1,
-                          a.wt + ((size_t)a.cw0 * coutp + co0) * 9, coutp * 9);
+    // (after the first segment's table: 9 words per channel and word, or
+    // 5 per channel when that segment takes paired taps)
+    const size_t seg1 = a.pair ? (size_t)coutp * 5 + (size_t)co0 * 9 : ((size_t)a.cw0 * coutp + co0) * 9;
+    conv_segment<MT, COG>(D, make_rsrc(a.in1, bytes1), vo, m, a.cw1, a.wt + seg1, coutp * 9);
   }
   if (!active) return;
 
@@ -1754,7 +1756,7 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   if (a.in1 && (size_t)(a.N * a.h1 * a.w1 + 1) * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
   if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4))
     return hipErrorInvalidValue;
-  if (a.pair && (a.cin > 16 || a.cw0 != 1 || a.in1)) return hipErrorInvalidValue;  // one half-word input
+  if (a.pair && a.cw0 != 1) return hipErrorInvalidValue;  // a first segment of one half-filled word
   switch (epi) {
     case EPI_FOLD:
       if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);

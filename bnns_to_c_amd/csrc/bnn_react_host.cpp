@@ -344,7 +344,7 @@ int build_device(ModelR* m) {
     L.cw1 = L.cs ? words(L.cin - L.cs) : 0;
     if (!b.input_real) {
       std::vector<uint32_t> w = repack_bin(b.conv1.packed, L.cin, L.cout, 9, L.cs);
-      L.p1 = !L.cs && L.cin <= 16;
+      L.p1 = (L.cs ? L.cs : L.cin) <= 16;
       if (L.p1) w = pair_taps(w, L.cout);
       if ((rc = dev_upload(D, &L.w1, w.data(), w.size()))) return rc;
       std::vector<float> pw(react_pw_lanes_len(L.cout, L.cin));
