@@ -34,6 +34,8 @@ extern "C" __device__ stem_f32x2 raw_load_f32x2(__amdgpu_buffer_rsrc_t rsrc, int
     "llvm.amdgcn.raw.ptr.buffer.load.v2f32");
 extern "C" __device__ stem_f32x4 raw_load_f32x4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux) __asm(
     "llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+extern "C" __device__ void raw_store_f32x2(stem_f32x2 vdata, __amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset,
+                                           int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.v2f32");
 
 namespace bnn {
 namespace {
@@ -1147,44 +1149,76 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
     };
     float hr[MT * MT][COG];  // the shortcut at each pixel (EPI_RXPOOL pools it)
     uint32_t bits[MT * MT];
+#pragma unroll
+    for (int p = 0; p < MT * MT; ++p) bits[p] = 0;
+    // a 2x2 block's two pixels of a row move as one 8-byte access when the
+    // width is even (then both lie inside the image or neither does)
+    const bool pairs = MT == 2 && (a.W & 1) == 0;
     // every shortcut value is loaded before the first store: the stores may
     // alias them as far as the compiler knows, and interleaved they would
     // wait for one load at a time
+    if (pairs) {
 #pragma unroll
-    for (int py = 0; py < MT; ++py)
-#pragma unroll
-      for (int px = 0; px < MT; ++px) {
-        const int p = py * MT + px;
-        const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
-        bits[p] = 0;
-        // one descriptor per channel plane (a channel past cout gets size
-        // 0), the pixel's offset past the end when it lies outside the image
-        const uint32_t voff = inimg[p] ? (uint32_t)pix * 4u : 0x80000000u;
-#pragma unroll
-        for (int j = 0; j < COG; ++j) hr[p][j] = ld_f32(plane_rsrc(a.res, j, plane), voff, 0);
-      }
-#pragma unroll
-    for (int py = 0; py < MT; ++py)
-#pragma unroll
-      for (int px = 0; px < MT; ++px) {
-        const int p = py * MT + px;
-        const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
-        // no branches: a pixel outside the image stores past the end (dropped)
-        // and a channel past cout into a zero-sized plane; neither sets a bit
-        const uint32_t voff = inimg[p] ? (uint32_t)pix * 4u : 0x80000000u;
+      for (int py = 0; py < MT; ++py) {
+        const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0;
+        const uint32_t voff = inimg[py * MT] ? (uint32_t)pix * 4u : 0x80000000u;
 #pragma unroll
         for (int j = 0; j < COG; ++j) {
-          const float h = rx(Pof(p, j), eA[j], eB[j], eW[j], hr[p][j]);
-          if (a.hout)
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h), plane_rsrc(a.hout, j, plane),
-                                                  (int)voff, 0, 0);
-          if (trs && co0 + j < a.cout && __fadd_rn(h, trs[j]) > 0.0f) bits[p] |= 1u << j;
-          if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h;
+          const stem_f32x2 v = raw_load_f32x2(plane_rsrc(a.res, j, plane), (int)voff, 0, 0);
+          hr[py * MT][j] = v[0];
+          hr[py * MT + 1][j] = v[1];
         }
-        if (trs && a.out && inimg[p])
-          store_bits<COG>(a.out, ((size_t)n * a.H + y0 + py) * a.W + x0 + px, a.cwo, co0, a.cout, bits[p],
-                          zero_end);
       }
+    } else {
+#pragma unroll
+      for (int py = 0; py < MT; ++py)
+#pragma unroll
+        for (int px = 0; px < MT; ++px) {
+          const int p = py * MT + px;
+          const size_t pix = ((size_t)n * a.H + y0 + py) * a.W + x0 + px;
+          // one descriptor per channel plane (a channel past cout gets size
+          // 0), the pixel's offset past the end when it lies outside the image
+          const uint32_t voff = inimg[p] ? (uint32_t)pix * 4u : 0x80000000u;
+#pragma unroll
+          for (int j = 0; j < COG; ++j) hr[p][j] = ld_f32(plane_rsrc(a.res, j, plane), voff, 0);
+        }
+    }
+#pragma unroll
+    for (int py = 0; py < MT; ++py) {
+      const size_t row = ((size_t)n * a.H + y0 + py) * a.W + x0;
+      // no branches: a pixel outside the image stores past the end (dropped)
+      // and a channel past cout into a zero-sized plane; neither sets a bit
+      uint32_t voff[MT];
+#pragma unroll
+      for (int px = 0; px < MT; ++px) voff[px] = inimg[py * MT + px] ? (uint32_t)(row + px) * 4u : 0x80000000u;
+#pragma unroll
+      for (int j = 0; j < COG; ++j) {
+        float h[MT];
+#pragma unroll
+        for (int px = 0; px < MT; ++px) {
+          const int p = py * MT + px;
+          h[px] = rx(Pof(p, j), eA[j], eB[j], eW[j], hr[p][j]);
+          if (trs && co0 + j < a.cout && __fadd_rn(h[px], trs[j]) > 0.0f) bits[p] |= 1u << j;
+          if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h[px];
+        }
+        if (a.hout) {
+          const __amdgpu_buffer_rsrc_t hd = plane_rsrc(a.hout, j, plane);
+          if constexpr (MT == 2) {
+            if (pairs) {
+              raw_store_f32x2(stem_f32x2{h[0], h[1]}, hd, (int)voff[0], 0, 0);
+              continue;
+            }
+          }
+#pragma unroll
+          for (int px = 0; px < MT; ++px)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h[px]), hd, (int)voff[px], 0, 0);
+        }
+      }
+#pragma unroll
+      for (int px = 0; px < MT; ++px)
+        if (trs && a.out && inimg[py * MT + px])
+          store_bits<COG>(a.out, row + px, a.cwo, co0, a.cout, bits[py * MT + px], zero_end);
+    }
     // the pad pixel after the last one: the tap bits of 0.0, read by a
     // concat where its upsample does not cover (csrc/bnn_model_react.c:282)
     if (EPI == EPI_RX && trs && a.out && tile == 0 && threadIdx.x == 0) {
