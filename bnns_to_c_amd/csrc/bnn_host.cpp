@@ -359,9 +359,10 @@ int mfma_conv_mode() {
   return 1;
 }
 
-// a batch splits its binary layers into parts of at least kSplitMin
-// patches, at most kSplitMax of them, on parallel streams (enqueue_forward;
-// measured at batch 1024: two parts 3% faster than one, four 11% slower)
+// a batch splits into parts of at least kSplitMin patches, at most
+// kSplitMax of them, on parallel streams (enqueue_forward; measured at batch
+// 1024: two parts 4-5% faster than one, four parts of the binary layers 11%
+// slower)
 constexpr int kSplitMin = 128;
 constexpr int kSplitMax = 2;
 
@@ -663,33 +664,34 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   int rc;
   if ((rc = mark(nullptr, nullptr, 0, 0))) return rc;
 
-  {
-    // v1 enc1.conv1 (3x3) or the v2 stem (1x1): real conv + real fold -> a1 bits
-    RealArgs ra{};
-    ra.x = d_in;
-    ra.w = D->rw;
-    ra.wm = D->rwm;
-    ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
-    ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
-    ra.out = w.a1;
-    ra.f32 = dump ? dmp->conv1 : nullptr;
-    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
-    if (D->stem) {
-      HIP_TRY(launch_stem(ra, s));
-      if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
-    } else {
-      HIP_TRY(launch_real(ra, s));
-      if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
-    }
-  }
-
-  // The binary layers of patches [nb, nb + cnt) on stream st: every
-  // workspace tensor is [N][h][w][words], the logits [N][ncls][H][W], so a
-  // part of the batch is the same tensors offset by nb patches.
+  // The forward of patches [nb, nb + cnt) on stream st: the input is
+  // [N][bands][H][W], every workspace tensor [N][h][w][words], the logits
+  // [N][ncls][H][W], so a part of the batch is the same tensors offset by
+  // nb patches.
   int nb = 0, cnt = N;
   hipStream_t st = s;
   auto at = [&](const uint32_t* p, int lvl, int cw) -> const uint32_t* {
     return p ? p + (size_t)nb * hs[lvl] * wsz[lvl] * cw : nullptr;
+  };
+  auto first_conv = [&]() -> int {
+    // v1 enc1.conv1 (3x3) or the v2 stem (1x1): real conv + real fold -> a1 bits
+    RealArgs ra{};
+    ra.x = d_in + (size_t)nb * D->rcin * H * W;
+    ra.w = D->rw;
+    ra.wm = D->rwm;
+    ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
+    ra.N = cnt; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
+    ra.out = const_cast<uint32_t*>(at(w.a1, 0, words(D->rcout)));
+    ra.f32 = dump ? dmp->conv1 : nullptr;
+    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
+    if (D->stem) {
+      HIP_TRY(launch_stem(ra, st));
+      if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
+    } else {
+      HIP_TRY(launch_real(ra, st));
+      if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
+    }
+    return BNN_OK;
   };
   auto bconv = [&](const DevBconv& L, int epi, const uint32_t* in0, const uint32_t* in1, int lvl, int lvl1,
                    uint32_t* out, uint32_t* out2, float* logits, const char* label) -> int {
@@ -737,7 +739,8 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   static const char* enc_c2[4] = {"enc1.c2", "enc2.c2", "enc3.c2", "enc4.c2"};
   static const char* dec_c1[4] = {"dec4.c1", "dec3.c1", "dec2.c1", "dec1.c1"};
   static const char* dec_c2[4] = {"dec4.c2", "dec3.c2", "dec2.c2", "dec1.c2"};
-  auto layers = [&]() -> int {
+  auto part = [&]() -> int {
+  if ((rc = first_conv())) return rc;
   const uint32_t* x = w.a1;
   for (int i = 0; i < 4; ++i) {
     const uint32_t* hin = x;
@@ -767,15 +770,16 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   }
   return BNN_OK;
   };
-  // A large plain batch runs its binary layers in parts on parallel
-  // streams: these kernels are short and latency bound (launch, ramp and
-  // drain are a large part of each), and independent chains keep each
-  // other's gaps filled.  One stream with per-kernel events, debug dumps
-  // or scene patches.
+  // A large plain batch runs as parts on parallel streams: the binary
+  // layers are short and latency bound (launch, ramp and drain are a large
+  // part of each kernel), and independent chains keep each other's gaps
+  // filled; each part's first conv runs on its own stream too, so one part's
+  // binary layers start while the other's first conv drains.  One stream
+  // with per-kernel events, debug dumps or scene patches.
   int parts = 1;
   if (!dump && !evs && !sc)
     while (parts < kSplitMax && N >= kSplitMin * parts * 2) parts *= 2;
-  if (parts == 1) return layers();
+  if (parts == 1) return part();
   if (!D->ev_fork) {
     HIP_TRY(hipEventCreateWithFlags(&D->ev_fork, hipEventDisableTiming));
     for (int k = 0; k < kSplitMax - 1; ++k) {
@@ -789,7 +793,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     nb = (int)((long)N * k / parts);
     cnt = (int)((long)N * (k + 1) / parts) - nb;
     st = k ? D->side[k - 1] : s;
-    if ((rc = layers())) return rc;
+    if ((rc = part())) return rc;
   }
   for (int k = 1; k < parts; ++k) {
     HIP_TRY(hipEventRecord(D->ev_join[k - 1], D->side[k - 1]));
