@@ -676,14 +676,14 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   auto first_conv = [&]() -> int {
     // v1 enc1.conv1 (3x3) or the v2 stem (1x1): real conv + real fold -> a1 bits
     RealArgs ra{};
-    ra.x = d_in + (size_t)nb * D->rcin * H * W;
+    ra.x = sc ? d_in : d_in + (size_t)nb * D->rcin * H * W;  // a scene part moves prow0 instead
     ra.w = D->rw;
     ra.wm = D->rwm;
     ra.alpha = D->ralpha; ra.A = D->rA; ra.B = D->rB; ra.slope = D->rslope; ra.rsign = D->rrsign;
     ra.N = cnt; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
     ra.out = const_cast<uint32_t*>(at(w.a1, 0, words(D->rcout)));
     ra.f32 = dump ? dmp->conv1 : nullptr;
-    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
+    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0 + nb / sc->pcols; }
     if (D->stem) {
       HIP_TRY(launch_stem(ra, st));
       if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
@@ -701,7 +701,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     in1 = at(in1, lvl1, L.cw1);
     out = const_cast<uint32_t*>(at(out, lvl, cwo));
     out2 = const_cast<uint32_t*>(at(out2, lvl + 1, cwo));
-    if (logits) logits += (size_t)nb * D->ncls * H * W;
+    if (logits && !sc) logits += (size_t)nb * D->ncls * H * W;  // a scene part moves prow0 instead
     a.in0 = in0; a.in1 = in1; a.cw0 = L.cw0; a.cw1 = L.cw1;
     a.padoff = 0x80000000u;  // uncovered concat positions read 0 bits
     a.N = cnt; a.H = hs[lvl]; a.W = wsz[lvl]; a.cin = L.cin; a.cout = L.cout;
@@ -716,7 +716,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     a.wt = L.wt; a.pair = L.pair; a.f1 = L.f1; a.f2 = L.f2;
     a.out = out; a.out2 = out2; a.cwo = words(L.cout);
     a.logits = logits; a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
-    if (sc && epi == EPI_HEAD) { a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0; }
+    if (sc && epi == EPI_HEAD) {
+      a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0 + nb / sc->pcols;
+    }
     if (dump) {
       a.P = dmp->P[pi++];
       if (epi == EPI_POOL) a.P2 = dmp->P2[lvl];
@@ -774,11 +776,14 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   // layers are short and latency bound (launch, ramp and drain are a large
   // part of each kernel), and independent chains keep each other's gaps
   // filled; each part's first conv runs on its own stream too, so one part's
-  // binary layers start while the other's first conv drains.  One stream
-  // with per-kernel events, debug dumps or scene patches.
+  // binary layers start while the other's first conv drains.  A scene splits
+  // at whole patch rows.  One stream with per-kernel events or debug dumps.
   int parts = 1;
-  if (!dump && !evs && !sc)
+  if (!dump && !evs)
     while (parts < kSplitMax && N >= kSplitMin * parts * 2) parts *= 2;
+  // a scene splits at whole patch rows (its patches are numbered row by row)
+  const int unit = sc ? sc->pcols : 1;
+  if (sc && N / unit < parts) parts = 1;
   if (parts == 1) return part();
   if (!D->ev_fork) {
     HIP_TRY(hipEventCreateWithFlags(&D->ev_fork, hipEventDisableTiming));
@@ -790,8 +795,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   HIP_TRY(hipEventRecord(D->ev_fork, s));
   for (int k = 1; k < parts; ++k) HIP_TRY(hipStreamWaitEvent(D->side[k - 1], D->ev_fork, 0));
   for (int k = 0; k < parts; ++k) {
-    nb = (int)((long)N * k / parts);
-    cnt = (int)((long)N * (k + 1) / parts) - nb;
+    const int rows = N / unit;
+    nb = (int)((long)rows * k / parts) * unit;
+    cnt = (k + 1 == parts ? N : (int)((long)rows * (k + 1) / parts) * unit) - nb;
     st = k ? D->side[k - 1] : s;
     if ((rc = part())) return rc;
   }

@@ -69,3 +69,22 @@ def test_scene_errors(tmp_path):
     with pytest.raises(E.BnnError, match="multiple of 16"):
         eng.forward_patched(np.zeros((120, 40, 40), np.float32), 24)
     eng.close()
+
+
+def test_scene_split_at_patch_rows(tmp_path, orc):
+    """a scene of 306 patches (18 patch rows, edge patches ragged) runs as two
+    parts of whole patch rows on two streams: the map equals the checker's"""
+    import torch
+    b = synth.make_blob(seed=5)
+    eng = _engine(tmp_path, b)
+    H, W, P = 549, 520, 32
+    cube = _cube(6, H, W)
+    want = scene.stitch(orc.parse(B.to_bytes(b)).forward_batch(scene.cut(cube, P)), H, W)
+    d_cube = torch.from_numpy(cube).cuda()
+    d_map = torch.full((3, H, W), float("nan"), device="cuda")
+    s = torch.cuda.Stream()
+    eng.forward_patched_device(d_cube.data_ptr(), H, W, d_map.data_ptr(), P, s.cuda_stream)
+    torch.cuda.synchronize()
+    assert _same(d_map.cpu().numpy(), want)
+    assert _same(eng.forward_patched(cube, P), want)
+    eng.close()
