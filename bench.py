@@ -13,6 +13,9 @@ timed between device synchronisations.  Prints ONE JSON line on stdout:
                 matrix peak
   bconv         the 17 binary convs: binary-op/s (2 per bit-MAC, border taps
                 counted) against the VALU-popcount roofline
+  cfg1          benchmark config 1: the isolated binary conv 64->64 at
+                64x64, batch 256, int32 P out: binary-op/s against the
+                VALU-popcount roofline and the HBM rate of its bytes
   fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
                 32x32, batch 1024 (the benchmark's fused-kernel config)
   cfg4          benchmark config 4: 256x256x120 patches, batch 64, base 32;
@@ -228,6 +231,34 @@ def main() -> int:
     bin_ms = sum(k["ms"] for k in kernels if k["op"] != "conv_real")
     bin_work = sum(agg[k["label"]][3] for k in kernels if k["op"] != "conv_real")
     bin_rate = 2 * bin_work / (bin_ms / 1e3)
+
+    # benchmark config 1: the isolated binary conv, 64->64 at 64x64, batch
+    # 256, int32 P out (268 MB, the accumulator the reference's bconv
+    # returns)
+    N1, S1, C1 = 256, 64, 64
+    a1 = synth.make_bits(20, N1, S1, S1, C1)
+    L1 = engine.ConvLayer(blob.pack_kidx(synth.make_signs(21, C1, C1)), C1, C1)
+    da1 = torch.from_numpy(a1).cuda()
+    act1 = torch.empty((N1, S1, S1, C1 // 32), dtype=torch.int32, device="cuda")
+    engine.pack_act_device(da1.data_ptr(), act1.data_ptr(), N1, C1, S1, S1, sp)
+    del da1
+    P1 = torch.empty((N1, C1, S1, S1), dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(20):
+        L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    c1_ms = e0.elapsed_time(e1) / 20
+    c1_bitmacs = N1 * C1 * S1 * S1 * C1 * 9
+    c1_rate = 2 * c1_bitmacs / (c1_ms / 1e3)
+    c1_bytes = N1 * S1 * S1 * (C1 // 8) + P1.numel() * 4  # packed bits in, int32 P out
+    log(f"cfg1 bconv 64->64 64x64 b{N1}, int32 P out: {c1_ms * 1e3:.1f} us, frac {c1_rate / valu_binop_peak():.3f} "
+        f"of VALU popcount peak, {c1_bytes / (c1_ms / 1e3) / 1e9:.0f} GB/s of algorithmic HBM bytes")
+    L1.close()
+    del act1, P1
 
     # fused bconv + fold + 2x2 max-pool, 128->128 at 32x32, batch 1024
     C = 128
@@ -447,6 +478,11 @@ def main() -> int:
         "bconv": {"kernels": 17, "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
                   "frac": round(bin_rate / valu_binop_peak(), 4), "ms": round(bin_ms, 5),
                   "unit": "binary-op/s (2 per bit-MAC, border taps counted)"},
+        "cfg1": {"config": "isolated bconv 64->64, 64x64, batch 256, int32 P out (benchmark config 1)",
+                 "us": round(c1_ms * 1e3, 2), "binary_op_s": round(c1_rate, 1),
+                 "frac": round(c1_rate / valu_binop_peak(), 4),
+                 "hbm_GB_s": round(c1_bytes / (c1_ms / 1e3) / 1e9, 1),
+                 "hbm_frac": round(c1_bytes / (c1_ms / 1e3) / PEAK_HBM, 4)},
         "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
                        "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
                        "frac": round(pool_rate / valu_binop_peak(), 4)},
