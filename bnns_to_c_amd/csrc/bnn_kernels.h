@@ -94,6 +94,10 @@ struct BconvArgs {
   const float* trs;     // rsign of the tap on h -> out bits (+ the pad pixel at N*H*W), or null
   const float *dA, *dB, *dW, *drs;  // EPI_RXPOOL: the pooled-down epilogue and its tap -> out2
   float* dout;          // EPI_RXPOOL: pooled h planes at (H/2, W/2)
+  // v3 batch parts: the planes and bit tensors hold ntot patches and this
+  // call covers N of them from patch n0, its pointers already moved to n0
+  // (ntot 0: the call covers the whole batch)
+  int ntot, n0;
 };
 
 struct RealArgs {
@@ -117,7 +121,8 @@ struct RealArgs {
   // h = RPReLU(A*(alpha*acc) + B + proj) with A, B (= B + move1), slope
   // (= PReLU weight) and rsign (= the next tap's bias) above
   const float* pw;      // projection weights [ceil(cout/16)][chunk][4][64], see react_proj_lanes
-  float* hout;          // h planes [cout][N*H*W]
+  float* hout;          // h planes [cout][N*H*W]; of ntot patches when ntot > 0 (a batch part)
+  int ntot;
   float* f32b;          // projection output [N][cout][H][W]; may be null
 };
 
@@ -229,6 +234,9 @@ struct ProjArgs {
   int N, H, W, h1, w1, oh, ow, uh, uw;
   const float* w;       // react_pw_lanes layout
   float* out;           // planes [cout][N*H*W]
+  // a batch part: every plane holds ntot patches, this call N of them from
+  // patch n0, x0/x1/out already moved to n0 (ntot 0: the whole batch)
+  int ntot, n0;
 };
 // [ceil(cout/16)][ceil(cin/4)][64]: lane l of quad q holds W[16g + l%16][4q + l/16]
 inline size_t react_pw_lanes_len(int cout, int cin) { return (size_t)((cout + 15) / 16) * ((cin + 3) / 4) * 64; }

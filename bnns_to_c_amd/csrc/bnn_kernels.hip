@@ -542,7 +542,7 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
       p_rs[k] = a.rsign[cq + k];
     }
     const int xo = x0 + wc + (lane & 15);
-    const size_t plane = (size_t)a.N * HW;
+    const size_t plane = (size_t)(a.ntot ? a.ntot : a.N) * HW;
     uint32_t w01 = 0, w23 = 0;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1127,7 +1127,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
     // separately rounded operations of csrc/bnn_react_epi.c:34-55 as the
     // reference build contracts them; tap bit = h + rsign > 0
     // (csrc/bnn_react_ops.c:75-85)
-    const size_t plane = (size_t)a.N * HW;
+    const size_t plane = (size_t)(a.ntot ? a.ntot : a.N) * HW;  // positions per plane
     // the per-channel parameters through the constant address space: the
     // kernel never writes them, and saying so makes their loads scalar
     typedef const __attribute__((address_space(4))) float* const_f32;
@@ -1219,14 +1219,15 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
         if (trs && a.out && inimg[py * MT + px])
           store_bits<COG>(a.out, row + px, a.cwo, co0, a.cout, bits[py * MT + px], zero_end);
     }
-    // the pad pixel after the last one: the tap bits of 0.0, read by a
-    // concat where its upsample does not cover (csrc/bnn_model_react.c:282)
+    // the pad pixel after the last one of the whole batch: the tap bits of
+    // 0.0, read by a concat where its upsample does not cover
+    // (csrc/bnn_model_react.c:282)
     if (EPI == EPI_RX && trs && a.out && tile == 0 && threadIdx.x == 0) {
       uint32_t pb = 0;
 #pragma unroll
       for (int j = 0; j < COG; ++j)
         if (co0 + j < a.cout && __fadd_rn(0.0f, trs[j]) > 0.0f) pb |= 1u << j;
-      store_bits<COG>(a.out, plane, a.cwo, co0, a.cout, pb, zero_end);
+      store_bits<COG>(a.out, plane - (size_t)a.n0 * HW, a.cwo, co0, a.cout, pb, zero_end);
     }
     if constexpr (EPI == EPI_RXPOOL) {
       // 2x2 floor-mode max of P (csrc/bnn_react_opt.c:71-82) and of the
@@ -1235,7 +1236,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       const bool pooled = y0 + 1 < a.H && x0 + 1 < a.W;
       if (!pooled) return;
       const int Hh = a.H >> 1, Wh = a.W >> 1;
-      const size_t hplane = (size_t)a.N * Hh * Wh, dp = ((size_t)n * Hh + ty) * Wh + tx;
+      const size_t hplane = (size_t)(a.ntot ? a.ntot : a.N) * Hh * Wh, dp = ((size_t)n * Hh + ty) * Wh + tx;
       const const_f32 drs = a.drs ? (const_f32)a.drs + co0 : nullptr;
       uint32_t b2 = 0;
 #pragma unroll
@@ -1461,7 +1462,10 @@ template <int G>
 __global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
   constexpr int U = G <= 2 ? 8 : 4;  // quads per batch (two batches of registers)
   const int lane = threadIdx.x & 63;
-  const long HW = (long)a.H * a.W, nq = (long)a.N * HW;
+  // nq positions to process, sq positions per plane (a batch part: its own
+  // patches out of ntot)
+  const long HW = (long)a.H * a.W, nq = (long)a.N * HW, sq = (long)(a.ntot ? a.ntot : a.N) * HW;
+  const long nrel = (long)(a.ntot ? a.ntot - a.n0 : a.N);  // patches from this call's first to the end
   const long q0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64;
   if (q0 >= nq) return;  // whole waves
   const long q = q0 + lane;
@@ -1469,11 +1473,13 @@ __global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
   const int ngrp = (a.cout + 15) / 16, nquad = (a.cin + 3) / 4;
   constexpr uint32_t kFar = 0x80000000u;  // plane sets stay below 2 GiB (launch_proj checks)
   ProjSrc S;
-  const uint32_t plane1 = (uint32_t)((size_t)a.N * a.h1 * a.w1);
+  const uint32_t plane1 = (uint32_t)((size_t)(a.ntot ? a.ntot : a.N) * a.h1 * a.w1);
   S.w = make_rsrc(a.w, (uint32_t)((size_t)ngrp * nquad * 256));
-  S.r0 = make_rsrc(a.x0, (uint32_t)((size_t)a.c0 * nq * 4));
-  S.r1 = make_rsrc(a.x1 ? a.x1 : a.x0, a.x1 ? (uint32_t)((size_t)(a.cin - a.c0) * plane1 * 4) : 0u);
-  S.nq4 = (uint32_t)nq * 4u;
+  // each source from this call's first position to the end of its last plane
+  S.r0 = make_rsrc(a.x0, a.c0 ? (uint32_t)(((size_t)(a.c0 - 1) * sq + nrel * HW) * 4) : 0u);
+  S.r1 = make_rsrc(a.x1 ? a.x1 : a.x0,
+                   a.x1 ? (uint32_t)(((size_t)(a.cin - a.c0 - 1) * plane1 + nrel * a.h1 * a.w1) * 4) : 0u);
+  S.nq4 = (uint32_t)sq * 4u;
   S.pl4 = plane1 * 4u;
   S.voff0 = qok ? (uint32_t)q * 4u : kFar;
   S.voff1 = kFar;
@@ -1515,7 +1521,7 @@ __global__ __launch_bounds__(256) void k_proj(const ProjArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int co = 16 * (S.g0 + gi) + 4 * (lane >> 4) + (r & 3);
       const long qq = q0 + 16 * (r >> 2) + (lane & 15);
-      if (co < a.cout && qq < nq) a.out[(size_t)co * nq + qq] = acc[gi][r];
+      if (co < a.cout && qq < nq) a.out[(size_t)co * sq + qq] = acc[gi][r];
     }
   }
 }
@@ -1760,7 +1766,8 @@ hipError_t go_bconv(BconvArgs a, hipStream_t s) {
   const int groups = (a.cout + COG - 1) / COG;
   const uint32_t b0 = (uint32_t)((size_t)a.N * a.H * a.W * a.cw0 * 4);
   // a pad pixel (v3) lies right after the low-res tensor
-  const uint32_t b1 = a.in1 ? (uint32_t)((size_t)(a.N * a.h1 * a.w1 + (a.padoff != 0x80000000u ? 1 : 0)) *
+  const int nrel = a.ntot ? a.ntot - a.n0 : a.N;  // patches from this call's first to the end
+  const uint32_t b1 = a.in1 ? (uint32_t)((size_t)(nrel * a.h1 * a.w1 + (a.padoff != 0x80000000u ? 1 : 0)) *
                                          a.cw1 * 4)
                             : 0u;
   hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for((long)ntiles), groups), dim3(kBlock), 0, s,
@@ -1787,8 +1794,10 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   if (a.N <= 0 || a.H <= 0 || a.W <= 0) return hipSuccess;
   // byte offsets are 32-bit and 0x80000000 marks "reads 0": tensors stay below 2 GiB
   if ((size_t)a.N * a.H * a.W * (a.cw0 > 0 ? a.cw0 : 1) * 4 >= 0x80000000ull) return hipErrorInvalidValue;
-  if (a.in1 && (size_t)(a.N * a.h1 * a.w1 + 1) * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
-  if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4))
+  if (a.ntot && (a.n0 < 0 || a.n0 + a.N > a.ntot)) return hipErrorInvalidValue;
+  const int nrel = a.ntot ? a.ntot - a.n0 : a.N;
+  if (a.in1 && (size_t)(nrel * a.h1 * a.w1 + 1) * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
+  if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)nrel * a.h1 * a.w1 * a.cw1 * 4))
     return hipErrorInvalidValue;
   if (a.pair && a.cw0 != 1) return hipErrorInvalidValue;  // a first segment of one half-filled word
   switch (epi) {
@@ -1872,7 +1881,10 @@ hipError_t launch_proj(const ProjArgs& a, hipStream_t s) {
   if (nq <= 0 || a.cout <= 0) return hipSuccess;
   if (!a.x0 || !a.w || !a.out || a.c0 < 0 || a.c0 > a.cin || (a.c0 < a.cin && !a.x1)) return hipErrorInvalidValue;
   // 32-bit buffer offsets, 0x80000000 past every source ("reads 0")
-  if ((long)a.c0 * nq * 4 >= 0x80000000l || (a.x1 && (long)(a.cin - a.c0) * a.N * a.h1 * a.w1 * 4 >= 0x80000000l))
+  if (a.ntot && (a.n0 < 0 || a.n0 + a.N > a.ntot)) return hipErrorInvalidValue;
+  const long ntot = a.ntot ? a.ntot : a.N;
+  if ((long)a.c0 * ntot * a.H * a.W * 4 >= 0x80000000l ||
+      (a.x1 && (long)(a.cin - a.c0) * ntot * a.h1 * a.w1 * 4 >= 0x80000000l))
     return hipErrorInvalidValue;
   if ((long)((a.cout + 15) / 16) * ((a.cin + 3) / 4) * 256 >= 0x80000000l) return hipErrorInvalidValue;
   const int ngrp = (a.cout + 15) / 16;

@@ -270,6 +270,9 @@ struct BnnReactDevice {
   RWorkspace ws;
   float *stage_in = nullptr, *stage_out = nullptr;
   size_t stage_in_cap = 0, stage_out_cap = 0;
+  // the second half of a large batch runs on this stream
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -303,11 +306,15 @@ int upload_epi(BnnReactDevice* D, DevEpi* e, const EpiR& r) {
 void release(BnnReactDevice* D) {
   if (!D) return;
   if (D->stream) (void)hipStreamSynchronize(D->stream);
+  if (D->side) (void)hipStreamSynchronize(D->side);
   for (void* p : D->allocs) (void)hipFree(p);
   D->allocs.clear();
   if (D->ws.base) (void)hipFree(D->ws.base);
   if (D->stage_in) (void)hipFree(D->stage_in);
   if (D->stage_out) (void)hipFree(D->stage_out);
+  if (D->ev_fork) (void)hipEventDestroy(D->ev_fork);
+  if (D->ev_join) (void)hipEventDestroy(D->ev_join);
+  if (D->side) (void)hipStreamDestroy(D->side);
   if (D->stream) (void)hipStreamDestroy(D->stream);
   D->stream = nullptr;
 }
@@ -453,28 +460,44 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
   const bool dump = dmp && dmp->on;
   int pi = 0, rc;
   if ((rc = mark(nullptr, nullptr, 0, 0))) return rc;
+  // The forward of patches [nb, nb + cnt) of the batch on stream st.  The
+  // float planes are [C][N*h*w] and the bit tensors [N*h*w + 1][words] (a
+  // pad pixel after the whole batch), so a part is the same tensors from
+  // patch nb on: every pointer moves by nb patches, the planes keep their
+  // stride of N patches (ntot), and the pad pixel stays where it is.
+  int nb = 0, cnt = N;
+  hipStream_t st = s;
+  auto pl = [&](const float* p, int lvl) -> float* {
+    return p ? const_cast<float*>(p) + (size_t)nb * hs[lvl] * wsz[lvl] : nullptr;
+  };
+  auto bt = [&](const uint32_t* p, int lvl, int cw) -> uint32_t* {
+    return p ? const_cast<uint32_t*>(p) + (size_t)nb * hs[lvl] * wsz[lvl] * cw : nullptr;
+  };
+  auto part = [&]() -> int {
   {
     const DevBlock& L = D->blk[0];
     RealArgs ra{};
-    ra.x = d_in;
+    ra.x = sc ? d_in : d_in + (size_t)nb * D->rcin * H * W;  // a scene part moves prow0 instead
     ra.wm = D->rwm;
     ra.pw = D->rpw;
     ra.alpha = D->ralpha; ra.A = L.e1.A; ra.B = L.e1.B; ra.slope = L.e1.W; ra.rsign = L.t2;
-    ra.N = N; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
-    ra.out = w.a2[0];
-    ra.hout = w.h1[0];
+    ra.N = cnt; ra.H = H; ra.W = W; ra.cin = D->rcin; ra.cout = D->rcout;
+    ra.out = bt(w.a2[0], 0, words(D->rcout));
+    ra.hout = pl(w.h1[0], 0);
+    ra.ntot = N;
     ra.f32 = dump ? dmp->conv : nullptr;
     ra.f32b = dump ? dmp->proj : nullptr;
-    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0; }
-    HIP_TRY(launch_react_in(ra, s));
+    if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0 + nb / sc->pcols; }
+    HIP_TRY(launch_react_in(ra, st));
     if ((rc = mark("enc1.u1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 10))) return rc;
   }
   auto proj = [&](int k, const float* x0, int c0, const float* x1, int lvl1, float* out) -> int {
     const DevBlock& L = D->blk[k];
     const int lvl = level_of(k);
     ProjArgs p{};
-    p.x0 = x0; p.x1 = x1; p.c0 = c0; p.cin = L.cin; p.cout = L.cout;
-    p.N = N; p.H = hs[lvl]; p.W = wsz[lvl];
+    p.x0 = pl(x0, lvl); p.x1 = x1 ? pl(x1, lvl1) : nullptr; p.c0 = c0; p.cin = L.cin; p.cout = L.cout;
+    p.N = cnt; p.H = hs[lvl]; p.W = wsz[lvl];
+    p.ntot = N; p.n0 = nb;
     if (x1) {
       p.h1 = hs[lvl1]; p.w1 = wsz[lvl1];
       const int uH = 2 * p.h1, uW = 2 * p.w1;
@@ -484,8 +507,8 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
       p.uw = std::min(uW, p.W);
     }
     p.w = L.pw;
-    p.out = out;
-    HIP_TRY(launch_proj(p, s));
+    p.out = pl(out, lvl);
+    HIP_TRY(launch_proj(p, st));
     static char lab[9][16];
     snprintf(lab[k], sizeof lab[k], "%s.proj", kName[k]);
     return mark(lab[k], "proj", (double)N * L.cout * p.H * p.W, (double)L.cin);
@@ -498,13 +521,15 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
     const BlockR& b = block_of(m, k);
     const int lvl = level_of(k);
     BconvArgs a{};
-    a.in0 = in0; a.in1 = in1;
-    a.N = N; a.H = hs[lvl]; a.W = wsz[lvl];
+    a.N = cnt; a.H = hs[lvl]; a.W = wsz[lvl];
+    a.ntot = N; a.n0 = nb;
     if (u == 1) {
       a.cin = L.cin; a.cout = L.cout; a.cw0 = L.cw0; a.cw1 = L.cw1; a.wt = L.w1; a.pair = L.p1;
     } else {
       a.cin = b.conv2.Cin; a.cout = b.conv2.Cout; a.cw0 = words(a.cin); a.cw1 = 0; a.wt = L.w2; a.pair = L.p2;
     }
+    a.in0 = bt(in0, lvl, a.cw0);
+    a.in1 = in1 ? bt(in1, lvl1, a.cw1) : nullptr;
     a.padoff = 0x80000000u;
     if (in1) {
       a.h1 = hs[lvl1]; a.w1 = wsz[lvl1];
@@ -513,21 +538,25 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
       a.ow = a.W > uW ? (a.W - uW) / 2 : 0;
       a.uh = std::min(uH, a.H);
       a.uw = std::min(uW, a.W);
-      a.padoff = (uint32_t)((size_t)N * a.h1 * a.w1 * a.cw1 * 4);
+      a.padoff = (uint32_t)((size_t)(N - nb) * a.h1 * a.w1 * a.cw1 * 4);  // the pad pixel after the batch
     }
     a.cwo = words(a.cout);
-    a.res = res; a.hout = hout; a.eA = e.A; a.eB = e.B; a.eW = e.W; a.trs = trs; a.out = out;
+    a.res = pl(res, lvl); a.hout = pl(hout, lvl); a.eA = e.A; a.eB = e.B; a.eW = e.W; a.trs = trs;
+    a.out = bt(out, lvl, a.cwo);
     if (ed) { a.dA = ed->A; a.dB = ed->B; a.dW = ed->W; }
-    a.drs = drs; a.dout = dout; a.out2 = out2;
-    a.logits = d_logits; a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
-    if (sc && epi == EPI_RXHEAD) { a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0; }
+    a.drs = drs; a.dout = pl(dout, lvl + 1); a.out2 = bt(out2, lvl + 1, a.cwo);
+    a.logits = (d_logits && !sc) ? d_logits + (size_t)nb * D->ncls * H * W : d_logits;
+    a.hw = D->hw; a.hb = D->hb; a.ncls = D->ncls;
+    if (sc && epi == EPI_RXHEAD) {
+      a.sH = sc->sH; a.sW = sc->sW; a.pcols = sc->pcols; a.prow0 = sc->prow0 + nb / sc->pcols;
+    }
     if (dump) {
       a.P = dmp->P[pi++];
       if (epi == EPI_RXPOOL) a.P2 = dmp->P2[k];
     }
     int mt, cog;
-    pick_shape(epi, N, a.H, a.W, a.cout, &mt, &cog);
-    HIP_TRY(launch_bconv(a, epi, mt, cog, dump, s));
+    pick_shape(epi, cnt, a.H, a.W, a.cout, &mt, &cog);
+    HIP_TRY(launch_bconv(a, epi, mt, cog, dump, st));
     static char lab[9][2][16];
     snprintf(lab[k][u - 1], sizeof lab[k][u - 1], "%s.c%d", kName[k], u);
     const char* ot = epi == EPI_RXPOOL ? "bconv_pool" : epi == EPI_RXHEAD ? "bconv_head" : "bconv";
@@ -576,6 +605,29 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
         return rc;
     }
   }
+  return BNN_OK;
+  };
+  // A large batch runs as two halves on two streams: the many short
+  // kernels of one half fill the launch, ramp and drain gaps of the
+  // other's.  A scene splits at whole patch rows; one stream with
+  // per-kernel events or debug dumps.
+  const int unit = sc ? sc->pcols : 1;
+  const bool split = !dump && !evs && N >= 256 && N / unit >= 2;
+  if (!split) return part();
+  if (!D->side) {
+    HIP_TRY(hipStreamCreateWithFlags(&D->side, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&D->ev_fork, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&D->ev_join, hipEventDisableTiming));
+  }
+  HIP_TRY(hipEventRecord(D->ev_fork, s));
+  HIP_TRY(hipStreamWaitEvent(D->side, D->ev_fork, 0));
+  const int half = (N / unit) / 2 * unit;
+  nb = 0; cnt = half; st = s;
+  if ((rc = part())) return rc;
+  nb = half; cnt = N - half; st = D->side;
+  if ((rc = part())) return rc;
+  HIP_TRY(hipEventRecord(D->ev_join, D->side));
+  HIP_TRY(hipStreamWaitEvent(s, D->ev_join, 0));
   return BNN_OK;
 }
 

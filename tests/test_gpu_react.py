@@ -111,7 +111,7 @@ def test_react_batch_1024(tmp_path, rorc):
     x = synth.make_input(11, N, 120, 32, 32)
     x[777] = x[3]
     got = eng.forward_batch(x)
-    idx = [0, 1, 3, 63, 64, 255, 500, 777, 1022, 1023]
+    idx = [0, 1, 3, 63, 64, 255, 500, 511, 512, 777, 1022, 1023]  # both halves of the two-stream split
     want = model.forward_batch(np.ascontiguousarray(x[idx]))
     for i, n in enumerate(idx):
         assert _same(got[n], want[i]), n
@@ -304,3 +304,27 @@ def test_react_kernel_abi(rorc, orc):
         o16 = np.zeros((cout, H, W), np.int16)
         L.bconv_blk_b4p4_i16(p(a, i8), p(pk, u64), p(o16, i16), cin, H, W, cout, 3, 3, 1, 1)
         assert np.array_equal(o16.astype(np.int32), want)
+
+
+def test_react_split_batch_and_scene(tmp_path, rorc):
+    """Batches of 256+ patches and scenes of 256+ patches run as two parts on
+    two streams (the scene at whole patch rows, the planes keeping the whole
+    batch's stride): an odd batch equals its patches run in small batches,
+    and a 289-patch scene equals the checker's patch-wise forward."""
+    import torch
+    b = synth.make_blob_react(seed=16, base=8)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(17, 301, 120, 16, 16)
+    small = np.concatenate([eng.forward_batch(x[i:i + 50]) for i in range(0, 301, 50)])
+    assert _same(eng.forward_batch(x), small)
+    model = rorc.parse(R.to_bytes(b))
+    rng = np.random.default_rng(18)
+    cube = rng.standard_normal((120, 272, 270)).astype(np.float32)
+    want = model.forward_patched(cube, 16)
+    d_cube = torch.from_numpy(cube).cuda()
+    d_map = torch.full((3, 272, 270), float("nan"), device="cuda")
+    s = torch.cuda.Stream()
+    eng.forward_patched_device(d_cube.data_ptr(), 272, 270, d_map.data_ptr(), 16, s.cuda_stream)
+    torch.cuda.synchronize()
+    assert _same(d_map.cpu().numpy(), want)
+    eng.close()
