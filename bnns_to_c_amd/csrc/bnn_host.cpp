@@ -728,7 +728,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       HIP_TRY(launch_bconv_mfma(a, L.mc, epi, dump, st));
     } else {
       int mt, cog;
-      pick_shape(epi, cnt, a.H, a.W, L.cout, &mt, &cog);
+      // the shape the whole batch would take: the parts run side by side,
+      // so each part's kernel needs only its share of the waves
+      pick_shape(epi, N, a.H, a.W, L.cout, &mt, &cog);
       HIP_TRY(launch_bconv(a, epi, mt, cog, dump, st));
     }
     const char* ot = epi == EPI_POOL ? (mm ? "bconv_pool_mfma" : "bconv_pool")
