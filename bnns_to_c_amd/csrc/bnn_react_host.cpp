@@ -555,7 +555,7 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
       if (epi == EPI_RXPOOL) a.P2 = dmp->P2[k];
     }
     int mt, cog;
-    pick_shape(epi, cnt, a.H, a.W, a.cout, &mt, &cog);
+    pick_shape(epi, N, a.H, a.W, a.cout, &mt, &cog);  // the whole batch's shape (parts run side by side)
     HIP_TRY(launch_bconv(a, epi, mt, cog, dump, st));
     static char lab[9][2][16];
     snprintf(lab[k][u - 1], sizeof lab[k][u - 1], "%s.c%d", kName[k], u);
