@@ -788,11 +788,23 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   if (sc && N / unit < parts) parts = 1;
   if (parts == 1) return part();
   if (!D->ev_fork) {
-    HIP_TRY(hipEventCreateWithFlags(&D->ev_fork, hipEventDisableTiming));
-    for (int k = 0; k < kSplitMax - 1; ++k) {
-      HIP_TRY(hipStreamCreateWithFlags(&D->side[k], hipStreamNonBlocking));
-      HIP_TRY(hipEventCreateWithFlags(&D->ev_join[k], hipEventDisableTiming));
+    // all or nothing: a failure leaves no half-made set behind
+    hipStream_t side[kSplitMax - 1] = {};
+    hipEvent_t fork = nullptr, join[kSplitMax - 1] = {};
+    bool ok = hipEventCreateWithFlags(&fork, hipEventDisableTiming) == hipSuccess;
+    for (int k = 0; ok && k < kSplitMax - 1; ++k)
+      ok = hipStreamCreateWithFlags(&side[k], hipStreamNonBlocking) == hipSuccess &&
+           hipEventCreateWithFlags(&join[k], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      if (fork) (void)hipEventDestroy(fork);
+      for (int k = 0; k < kSplitMax - 1; ++k) {
+        if (join[k]) (void)hipEventDestroy(join[k]);
+        if (side[k]) (void)hipStreamDestroy(side[k]);
+      }
+      return set_err(BNN_EHIP, "cannot create the streams of a split batch");
     }
+    D->ev_fork = fork;
+    for (int k = 0; k < kSplitMax - 1; ++k) { D->side[k] = side[k]; D->ev_join[k] = join[k]; }
   }
   HIP_TRY(hipEventRecord(D->ev_fork, s));
   for (int k = 1; k < parts; ++k) HIP_TRY(hipStreamWaitEvent(D->side[k - 1], D->ev_fork, 0));

@@ -615,9 +615,18 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
   const bool split = !dump && !evs && N >= 256 && N / unit >= 2;
   if (!split) return part();
   if (!D->side) {
-    HIP_TRY(hipStreamCreateWithFlags(&D->side, hipStreamNonBlocking));
-    HIP_TRY(hipEventCreateWithFlags(&D->ev_fork, hipEventDisableTiming));
-    HIP_TRY(hipEventCreateWithFlags(&D->ev_join, hipEventDisableTiming));
+    // all or nothing: a failure leaves no half-made set behind
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (hipStreamCreateWithFlags(&side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) {
+      if (join) (void)hipEventDestroy(join);
+      if (fork) (void)hipEventDestroy(fork);
+      if (side) (void)hipStreamDestroy(side);
+      return set_err(BNN_EHIP, "cannot create the stream of a split batch");
+    }
+    D->side = side; D->ev_fork = fork; D->ev_join = join;
   }
   HIP_TRY(hipEventRecord(D->ev_fork, s));
   HIP_TRY(hipStreamWaitEvent(D->side, D->ev_fork, 0));
