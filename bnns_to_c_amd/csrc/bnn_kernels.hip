@@ -286,6 +286,12 @@ __device__ __forceinline__ void mfma_chain(f32x16& acc, const float (&wa)[3], co
 #ifndef BNN_MWPE
 #define BNN_MWPE 2
 #endif
+#ifndef BNN_MWPE_RX
+#define BNN_MWPE_RX 3
+#endif
+#ifndef BNN_MLC_RX
+#define BNN_MLC_RX 48
+#endif
 // an offset past any input of the matrix-core real conv (inputs are smaller)
 constexpr uint32_t kRealFar = 0x7FFFFFF0u;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -300,17 +306,26 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // bnn_react_ops.c:75-85).  The projection weights of a chunk ride along
 // with its input rows: one more LDS-writing load per wave.
 template <int WR, int WC, bool PARTIAL, bool RX>
-__global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(BNN_MWPE)))
+__global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(RX ? BNN_MWPE_RX : BNN_MWPE)))
 void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   constexpr int TR = 4 * WR, TC = 16 * WC, NW = WR * WC;
   constexpr int CI = kRealMfmaCI;  // input channels per LDS chunk
   // A chunk is CI x LR rows of the input tile (LW = TC + 2 columns with the
   // halo).  Each row is filled by one buffer load that writes LDS (lane l
-  // lands at the load's LDS base + 4*l, so a row takes 64 slots); rows are
-  // LC = 80 floats apart, 16 (mod 32), so the four 16-lane rows of a wave's
-  // B read fall in disjoint banks.
-  constexpr int LR = TR + 2, LW = TC + 2, LC = 80, LPL = LR * LC;
+  // lands at the load's LDS base + 4*l).  Rows are LC floats apart, an odd
+  // multiple of 16, so the four 16-lane rows of a wave's B read fall in four
+  // disjoint 16-bank groups of 64 banks (and in two of 32).  LC = 80 lets a
+  // row take all 64 slots.  The RX unit has the registers for three waves
+  // per SIMD but three buffers of 80-float rows leave LDS for two blocks per
+  // CU: there LC = 48 and only the LW lanes of a row issue its load (the
+  // rest are switched off and write nothing), which fits three.  The arrays
+  // carry 64 - LC floats of tail so that a full-width row write would still
+  // stay inside them.
+  constexpr int LR = TR + 2, LW = TC + 2, LC = RX ? BNN_MLC_RX : 80, LPL = LR * LC;
+  constexpr bool kRowMask = LC < 64;
+  constexpr int LTAIL = kRowMask ? 64 - LC : 0;
   static_assert(LW <= 64, "a tile row must fit one 64-lane load");
+  static_assert(LW <= LC && LC % 16 == 0 && (LC / 16) % 2 == 1, "rows hold LW floats in odd 16-bank groups");
   constexpr int NROW = CI * LR;             // row loads per chunk
   constexpr int KR = NROW / NW;  // row loads per wave
   static_assert(NROW % NW == 0, "every wave issues the same number of row loads");
@@ -318,7 +333,7 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   constexpr int KL = KR + (RX ? 1 : 0);  // LDS-writing loads per wave and chunk
   // Three buffers: chunk ch is read from one while ch+1 has landed in the
   // next and ch+2 is in flight into the third.
-  __shared__ float tile0[CI * LPL], tile1[CI * LPL], tile2[CI * LPL];  // [ci][row][col]
+  __shared__ float tile0[CI * LPL + LTAIL], tile1[CI * LPL + LTAIL], tile2[CI * LPL + LTAIL];  // [ci][row][col]
   constexpr int WL = RX ? 4 * 64 : 1;  // projection rows of a chunk (RX)
   __shared__ float wl0[WL], wl1[WL], wl2[WL];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -385,24 +400,29 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
     int cw0 = wv * (KR / LR);
     asm volatile("" : "+s"(cw0));
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_f32)(bufp(bc)) + (uint32_t)(cw0 * LPL * 4);
+    auto rows = [&] {
 #pragma unroll
-    for (int j = 0; j < KR / LR; ++j) {
-      const int cin_j = ch * CI + cw0 + j;  // input channel of these rows
-      const bool chan_ok = !PARTIAL || cin_j < a.cin;
-      const uint32_t cbase = (uint32_t)cin_j * cs4 + (uint32_t)(y0 - 1) * rs4;
+      for (int j = 0; j < KR / LR; ++j) {
+        const int cin_j = ch * CI + cw0 + j;  // input channel of these rows
+        const bool chan_ok = !PARTIAL || cin_j < a.cin;
+        const uint32_t cbase = (uint32_t)cin_j * cs4 + (uint32_t)(y0 - 1) * rs4;
 #pragma unroll
-      for (int r = 0; r < LR; ++r) {
-        const bool ok = chan_ok && r >= rlo && r < rhi;
-        const uint32_t soff = ok ? cbase + (uint32_t)r * rs4 : kRealFar;
-        const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + (uint32_t)((j * LPL + r * LC) * 4)));
-        const uint32_t vl = vo_lane;
-        const u32x4 rd = rsrc;
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-                     :
-                     : "s"(m0v), "v"(vl), "s"(rd), "s"(soff)
-                     : "memory");
+        for (int r = 0; r < LR; ++r) {
+          const bool ok = chan_ok && r >= rlo && r < rhi;
+          const uint32_t soff = ok ? cbase + (uint32_t)r * rs4 : kRealFar;
+          const uint32_t m0v =
+              (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + (uint32_t)((j * LPL + r * LC) * 4)));
+          const uint32_t vl = vo_lane;
+          const u32x4 rd = rsrc;
+          asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                       :
+                       : "s"(m0v), "v"(vl), "s"(rd), "s"(soff)
+                       : "memory");
+        }
       }
-    }
+    };
+    // one lane-masked region for all of the wave's row loads
+    if (!kRowMask || lane < LW) rows();
     if constexpr (RX) {
       // this wave's projection row of the chunk (lane l -> slot 64*wv + l)
       const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane(
