@@ -292,6 +292,9 @@ __device__ __forceinline__ void mfma_chain(f32x16& acc, const float (&wa)[3], co
 #ifndef BNN_MLC_RX
 #define BNN_MLC_RX 48
 #endif
+#ifndef BNN_MLC
+#define BNN_MLC 80
+#endif
 // an offset past any input of the matrix-core real conv (inputs are smaller)
 constexpr uint32_t kRealFar = 0x7FFFFFF0u;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -321,7 +324,7 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
   // rest are switched off and write nothing), which fits three.  The arrays
   // carry 64 - LC floats of tail so that a full-width row write would still
   // stay inside them.
-  constexpr int LR = TR + 2, LW = TC + 2, LC = RX ? BNN_MLC_RX : 80, LPL = LR * LC;
+  constexpr int LR = TR + 2, LW = TC + 2, LC = RX ? BNN_MLC_RX : BNN_MLC, LPL = LR * LC;
   constexpr bool kRowMask = LC < 64;
   constexpr int LTAIL = kRowMask ? 64 - LC : 0;
   static_assert(LW <= 64, "a tile row must fit one 64-lane load");
