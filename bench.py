@@ -170,8 +170,7 @@ def main() -> int:
     x = torch.from_numpy(synth.make_input(1, N)).cuda()
     y = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
     # every engine enqueues on this stream and the timing events are recorded
-    # on it (a handle of 0, torch's default stream, would make the engines
-    # use their own streams, which the events would not order)
+    # on it
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     sp = stream.cuda_stream

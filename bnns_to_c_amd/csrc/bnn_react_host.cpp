@@ -818,7 +818,8 @@ void bnn_forward_react(const ModelR* m, const float* input, int H, int W, float*
 int bnn_react_forward_device(const ModelR* m, const float* d_input, int N, int H, int W, float* d_logits,
                              void* stream) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
-  return run_device(m, d_input, N, H, W, d_logits, stream ? (hipStream_t)stream : m->dev->stream, nullptr);
+  // NULL is the HIP default stream, as for every stream argument in HIP
+  return run_device(m, d_input, N, H, W, d_logits, (hipStream_t)stream, nullptr);
 }
 
 void* bnn_react_stream(const ModelR* m) { return (m && m->dev) ? (void*)m->dev->stream : nullptr; }
@@ -844,7 +845,7 @@ void bnn_forward_react_patched_file(const ModelR* m, FILE* f, int H, int W, floa
 int bnn_react_forward_patched_device(const ModelR* m, const float* d_input, int H, int W, float* d_logits, int P,
                                      void* stream) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
-  return run_patched_device(m, d_input, H, W, d_logits, P, stream ? (hipStream_t)stream : m->dev->stream);
+  return run_patched_device(m, d_input, H, W, d_logits, P, (hipStream_t)stream);
 }
 
 int bnn_react_forward_debug(const ModelR* m, const float* input, int N, int H, int W, float* logits,

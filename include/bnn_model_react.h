@@ -120,10 +120,11 @@ int bnn_react_blob_check(const char *path);
 int bnn_react_load_status(const char *path, ModelR **out);
 /* N patches [N][n_bands][H][W] -> logits [N][n_classes][H][W], host pointers */
 int bnn_react_forward_batch(const ModelR *m, const float *input, int N, int H, int W, float *logits);
-/* the same on device pointers, enqueued on stream (NULL: the model's own) */
+/* the same on device pointers, enqueued on stream (a hipStream_t; NULL = the
+ * HIP default stream, as everywhere in HIP); returns once enqueued */
 int bnn_react_forward_device(const ModelR *m, const float *d_input, int N, int H, int W,
                              float *d_logits, void *stream);
-void *bnn_react_stream(const ModelR *m);
+void *bnn_react_stream(const ModelR *m); /* the model's own hipStream_t (used by the host-pointer calls) */
 int bnn_react_forward_patched(const ModelR *m, const float *input, int H, int W, float *logits, int P);
 int bnn_react_forward_patched_device(const ModelR *m, const float *d_input, int H, int W, float *d_logits,
                                      int P, void *stream);

@@ -228,3 +228,21 @@ def test_cfg4_large_tile_vs_checker(tmp_path, orc, monkeypatch):
     for n in (1, 2):
         assert _same(batch[n], eng.forward_batch(x[n:n + 1])[0]), n
     eng.close()
+
+
+def test_default_stream_is_ordered(tmp_path):
+    """stream = NULL is the HIP default stream: the host copy the caller
+    enqueues there next (it waits for that stream only) sees the finished
+    logits of a split batch."""
+    import torch
+    eng, _ = _engine(tmp_path, synth.make_blob(seed=9))
+    N = 512
+    x = synth.make_input(10, N)
+    want = eng.forward_batch(x)
+    with torch.cuda.stream(torch.cuda.default_stream()):
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.full((N, 3, 32, 32), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_device(dx.data_ptr(), N, 32, 32, dy.data_ptr(), None)
+        assert _same(dy.cpu().numpy(), want)
+    eng.close()

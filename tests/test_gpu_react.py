@@ -328,3 +328,32 @@ def test_react_split_batch_and_scene(tmp_path, rorc):
     torch.cuda.synchronize()
     assert _same(d_map.cpu().numpy(), want)
     eng.close()
+
+
+def test_react_default_stream_is_ordered(tmp_path):
+    """stream = NULL is the HIP default stream, as for the v1 entry points:
+    work the caller enqueues on the default stream after the call (here the
+    copy to the host, which waits for that stream only) sees the finished
+    logits, for a split batch and for a scene."""
+    import torch
+    b = synth.make_blob_react(seed=19, base=8)
+    eng, _ = _engine(tmp_path, b)
+    N = 512
+    x = synth.make_input(20, N, 120, 16, 16)
+    want = eng.forward_batch(x)
+    with torch.cuda.stream(torch.cuda.default_stream()):
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.full((N, 3, 16, 16), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_device(dx.data_ptr(), N, 16, 16, dy.data_ptr(), None)
+        got = dy.cpu().numpy()
+        assert _same(got, want)
+        rng = np.random.default_rng(21)
+        cube = rng.standard_normal((120, 272, 270)).astype(np.float32)
+        want_map = eng.forward_patched(cube, 16)
+        d_cube = torch.from_numpy(cube).cuda()
+        d_map = torch.full((3, 272, 270), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_patched_device(d_cube.data_ptr(), 272, 270, d_map.data_ptr(), 16, None)
+        assert _same(d_map.cpu().numpy(), want_map)
+    eng.close()
