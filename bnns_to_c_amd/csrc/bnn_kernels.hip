@@ -1026,6 +1026,41 @@ __device__ __forceinline__ void store_bits(uint32_t* base, size_t pix, int cw, i
   for (int b = (co0 + COG) >> 3; b < zero_end; ++b) row[b] = 0;
 }
 
+// The 1x1 head of one pixel: per class the bias, then the channels in
+// order, one fused step each (csrc/bnn_head.c:21-34,
+// csrc/bnn_react_opt.c:33-41).  The weights come through the constant
+// address space (scalar loads that the logits stores cannot invalidate).
+// When the group holds exactly cout channels the weights of a class are
+// fetched as one batch, one wait per class instead of one per weight; the
+// guarded loop serves a smaller cout.
+template <int COG>
+__device__ __forceinline__ void head_logits(const float* hw_, const float* hb_, int ncls, int cout,
+                                            const float (&v)[COG], float* logits, size_t lbase, size_t lstride) {
+  typedef const __attribute__((address_space(4))) float* const_hf;
+  const const_hf hw = (const_hf)hw_, hb = (const_hf)hb_;
+  if (cout == COG) {
+#pragma unroll 1
+    for (int o = 0; o < ncls; ++o) {
+      float w[COG];
+#pragma unroll
+      for (int j = 0; j < COG; ++j) w[j] = hw[o * COG + j];
+      float accf = hb[o];
+#pragma unroll
+      for (int j = 0; j < COG; ++j) accf = __fmaf_rn(w[j], v[j], accf);
+      logits[lbase + (size_t)o * lstride] = accf;
+    }
+    return;
+  }
+#pragma unroll 1
+  for (int o = 0; o < ncls; ++o) {
+    float accf = hb[o];
+#pragma unroll
+    for (int j = 0; j < COG; ++j)
+      if (j < cout) accf = __fmaf_rn(hw[o * cout + j], v[j], accf);
+    logits[lbase + (size_t)o * lstride] = accf;
+  }
+}
+
 template <int MT, int COG, int EPI, bool DUMP>
 __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t bytes0, uint32_t bytes1) {
   constexpr int NP = MT + 2;
@@ -1292,15 +1327,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
         lbase = (size_t)sy * a.sW + sx;
         lstride = (size_t)a.sH * a.sW;
       }
-      const const_f32 hw = (const_f32)a.hw, hb = (const_f32)a.hb;
-#pragma unroll 1
-      for (int o = 0; o < a.ncls; ++o) {
-        float accf = hb[o];
-#pragma unroll
-        for (int j = 0; j < COG; ++j)
-          if (j < a.cout) accf = __fmaf_rn(hw[o * a.cout + j], hr[0][j], accf);
-        a.logits[lbase + (size_t)o * lstride] = accf;
-      }
+      head_logits<COG>(a.hw, a.hb, a.ncls, a.cout, hr[0], a.logits, lbase, lstride);
     }
     return;
   }
@@ -1384,18 +1411,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       lstride = (size_t)a.sH * a.sW;
     }
     if (!keep) return;
-    // the head through the constant address space: scalar loads that the
-    // logits stores cannot invalidate
-    typedef const __attribute__((address_space(4))) float* const_hf;
-    const const_hf hw = (const_hf)a.hw, hb = (const_hf)a.hb;
-#pragma unroll 1
-    for (int o = 0; o < a.ncls; ++o) {
-      float accf = hb[o];
-#pragma unroll
-      for (int j = 0; j < COG; ++j)
-        if (j < a.cout) accf = __fmaf_rn(hw[o * a.cout + j], sg[j], accf);
-      a.logits[lbase + (size_t)o * lstride] = accf;
-    }
+    head_logits<COG>(a.hw, a.hb, a.ncls, a.cout, sg, a.logits, lbase, lstride);
   }
 }
 
