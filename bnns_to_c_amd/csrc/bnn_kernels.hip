@@ -1205,6 +1205,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       const float t = __fadd_rn(__fmaf_rn(A, (float)P, Bm), res);
       return t >= 0.0f ? t : __fmul_rn(w, t);
     };
+    constexpr int JP = COG < 8 ? COG : 8;  // channels per parameter batch
     float hr[MT * MT][COG];  // the shortcut at each pixel (EPI_RXPOOL pools it)
     uint32_t bits[MT * MT];
 #pragma unroll
@@ -1249,27 +1250,42 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       uint32_t voff[MT];
 #pragma unroll
       for (int px = 0; px < MT; ++px) voff[px] = inimg[py * MT + px] ? (uint32_t)(row + px) * 4u : 0x80000000u;
+      // the parameters of JP channels in one batch of scalar loads (next to
+      // their uses, after the stores of the previous channel, each would be
+      // waited for alone); the tap rsign index stays below cout
 #pragma unroll
-      for (int j = 0; j < COG; ++j) {
-        float h[MT];
+      for (int j0 = 0; j0 < COG; j0 += JP) {
+        float pA[JP], pB[JP], pW[JP], pT[JP];
 #pragma unroll
-        for (int px = 0; px < MT; ++px) {
-          const int p = py * MT + px;
-          h[px] = rx(Pof(p, j), eA[j], eB[j], eW[j], hr[p][j]);
-          if (trs && co0 + j < a.cout && __fadd_rn(h[px], trs[j]) > 0.0f) bits[p] |= 1u << j;
-          if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h[px];
+        for (int jj = 0; jj < JP; ++jj) {
+          pA[jj] = eA[j0 + jj];
+          pB[jj] = eB[j0 + jj];
+          pW[jj] = eW[j0 + jj];
+          pT[jj] = trs ? trs[min(co0 + j0 + jj, a.cout - 1) - co0] : 0.0f;
         }
-        if (a.hout) {
-          const __amdgpu_buffer_rsrc_t hd = plane_rsrc(a.hout, j, plane);
-          if constexpr (MT == 2) {
-            if (pairs) {
-              raw_store_f32x2(stem_f32x2{h[0], h[1]}, hd, (int)voff[0], 0, 0);
-              continue;
-            }
-          }
 #pragma unroll
-          for (int px = 0; px < MT; ++px)
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h[px]), hd, (int)voff[px], 0, 0);
+        for (int jj = 0; jj < JP; ++jj) {
+          const int j = j0 + jj;
+          float h[MT];
+#pragma unroll
+          for (int px = 0; px < MT; ++px) {
+            const int p = py * MT + px;
+            h[px] = rx(Pof(p, j), pA[jj], pB[jj], pW[jj], hr[p][j]);
+            if (trs && co0 + j < a.cout && __fadd_rn(h[px], pT[jj]) > 0.0f) bits[p] |= 1u << j;
+            if constexpr (EPI == EPI_RXHEAD) hr[p][j] = h[px];
+          }
+          if (a.hout) {
+            const __amdgpu_buffer_rsrc_t hd = plane_rsrc(a.hout, j, plane);
+            if constexpr (MT == 2) {
+              if (pairs) {
+                raw_store_f32x2(stem_f32x2{h[0], h[1]}, hd, (int)voff[0], 0, 0);
+                continue;
+              }
+            }
+#pragma unroll
+            for (int px = 0; px < MT; ++px)
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h[px]), hd, (int)voff[px], 0, 0);
+          }
         }
       }
 #pragma unroll
@@ -1298,20 +1314,34 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
       const const_f32 drs = a.drs ? (const_f32)a.drs + co0 : nullptr;
       uint32_t b2 = 0;
 #pragma unroll
-      for (int j = 0; j < COG; ++j) {
-        if (co0 + j >= a.cout) continue;
-        int32_t pm = Pof(0, j);
-        float hm = hr[0][j];
+      for (int j0 = 0; j0 < COG; j0 += JP) {
+        // one batch of scalar loads per JP channels, indices kept below cout
+        float qA[JP], qB[JP], qW[JP], qT[JP];
 #pragma unroll
-        for (int p = 1; p < 4; ++p) {
-          pm = max(pm, Pof(p, j));
-          if (hr[p][j] > hm) hm = hr[p][j];
+        for (int jj = 0; jj < JP; ++jj) {
+          const int c = min(co0 + j0 + jj, a.cout - 1);
+          qA[jj] = ((const_f32)a.dA)[c];
+          qB[jj] = ((const_f32)a.dB)[c];
+          qW[jj] = ((const_f32)a.dW)[c];
+          qT[jj] = drs ? drs[c - co0] : 0.0f;
         }
-        if (DUMP) a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
-        const float d = rx(pm, ((const_f32)a.dA)[co0 + j], ((const_f32)a.dB)[co0 + j], ((const_f32)a.dW)[co0 + j], hm);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, d), plane_rsrc(a.dout, j, hplane),
-                                              (int)((uint32_t)dp * 4u), 0, 0);
-        if (drs && __fadd_rn(d, drs[j]) > 0.0f) b2 |= 1u << j;
+#pragma unroll
+        for (int jj = 0; jj < JP; ++jj) {
+          const int j = j0 + jj;
+          if (co0 + j >= a.cout) continue;
+          int32_t pm = Pof(0, j);
+          float hm = hr[0][j];
+#pragma unroll
+          for (int p = 1; p < 4; ++p) {
+            pm = max(pm, Pof(p, j));
+            if (hr[p][j] > hm) hm = hr[p][j];
+          }
+          if (DUMP) a.P2[((size_t)n * a.cout + co0 + j) * Hh * Wh + ty * Wh + tx] = pm;
+          const float d = rx(pm, qA[jj], qB[jj], qW[jj], hm);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, d), plane_rsrc(a.dout, j, hplane),
+                                                (int)((uint32_t)dp * 4u), 0, 0);
+          if (drs && __fadd_rn(d, qT[jj]) > 0.0f) b2 |= 1u << j;
+        }
       }
       if (drs && a.out2) store_bits<COG>(a.out2, dp, a.cwo, co0, a.cout, b2, zero_end);
     }
