@@ -898,7 +898,7 @@ struct Acc {
 // one batch of scalar loads before their products: fetched channel by
 // channel, each would wait for its own load.
 #ifndef BNN_BJB
-#define BNN_BJB 4
+#define BNN_BJB 8
 #endif
 template <int MT, int COG>
 __device__ __forceinline__ void accumulate(Acc<MT, COG>& D, const uint32_t (&av)[MT + 2][MT + 2],
