@@ -386,6 +386,7 @@ hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& mc, int epi, bo
   if ((epi != EPI_FOLD && epi != EPI_POOL) || !mc.w || !mc.s || a.cout % 64 || !mfma_tile(a.H, a.W, epi, &T))
     return hipErrorInvalidValue;
   if (a.in1 && a.padoff != 0x80000000u) return hipErrorInvalidValue;  // v1 concat semantics only
+  if (dump && (!a.P || (epi == EPI_POOL && !a.P2))) return hipErrorInvalidValue;  // dumps need their targets
   const size_t npix = (size_t)a.N * a.H * a.W;
   if (npix * a.cw0 * 4 >= 0x80000000ull) return hipErrorInvalidValue;
   if (a.in1 && (size_t)a.N * a.h1 * a.w1 * a.cw1 * 4 >= 0x80000000ull) return hipErrorInvalidValue;

@@ -1093,9 +1093,14 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
   Dumps d;
   d.on = true;
   std::vector<void*> tmp;
+  bool oom = false;  // any failed allocation: no dump kernel may run with a null target
   auto alloc = [&](size_t bytes) -> void* {
     void* p = nullptr;
-    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) return nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) {
+      (void)hipGetLastError();
+      oom = true;
+      return nullptr;
+    }
     tmp.push_back(p);
     return p;
   };
@@ -1104,8 +1109,7 @@ int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, f
   for (size_t i = 0; i < pinfo.size(); ++i)
     d.P[i] = (int32_t*)alloc((size_t)N * pinfo[i].c * hs[pinfo[i].lvl] * ws[pinfo[i].lvl] * 4);
   for (int i = 0; i < 4; ++i) d.P2[i] = (int32_t*)alloc((size_t)N * m->enc_conv2[i].Cout * hs[i + 1] * ws[i + 1] * 4);
-  for (void* p : tmp)
-    if (!p) { cleanup(); return set_err(BNN_EHIP, "hipMalloc failed for debug dumps"); }
+  if (oom) { cleanup(); return set_err(BNN_EHIP, "hipMalloc failed for debug dumps (N=%d)", N); }
   if ((rc = run_host(m, input, N, H, W, logits, &d))) { cleanup(); return rc; }
   if (cb) {
     const Workspace& w = D->ws;

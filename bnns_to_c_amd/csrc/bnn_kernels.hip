@@ -1869,6 +1869,9 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
   if (a.in1 && a.padoff != 0x80000000u && a.padoff != (uint32_t)((size_t)nrel * a.h1 * a.w1 * a.cw1 * 4))
     return hipErrorInvalidValue;
   if (a.pair && a.cw0 != 1) return hipErrorInvalidValue;  // a first segment of one half-filled word
+  // a dump launch stores every P (and every pooled P) it computes: no null target
+  if ((dump || epi == EPI_P) && !a.P) return hipErrorInvalidValue;
+  if (dump && (epi == EPI_POOL || epi == EPI_RXPOOL) && !a.P2) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_FOLD:
       if (mt == 1) return dump ? go_bconv_cog<1, EPI_FOLD, true>(a, cog, s) : go_bconv_cog<1, EPI_FOLD, false>(a, cog, s);

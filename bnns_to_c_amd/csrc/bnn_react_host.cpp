@@ -858,9 +858,14 @@ int bnn_react_forward_debug(const ModelR* m, const float* input, int N, int H, i
   level_dims(H, W, hs, wsz);
   // P dumps: conv1 (not enc1) and conv2 of every block, in launch order
   std::vector<void*> bufs;
+  bool oom = false;  // any failed allocation: no dump kernel may run with a null target
   auto alloc = [&](size_t bytes) -> void* {
     void* p = nullptr;
-    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) return nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) {
+      (void)hipGetLastError();
+      oom = true;
+      return nullptr;
+    }
     bufs.push_back(p);
     return p;
   };
@@ -879,11 +884,10 @@ int bnn_react_forward_debug(const ModelR* m, const float* input, int N, int H, i
   }
   for (size_t i = 0; i < pinfo.size(); ++i)
     dm.P[i] = (int32_t*)alloc((size_t)N * pinfo[i].c * hs[pinfo[i].lvl] * wsz[pinfo[i].lvl] * 4);
-  for (void* p : bufs)
-    if (!p) {
-      for (void* q : bufs) (void)hipFree(q);
-      return set_err(BNN_EHIP, "out of device memory for the debug dumps");
-    }
+  if (oom) {
+    for (void* q : bufs) (void)hipFree(q);
+    return set_err(BNN_EHIP, "out of device memory for the debug dumps (N=%d)", N);
+  }
   rc = run_host(m, input, N, H, W, logits, &dm);
   if (!rc && cb) {
     RWorkspace& w = D->ws;
