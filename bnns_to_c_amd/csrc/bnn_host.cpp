@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -414,6 +415,10 @@ struct BnnDevice {
   // the later parts of a large batch run their binary layers on these streams
   hipStream_t side[kSplitMax - 1] = {};
   hipEvent_t ev_fork = nullptr, ev_join[kSplitMax - 1] = {};
+  // this device's copy of `scratch` (bnn_forward_device_noalloc), null if
+  // its address could not be looked up (scratch_err says why)
+  uint8_t* scratch = nullptr;
+  std::string scratch_err;
 };
 
 struct BnnConvLayer {
@@ -532,6 +537,33 @@ void release(BnnDevice* D) {
   D->stream = nullptr;
 }
 
+// ------------------------------------------------- allocation-free forward
+// bnn_forward_device_noalloc keeps its inter-layer tensors in this array, of
+// which every GPU holds its own copy from the library's load until the
+// process ends.  In host code `scratch` names a host-side stand-in, not
+// device memory: each device's address comes from hipGetSymbolAddress, looked
+// up once per device (with that device current) when the first model is
+// loaded there, and only that address is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[BNN_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::vector<uint8_t*> g_scratch_dev;  // by device ordinal; null until looked up
+
+int scratch_lookup(int dev, uint8_t** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (dev < 0) return set_err(BNN_EHIP, "bad device ordinal %d", dev);
+  if ((int)g_scratch_dev.size() <= dev) g_scratch_dev.resize(dev + 1, nullptr);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_err(BNN_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_dev[dev] = (uint8_t*)p;
+  }
+  *out = g_scratch_dev[dev];
+  return BNN_OK;
+}
+
 int build_device(Model* m, const StemPart* st = nullptr) {
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
@@ -541,6 +573,11 @@ int build_device(Model* m, const StemPart* st = nullptr) {
   HIP_TRY(hipGetDevice(&D->device));
   HIP_TRY(hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking));
   int rc;
+  // a failed lookup only disables the allocation-free entry point
+  if (scratch_lookup(D->device, &D->scratch)) {
+    D->scratch = nullptr;
+    D->scratch_err = g_err;
+  }
   D->stem = st != nullptr;
   if ((rc = st ? upload_real(D, st->c, st->a) : upload_real(D, m->enc_conv1[0], m->enc_act1[0]))) return rc;
   if ((rc = upload_bconv(D, &D->e2[0], m->enc_conv2[0], 0, &m->enc_act2_skip[0], &m->enc_act2_down[0]))) return rc;
@@ -570,14 +607,17 @@ void level_dims(int H, int W, int* hs, int* wsz) {
   for (int l = 1; l <= 4; ++l) { hs[l] = hs[l - 1] / 2; wsz[l] = wsz[l - 1] / 2; }
 }
 
-int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
-  if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
-  // a forward may still be in flight on a caller's stream
-  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; }
+// Lay the inter-layer tensors of an N x H x W forward out from `base` (each
+// on a 256-byte boundary) and return the bytes they take; with base null only
+// the size is computed.
+size_t plan_ws(const Model* m, const BnnDevice* D, Workspace& w, int N, int H, int W, uint8_t* base) {
   int hs[5], ws[5];
   level_dims(H, W, hs, ws);
-  std::vector<std::pair<uint32_t**, size_t>> plan;
-  auto add = [&](uint32_t** p, int lvl, int c) { plan.push_back({p, (size_t)N * hs[lvl] * ws[lvl] * words(c)}); };
+  size_t off = 0;
+  auto add = [&](uint32_t** p, int lvl, int c) {
+    if (base) *p = (uint32_t*)(base + off);
+    off += ((size_t)N * hs[lvl] * ws[lvl] * words(c) * 4 + 255) & ~(size_t)255;
+  };
   add(&w.a1, 0, D->rcout);  // first-stage bits
   for (int i = 0; i < 4; ++i) {
     if (i || D->stem) add(&w.h[i], i, m->enc_conv1[i].Cout);
@@ -590,15 +630,17 @@ int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
     add(&w.d1[i], 3 - i, m->dec_conv1[i].Cout);
     add(&w.d2[i], 3 - i, m->dec_conv2[i].Cout);
   }
-  size_t total = 0;
-  for (auto& e : plan) total += (e.second * 4 + 255) & ~(size_t)255;
-  HIP_TRY(hipMalloc((void**)&w.base, total));
-  size_t off = 0;
-  for (auto& e : plan) {
-    *e.first = (uint32_t*)(w.base + off);
-    off += (e.second * 4 + 255) & ~(size_t)255;
-  }
-  w.N = N; w.H = H; w.W = W;
+  if (base) { w.base = base; w.N = N; w.H = H; w.W = W; }
+  return off;
+}
+
+int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
+  if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
+  // a forward may still be in flight on a caller's stream
+  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; }
+  uint8_t* base = nullptr;
+  HIP_TRY(hipMalloc((void**)&base, plan_ws(m, D, w, N, H, W, nullptr)));
+  plan_ws(m, D, w, N, H, W, base);
   return BNN_OK;
 }
 
@@ -647,7 +689,7 @@ struct Op {
 // kernel.
 int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_in, int N, int H, int W,
                     float* d_logits, hipStream_t s, Dumps* dmp, std::vector<Op>* ops,
-                    std::vector<hipEvent_t>* evs, const Scene* sc = nullptr) {
+                    std::vector<hipEvent_t>* evs, const Scene* sc = nullptr, int max_parts = kSplitMax) {
   int hs[5], wsz[5];
   level_dims(H, W, hs, wsz);
   auto mark = [&](const char* label, const char* optype, double oe, double taps) -> int {
@@ -782,7 +824,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   // at whole patch rows.  One stream with per-kernel events or debug dumps.
   int parts = 1;
   if (!dump && !evs)
-    while (parts < kSplitMax && N >= kSplitMin * parts * 2) parts *= 2;
+    while (parts < std::min(kSplitMax, max_parts) && N >= kSplitMin * parts * 2) parts *= 2;
   // a scene splits at whole patch rows (its patches are numbered row by row)
   const int unit = sc ? sc->pcols : 1;
   if (sc && N / unit < parts) parts = 1;
@@ -1051,6 +1093,24 @@ int bnn_forward_device(const Model* m, const float* d_input, int N, int H, int W
 }
 
 void* bnn_stream(const Model* m) { return (m && m->dev) ? (void*)m->dev->stream : nullptr; }
+
+int bnn_forward_device_noalloc(const Model* m, const float* d_input, int N, int H, int W, float* d_logits,
+                               void* stream) {
+  int rc;
+  if ((rc = check_shape(m, N, H, W))) return rc;
+  if (N == 0) return BNN_OK;
+  BnnDevice* D = m->dev;
+  if (!D->scratch) return set_err(BNN_EHIP, "allocation-free forward unavailable: %s", D->scratch_err.c_str());
+  Workspace w;
+  const size_t need = plan_ws(m, D, w, N, H, W, nullptr);
+  if (need > (size_t)BNN_NOALLOC_SCRATCH_BYTES)
+    return set_err(BNN_EARG, "N=%d H=%d W=%d needs %zu bytes of scratch; the allocation-free forward holds %zu",
+                   N, H, W, need, (size_t)BNN_NOALLOC_SCRATCH_BYTES);
+  plan_ws(m, D, w, N, H, W, D->scratch);
+  // one part on the caller's stream: no side streams, events or profiling
+  return enqueue_forward(m, D, w, d_input, N, H, W, d_logits, (hipStream_t)stream, nullptr, nullptr, nullptr,
+                         nullptr, 1);
+}
 
 int bnn_forward_patched(const Model* m, const float* input, int H, int W, float* logits, int P) {
   return run_scene_host(m, input, H, W, logits, P);

@@ -73,6 +73,7 @@ def lib() -> C.CDLL:
     L.bnn_forward.argtypes = [_vp, _f32, _ci, _ci, _f32]
     L.bnn_forward_batch.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32]
     L.bnn_forward_device.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
+    L.bnn_forward_device_noalloc.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
     L.bnn_forward_debug.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32, STAGE_CB, _vp]
     L.bnn_forward_patched.argtypes = [_vp, _f32, _ci, _ci, _f32, _ci]
     L.bnn_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
@@ -204,6 +205,13 @@ class Engine:
                        stream: Optional[int] = None) -> None:
         _check(self._fn("forward_device")(self.h, _vp(d_in), N, H, W, _vp(d_out),
                                           _vp(stream or None)))
+
+    def forward_device_noalloc(self, d_in: int, N: int, H: int, W: int, d_out: int,
+                               stream: Optional[int] = None) -> None:
+        """bnn_forward_device with no device allocation (v1 models only): the
+        inter-layer tensors live in the library's fixed per-GPU scratch array."""
+        _check(lib().bnn_forward_device_noalloc(self.h, _vp(d_in), N, H, W, _vp(d_out),
+                                                _vp(stream or None)))
 
     def forward_patched(self, cube: np.ndarray, P: int = 32) -> np.ndarray:
         """Scene [n_bands, H, W] -> logit map [n_classes, H, W] by independent

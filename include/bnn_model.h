@@ -102,6 +102,21 @@ int bnn_forward_device(const Model *m, const float *d_input, int N, int H, int W
                        float *d_logits, void *stream);
 void *bnn_stream(const Model *m);      /* the model's own hipStream_t (used by the host-pointer calls) */
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): bnn_forward_device without any allocation.  The
+ * inter-layer tensors live in a fixed device array of
+ * BNN_NOALLOC_SCRATCH_BYTES per GPU, held from the first bnn_load on that GPU
+ * until the process ends; a call whose tensors do not fit returns BNN_EARG
+ * (32x32 patches of the base-16 UNet: up to 1,980 per call).  It runs on
+ * `stream` alone (no side streams) and calls no hipMalloc, hipFree or
+ * allocating library routine.  Every call on one GPU shares that array, and
+ * nothing in it needs to start at zero: calls that overlap on one GPU, even
+ * on different models, race and must be ordered by the caller. */
+#define BNN_NOALLOC_SCRATCH_BYTES (48u << 20)
+int bnn_forward_device_noalloc(const Model *m, const float *d_input, int N, int H, int W,
+                               float *d_logits, void *stream);
+
 /* Scene inference by independent P x P patches, the tiling of the reference's
  * csrc/bnn_model_react.c:454-476 (bnn_forward_react_patched) applied to the v1
  * forward: patches start at multiples of P (a multiple of 16), an edge patch
