@@ -30,10 +30,12 @@ def build_engine(force: bool = True) -> None:
 
 def build_checker(force: bool = True) -> None:
     """CPU restatement of the reference (oracle/) and, where the reference
-    sources are present, the reference C itself into oracle/_ref/."""
+    sources are present, the reference C itself into oracle/_ref/, and the
+    reference's CLI mains built unchanged against include/ and the engine
+    (oracle/_ref/dropin/)."""
     _make(ORACLE, force=force)
     if os.path.isdir(REFERENCE_CSRC):
-        _make(ORACLE, "ref", force=force)
+        _make(ORACLE, "ref", "dropin", force=force)
 
 
 def build_all(force: bool = True) -> None:

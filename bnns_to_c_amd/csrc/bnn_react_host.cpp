@@ -270,6 +270,9 @@ struct BnnReactDevice {
   RWorkspace ws;
   float *stage_in = nullptr, *stage_out = nullptr;
   size_t stage_in_cap = 0, stage_out_cap = 0;
+  // pinned row strips of a streamed input file, filled in turn
+  float* strip[2] = {nullptr, nullptr};
+  hipEvent_t strip_done[2] = {nullptr, nullptr};
   // the second half of a large batch runs on this stream
   hipStream_t side = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
@@ -312,6 +315,12 @@ void release(BnnReactDevice* D) {
   if (D->ws.base) (void)hipFree(D->ws.base);
   if (D->stage_in) (void)hipFree(D->stage_in);
   if (D->stage_out) (void)hipFree(D->stage_out);
+  for (int k = 0; k < 2; ++k) {
+    if (D->strip[k]) (void)hipHostFree(D->strip[k]);
+    if (D->strip_done[k]) (void)hipEventDestroy(D->strip_done[k]);
+    D->strip[k] = nullptr;
+    D->strip_done[k] = nullptr;
+  }
   if (D->ev_fork) (void)hipEventDestroy(D->ev_fork);
   if (D->ev_join) (void)hipEventDestroy(D->ev_join);
   if (D->side) (void)hipStreamDestroy(D->side);
@@ -732,11 +741,63 @@ int run_patched_host(const ModelR* m, const float* cube, int H, int W, float* ma
   return BNN_OK;
 }
 
-int read_cube(FILE* f, int nb, int H, int W, std::vector<float>* cube) {
+// Row strips of a streamed input file hold this many floats (4 MiB).
+constexpr size_t kStripFloats = size_t(1) << 20;
+
+// The [nb,H,W] float32 cube in f, from the start of the file, into
+// D->stage_in, as the reference's file reader takes it: band by band, rows
+// r0..r1 of a band at their absolute offset (csrc/bnn_model_react.c:505-520).
+// Each strip of whole rows goes through one of two pinned buffers and is
+// copied on D->stream while the next one is read, so host memory never holds
+// the cube.  A short read fails with the reference's message.
+int stream_cube(BnnReactDevice* D, FILE* f, int nb, int H, int W) {
   if (!f) return set_err(BNN_EARG, "null input file");
-  cube->resize((size_t)nb * H * W);
-  if (fread(cube->data(), sizeof(float), cube->size(), f) != cube->size())
-    return set_err(BNN_EARG, "short read of the %dx%dx%d input cube", nb, H, W);
+  const size_t plane = (size_t)H * W;
+  int rc;
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, (size_t)nb * plane * 4))) return rc;
+  for (int k = 0; k < 2; ++k) {
+    if (!D->strip[k]) HIP_TRY(hipHostMalloc((void**)&D->strip[k], kStripFloats * 4, hipHostMallocDefault));
+    if (!D->strip_done[k]) HIP_TRY(hipEventCreateWithFlags(&D->strip_done[k], hipEventDisableTiming));
+  }
+  int rows = (int)std::min<size_t>(H, kStripFloats / (size_t)W);
+  // BNN_STREAM_ROWS=<r> caps a strip at r rows (any r >= 1 gives the same
+  // cube; tests use it to cross many strip boundaries on small images)
+  if (const char* e = getenv("BNN_STREAM_ROWS")) rows = std::min(rows, std::max(1, atoi(e)));
+  if (rows < 1) return set_err(BNN_EARG, "image rows of %d floats exceed a %zu-float strip", W, kStripFloats);
+  bool used[2] = {false, false};
+  int k = 0;
+  for (int b = 0; b < nb; ++b) {
+    for (int r0 = 0; r0 < H; r0 += rows, k ^= 1) {
+      const int r1 = std::min(H, r0 + rows);
+      const size_t n = (size_t)(r1 - r0) * W;
+      if (used[k]) HIP_TRY(hipEventSynchronize(D->strip_done[k]));  // its last copy has left
+      const off_t at = (off_t)(((size_t)b * H + r0) * W * 4);
+      if (fseeko(f, at, SEEK_SET) != 0 || fread(D->strip[k], 4, n, f) != n)
+        return set_err(BNN_EARG, "file_reader: short read band %d rows %d..%d", b, r0, r1);
+      HIP_TRY(hipMemcpyAsync(D->stage_in + b * plane + (size_t)r0 * W, D->strip[k], n * 4, hipMemcpyHostToDevice,
+                             D->stream));
+      HIP_TRY(hipEventRecord(D->strip_done[k], D->stream));
+      used[k] = true;
+    }
+  }
+  return BNN_OK;
+}
+
+// The forward of a streamed file: whole image (P = 0) or patch-wise.
+int run_file(const ModelR* m, FILE* f, int H, int W, float* logits, int P) {
+  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+  int rc;
+  if (!P && (rc = check_shape(m, 1, H, W))) return rc;
+  if (P && (size_t)m->n_bands * H * W * 4 >= 0x7FFFFFF0ull) return set_err(BNN_EARG, "cube >= 2 GiB");
+  BnnReactDevice* D = m->dev;
+  const size_t nout = (size_t)m->n_classes * H * W;
+  if ((rc = stream_cube(D, f, m->n_bands, H, W))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, nout * 4))) return rc;
+  rc = P ? run_patched_device(m, D->stage_in, H, W, D->stage_out, P, D->stream)
+         : run_device(m, D->stage_in, 1, H, W, D->stage_out, D->stream, nullptr);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(logits, D->stage_out, nout * 4, hipMemcpyDeviceToHost, D->stream));
+  HIP_TRY(hipStreamSynchronize(D->stream));
   return BNN_OK;
 }
 
@@ -825,8 +886,7 @@ int bnn_react_forward_device(const ModelR* m, const float* d_input, int N, int H
 void* bnn_react_stream(const ModelR* m) { return (m && m->dev) ? (void*)m->dev->stream : nullptr; }
 
 void bnn_forward_react_file(const ModelR* m, FILE* in_f, int H, int W, float* logits) {
-  std::vector<float> cube;
-  if (!m || read_cube(in_f, m->n_bands, H, W, &cube) || run_host(m, cube.data(), 1, H, W, logits, nullptr)) die();
+  if (run_file(m, in_f, H, W, logits, 0)) die();
 }
 
 void bnn_forward_react_patched(const ModelR* m, const float* input, int H, int W, float* logits, int P) {
@@ -838,8 +898,7 @@ int bnn_react_forward_patched(const ModelR* m, const float* input, int H, int W,
 }
 
 void bnn_forward_react_patched_file(const ModelR* m, FILE* f, int H, int W, float* logits, int P) {
-  std::vector<float> cube;
-  if (!m || read_cube(f, m->n_bands, H, W, &cube) || run_patched_host(m, cube.data(), H, W, logits, P)) die();
+  if (run_file(m, f, H, W, logits, P)) die();
 }
 
 int bnn_react_forward_patched_device(const ModelR* m, const float* d_input, int H, int W, float* d_logits, int P,

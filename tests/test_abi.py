@@ -49,6 +49,47 @@ def test_header_compiles_as_c(tmp_path):
                     "-c", str(src), "-o", str(tmp_path / "t.o")], check=True)
 
 
+REFERENCE_CSRC = "/root/reference/csrc"
+
+
+@pytest.mark.parametrize("main", ["main.c", "main_stem.c", "main_react.c"])
+def test_reference_mains_build_against_include(tmp_path, main):
+    """The reference's CLI mains compile unchanged against include/ (fed on
+    standard input, so their #include "bnn_model.h" finds include/ and not
+    the reference's header beside them) and link against libbnn_hip.so:
+    every symbol they call is exported with a matching declaration."""
+    src = os.path.join(REFERENCE_CSRC, main)
+    if not os.path.exists(src):
+        pytest.skip("reference sources absent")
+    exe = tmp_path / main.replace(".c", "")
+    with open(src, "rb") as f:
+        r = subprocess.run(["gcc", "-O2", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                            "-x", "c", "-", "-x", "none", "-o", str(exe), "-L", os.path.dirname(E.LIB_PATH),
+                            "-lbnn_hip", "-lm"], stdin=f, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    # the headers it resolved are this repository's
+    with open(src, "rb") as f:
+        deps = subprocess.run(["gcc", "-M", "-I", os.path.join(ROOT, "include"), "-x", "c", "-"], stdin=f,
+                              capture_output=True, text=True).stdout
+    assert os.path.join(ROOT, "include", "bnn_prof.h") in deps and REFERENCE_CSRC not in deps
+
+
+def test_cli_argument_errors():
+    """The CLIs' argument checks run before any GPU call and keep the
+    reference's exit codes and messages (csrc/main.c:23-26,
+    csrc/main_react.c:44-50)."""
+    r = subprocess.run([E.CLI_PATH, "a.blob", "rand"], capture_output=True, text=True)
+    assert r.returncode == 1 and "input.bin|rand output.bin [H W [reps]]" in r.stderr
+    assert "weights.blob" in r.stderr
+    r = subprocess.run([E.CLI_STEM_PATH], capture_output=True, text=True)
+    assert r.returncode == 1 and "weights_stem.blob" in r.stderr
+    r = subprocess.run([E.CLI_REACT_PATH, "a.blob", "rand", "o.bin", "32"], capture_output=True, text=True)
+    assert r.returncode == 2 and "blob input|rand output H W [reps]" in r.stderr
+    for hw in (["0", "32"], ["32", "-4"], ["32", "32", "0"]):
+        r = subprocess.run([E.CLI_REACT_PATH, "a.blob", "rand", "o.bin"] + hw, capture_output=True, text=True)
+        assert r.returncode == 2 and "bad H/W/reps" in r.stderr, hw
+
+
 def test_model_struct_prefix_matches_reference():
     # main.c reads m->n_bands / m->n_classes: the leading ints keep their order
     class Conv(ctypes.Structure):
