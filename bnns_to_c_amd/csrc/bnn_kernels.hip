@@ -20,6 +20,7 @@
 // reference's multiply-then-add.  Out-of-image taps read zeros and sum to
 // +0; skipping a tap and adding that +0 are the same, since s and acc never
 // hold -0.
+#include <algorithm>
 #include <utility>
 
 #include "bnn_device.h"
@@ -661,6 +662,273 @@ void k_real_mfma(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW) {
 }
 
 // ------------------------------------------------------------------------
+// real-input conv on the matrix cores, persistent, 16-byte staging
+// ------------------------------------------------------------------------
+// The same per-tap K = 1 MFMA chains, weight masks and epilogue as
+// k_real_mfma<2, 2> (8 x 32 output tile per block, 4 waves of 4 x 16
+// pixels, 16 channels per group), for inputs whose row width is a multiple
+// of 4, with two changes to the input staging:
+//  * Each lane's LDS-writing load moves 16 bytes (4 columns), so a chunk of
+//    8 channels x 10 tile rows is 15 loads per block instead of 80.  A tile
+//    row is 10 such slots, image columns x0-4 .. x0+35 (the 34 the taps
+//    read sit at 3..36), padded to 12 slots = 48 floats, 16 mod 32: the
+//    four 16-lane rows of an operand read fall in disjoint bank groups of
+//    each half-wave.  A slot outside the image, or a pad slot, takes the
+//    offset kFar and lands as zeros.  The load's LDS address is
+//    M0 + 16 * lane, so slot s of a chunk (row s / 12, slot s % 12) is byte
+//    16 s of its buffer and the 960 slots are 15 contiguous 1 KiB loads,
+//    load k issued by wave k % 4.
+//  * Persistent blocks walk tiles blockIdx.x, +gridDim.x, ...; the chunk
+//    pipeline (three buffers: one read, one landed, one in flight) runs
+//    across tile boundaries, so a tile's first chunks arrive during the
+//    previous tile's last ones and its epilogue.
+// Measured against reading the weights as per-lane floats from LDS (three
+// more LDS reads per channel instead of three selects): the selects are
+// faster.  Every helper lambda is forced inline: one left out of line takes
+// the accumulators by reference, which puts them in scratch memory for the
+// whole kernel.
+#ifndef BNN_R4ROWF
+#define BNN_R4ROWF 48
+#endif
+constexpr int kR4RowF = BNN_R4ROWF;                  // floats per LDS tile row
+constexpr int kR4Slots = kR4RowF / 4;                // 16-byte slots per row
+constexpr int kR4Rows = kRealMfmaCI * 10;            // tile rows per chunk
+constexpr int kR4Ld = kR4Rows * kR4Slots / 64;       // loads per chunk
+constexpr int kR4LdW = (kR4Ld + 3) / 4;              // loads per wave (at most)
+constexpr int kR4BufF = kR4Ld * 256;                 // floats per buffer
+static_assert(kR4Rows * kR4Slots % 64 == 0, "whole 1 KiB loads per chunk");
+static_assert(kR4RowF % 32 == 16 && kR4Slots >= 10, "rows of 10 slots, 16 mod 32 floats apart");
+
+template <bool PARTIAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_real_mfma4(const RealArgs a, uint32_t xbytes, int tilesH, int tilesW, int ntile) {
+  constexpr int CI = kRealMfmaCI, LR = 10, TR = 8, TC = 32, LPL = LR * kR4RowF;
+  __shared__ __attribute__((aligned(16))) float buf[3 * kR4BufF];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = (wv >> 1) * 4, wc = (wv & 1) * 16;
+  const int g = blockIdx.y;
+  const int nchunk = (a.cin + CI - 1) / CI;
+  const int t0 = blockIdx.x, tstep = gridDim.x;
+  const int mytiles = t0 < ntile ? (ntile - t0 + tstep - 1) / tstep : 0;
+  const int total = mytiles * nchunk;
+  if (total == 0) return;
+  const int cq = g * 16 + 4 * (lane >> 4);
+  // this wave's loads k = wv + 4m < 15
+  const int nld = (kR4Ld - wv + 3) / 4;
+  // per row load m: the lane's slot -> channel lcl, tile row lr and column
+  // group lj; rel is the slot's element offset from the tile's first row and
+  // column group.  A pad slot, or a slot past the chunk's loads, gets a row
+  // far outside every image, so the per-tile test below rejects it.  (Plain
+  // integers: per-lane flags would each take a scalar register pair.)
+  const InGeom ig0 = in_geom(a, 0);
+  const uint32_t cstr = (uint32_t)ig0.cstride, rstr = (uint32_t)ig0.rstride;
+  int lcl[kR4LdW], lr[kR4LdW], lj4[kR4LdW];
+  uint32_t rel[kR4LdW];
+#pragma unroll
+  for (int m = 0; m < kR4LdW; ++m) {
+    const int k = wv + 4 * m;
+    const int sl = k * 64 + lane, row = sl / kR4Slots, j = sl - row * kR4Slots;
+    lcl[m] = row / LR;
+    lr[m] = (k < kR4Ld && j < 10) ? row - lcl[m] * LR : -(1 << 20);
+    lj4[m] = 4 * j;
+    rel[m] = (uint32_t)lcl[m] * cstr + (uint32_t)(row - lcl[m] * LR) * rstr + (uint32_t)(4 * j);
+  }
+  const uint32_t cs4 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(cstr * 4u));
+  // lane part of the byte offset of each row load for tile t (kRealFar
+  // where the slot lies outside the image or is a pad slot); the sums wrap
+  // modulo 2^32 and are exact for the slots inside the image
+  auto tile_offsets = [&](int t, uint32_t (&lo)[kR4LdW]) __attribute__((always_inline)) {
+    const int tx = t % tilesW, rest = t / tilesW, ty = rest % tilesH, n = rest / tilesH;
+    const InGeom ig = in_geom(a, n);
+    const int y0 = ty * TR, x0 = tx * TC;
+    const uint32_t org = (uint32_t)ig.base + (uint32_t)(y0 - 1) * rstr + (uint32_t)(x0 - 4);
+#pragma unroll
+    for (int m = 0; m < kR4LdW; ++m) {
+      const uint32_t iy = (uint32_t)(y0 - 1 + lr[m]), ix = (uint32_t)(x0 - 4 + lj4[m]);
+      const bool ok = (iy < (uint32_t)ig.ylim) & (ix < (uint32_t)ig.xlim);
+      lo[m] = ok ? (org + rel[m]) * 4u : kRealFar;
+    }
+  };
+  const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
+  // (every word through readfirstlane: the descriptors must live in SGPRs)
+  auto uni = [](uint32_t v) __attribute__((always_inline)) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+  const u32x4 xsrc = {uni((uint32_t)xaddr), uni((uint32_t)(xaddr >> 32) & 0xFFFFu), uni(xbytes), 0x00020000u};
+  typedef __attribute__((address_space(3))) float* lds_f32;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_f32)buf;
+  // chunk ch of the tile whose row offsets are lo, into buffer B
+  auto issue = [&](int b, int ch, const uint32_t (&lo)[kR4LdW]) __attribute__((always_inline)) {
+    const uint32_t dst = lds0 + (uint32_t)(b * kR4BufF * 4);
+    const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(ch * CI) * cs4));
+#pragma unroll
+    for (int m = 0; m < kR4LdW; ++m) {
+      const int k = wv + 4 * m;
+      if (k >= kR4Ld) break;
+      const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + (uint32_t)(k * 1024)));
+      uint32_t vo = lo[m];
+      if (PARTIAL && lcl[m] >= a.cin - ch * CI) vo = kRealFar;
+      const u32x4 rd = xsrc;
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :
+                   : "s"(m0v), "v"(vo), "s"(rd), "s"(sx)
+                   : "memory");
+    }
+  };
+
+  f32x16 acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+  // the lane's operand base in a buffer: tile row wr + lane/16, LDS column
+  // wc + lane%16 + 3 (image column x0 + wc + lane%16 - 1)
+  const int lb = (wr + (lane >> 4)) * kR4RowF + wc + (lane & 15) + 3;
+  // the weight masks through the constant address space (scalar loads)
+  typedef const __attribute__((address_space(4))) uint64_t* const_u64;
+  const const_u64 wm = (const_u64)a.wm + (size_t)g * nchunk * CI * 3;
+  auto run_chunk = [&](auto bc, int ch) __attribute__((always_inline)) {
+    const float* tb = buf + decltype(bc)::value * kR4BufF + lb;
+    uint64_t mk[CI][3];
+#pragma unroll
+    for (int cl = 0; cl < CI; ++cl)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) mk[cl][q] = wm[(size_t)(ch * CI + cl) * 3 + q];
+    float xb[2][9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) xb[0][t] = tb[(t / 3) * kR4RowF + t % 3];
+#pragma unroll
+    for (int cl = 0; cl < CI; ++cl) {
+      float wa[3];
+#pragma unroll
+      for (int q = 0; q < 3; ++q) wa[q] = __builtin_amdgcn_inverse_ballot_w64(mk[cl][q]) ? 1.0f : -1.0f;
+      if (cl + 1 < CI) {
+#pragma unroll
+        for (int t = 0; t < 9; ++t) xb[(cl + 1) & 1][t] = tb[(cl + 1) * LPL + (t / 3) * kR4RowF + t % 3];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_taps(acc, wa, xb[cl & 1], std::make_integer_sequence<int, 9>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto chunk_barrier = []() __attribute__((always_inline)) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  // wait until only this wave's loads of the newest chunk may be in flight
+  constexpr int kWaitHi = (kR4LdW & 15) | (7 << 4) | (15 << 8), kWaitLo = ((kR4LdW - 1) & 15) | (7 << 4) | (15 << 8);
+  static_assert(kR4LdW < 16, "vmcnt field");
+  auto wait_landed = [&](bool newest_in_flight) __attribute__((always_inline)) {
+    if (!newest_in_flight) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    else if (nld == kR4LdW) __builtin_amdgcn_s_waitcnt(kWaitHi);
+    else __builtin_amdgcn_s_waitcnt(kWaitLo);
+  };
+
+  // alpha and fold parameters of the lane's four channels, the same for
+  // every tile (arrays padded to 32 channels)
+  float p_al[4], p_A[4], p_B[4], p_sl[4], p_rs[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    p_al[k] = a.alpha[cq + k];
+    if (a.out) {
+      p_A[k] = a.A[cq + k];
+      p_B[k] = a.B[cq + k];
+      p_sl[k] = a.slope[cq + k];
+      p_rs[k] = a.rsign[cq + k];
+    }
+  }
+  const int HW = a.H * a.W;
+  // the tile's taps summed in row-major order, alpha, the real fold, bits
+  // (the k_real_mfma epilogue; csrc/bnn_conv_realin.c:99-111,
+  // csrc/bnn_fold.c:62-77)
+  auto epilogue = [&](int t) __attribute__((always_inline)) {
+    const int tx = t % tilesW, rest = t / tilesW, ty = rest % tilesH, n = rest / tilesH;
+    const int y0 = ty * TR, x0 = tx * TC;
+    const int xo = x0 + wc + (lane & 15);
+    uint32_t w01 = 0, w23 = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = 0.0f;
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) v = __fadd_rn(v, acc[tp][r]);
+      const int k = r & 3, b = r >> 2;
+      const int y = y0 + wr + b;
+      const int co = cq + k;
+      const float o = __fmul_rn(p_al[k], v);
+      if (a.f32 && y < a.H && xo < a.W && co < a.cout)
+        a.f32[((size_t)n * a.cout + co) * HW + (size_t)y * a.W + xo] = o;
+      if (a.out) {
+        float z = __fmaf_rn(p_A[k], o, p_B[k]);
+        if (z < 0.0f) z = __fmul_rn(p_sl[k], z);
+        const float rr = __fadd_rn(z, p_rs[k]);
+        const uint32_t bit = (rr > 0.0f && co < a.cout) ? 1u : 0u;
+        const int sh = 16 * (b & 1) + 4 * (lane >> 4) + k;
+        if (b < 2) w01 |= bit << sh;
+        else w23 |= bit << sh;
+      }
+    }
+    if (!a.out) return;
+    w01 |= (uint32_t)__shfl_xor((int)w01, 16);
+    w01 |= (uint32_t)__shfl_xor((int)w01, 32);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 16);
+    w23 |= (uint32_t)__shfl_xor((int)w23, 32);
+    const int q = lane >> 4;
+    const uint32_t word = ((q < 2 ? w01 : w23) >> (16 * (q & 1))) & 0xFFFFu;
+    const int y = y0 + wr + q;
+    if (y >= a.H || xo >= a.W) return;
+    const int cwo = (a.cout + 31) >> 5;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)y * a.W + xo) * cwo) + g * 2;
+    if ((g & 1) == 0 && g == (int)gridDim.y - 1) *reinterpret_cast<uint32_t*>(dst) = word;
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+  };
+
+  // The issue position runs two chunks ahead of the compute position, so
+  // the last two steps of a tile issue the next tile's first two chunks.
+  // Row offsets of the current and the next tile are computed once per tile,
+  // outside the chunk loop (kept out of it, the address arithmetic takes
+  // the scalar registers the loop needs).  Chunk c of a tile lives in
+  // buffer c % 3: with nchunk a multiple of 3 every tile starts in buffer 0
+  // and each read's buffer is a compile-time constant.
+  uint32_t lo_cur[kR4LdW], lo_nxt[kR4LdW];
+  tile_offsets(t0, lo_cur);
+  if (mytiles > 1) tile_offsets(t0 + tstep, lo_nxt);
+  issue(0, 0, lo_cur);
+  if (nchunk > 1) issue(1, 1, lo_cur);
+  else if (mytiles > 1) issue(1, 0, lo_nxt);
+  wait_landed(total > 1);
+  chunk_barrier();
+  int gc = 0;
+  auto step = [&](auto bc, int ch) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
+    const bool ahead = gc + 2 < total;
+    if (ahead) {
+      if (ch + 2 < nchunk) issue((B + 2) % 3, ch + 2, lo_cur);
+      else issue((B + 2) % 3, ch + 2 - nchunk, lo_nxt);
+    }
+    run_chunk(bc, ch);
+    wait_landed(ahead);
+    chunk_barrier();
+    ++gc;
+  };
+#pragma unroll 1
+  for (int tc = 0; tc < mytiles; ++tc) {
+#pragma unroll 1
+    for (int ch = 0; ch < nchunk; ch += 3) {
+      step(std::integral_constant<int, 0>{}, ch);
+      step(std::integral_constant<int, 1>{}, ch + 1);
+      step(std::integral_constant<int, 2>{}, ch + 2);
+    }
+    epilogue(t0 + tc * tstep);
+#pragma unroll
+    for (int tp = 0; tp < 9; ++tp)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[tp][r] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kR4LdW; ++m) lo_cur[m] = lo_nxt[m];
+    if (tc + 2 < mytiles) tile_offsets(t0 + (tc + 2) * tstep, lo_nxt);
+  }
+}
+
 // 1x1 real-input stem on the matrix cores (v2 models)
 // ------------------------------------------------------------------------
 // out[co][p] = alpha[co] * (sum over ci from 0 in order of w[co][ci] * x[ci][p])
@@ -1914,10 +2182,40 @@ hipError_t launch_bconv(const BconvArgs& a, int epi, int mt, int cog, bool dump,
 #define BNN_MWC 2
 #endif
 
-hipError_t launch_real(const RealArgs& a, hipStream_t s) {
+// compute units of the current device (cached per device)
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+hipError_t launch_real(const RealArgs& a, hipStream_t s, int parts) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
+  // 16-byte staging: every 4-column group of the input lies wholly inside
+  // or wholly outside the image when the row width is a multiple of 4
+  const int rowlen = a.pcols > 0 ? a.sW : a.W;
+  const int nchunk = (a.cin + kRealMfmaCI - 1) / kRealMfmaCI;
+  if (a.wm && rowlen % 4 == 0 && (uintptr_t)a.x % 16 == 0 && xbytes < kRealFar && nchunk % 3 == 0) {
+    const int tilesH = (a.H + 7) / 8, tilesW = (a.W + 31) / 32;
+    const long ntile = (long)a.N * tilesH * tilesW;
+    if (ntile >= 0x80000000l) return hipErrorInvalidValue;
+    const int groups = (a.cout + 15) / 16;
+    const long share = std::max(1l, 2l * device_cus() / std::max(1, parts));
+    dim3 grid((unsigned)std::min(ntile, share), (unsigned)groups);
+    if (a.cin % kRealMfmaCI)
+      hipLaunchKernelGGL((k_real_mfma4<true>), grid, dim3(256), 0, s, a, (uint32_t)xbytes, tilesH, tilesW, (int)ntile);
+    else
+      hipLaunchKernelGGL((k_real_mfma4<false>), grid, dim3(256), 0, s, a, (uint32_t)xbytes, tilesH, tilesW, (int)ntile);
+    return hipGetLastError();
+  }
   if (a.wm) {
     if (xbytes >= kRealFar) return hipErrorInvalidValue;
     constexpr int WR = BNN_MWR, WC = BNN_MWC;

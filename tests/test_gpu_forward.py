@@ -84,6 +84,34 @@ def test_first_conv_general_signs(tmp_path, orc):
         eng.close()
 
 
+@pytest.mark.parametrize("nb,H,W,N", [
+    (13, 32, 32, 2),   # last chunk of 8 bands partly empty; 16-byte staging
+    (37, 16, 36, 2),   # two tiles across, the second partly outside
+    (120, 24, 64, 3),  # full chunks, two tiles across, a partial tile row
+    (5, 20, 17, 2),    # width not a multiple of 4: the 4-byte staging kernel
+    (120, 16, 16, 300),  # more tiles than the persistent grid, two batch parts
+])
+def test_first_conv_shapes(tmp_path, orc, nb, H, W, N):
+    """The real first conv on both staging kernels (16-byte slots when the
+    width is a multiple of 4, 4-byte rows otherwise), band counts that leave
+    the last 8-channel chunk partly empty, tiles cut by the image edge and a
+    batch larger than the persistent grid: enc1.conv1, enc1.act1 and the
+    logits bit for bit against the checker."""
+    b = synth.make_blob(seed=40 + nb, base=8, n_bands=nb)
+    eng, _ = _engine(tmp_path, b)
+    model = orc.parse(B.to_bytes(b))
+    x = synth.make_input(41 + nb, N, nb, H, W)
+    logits, st = eng.forward_debug(x)
+    for n in sorted({0, N // 2, N - 1}):
+        want, ref_st = model.forward(x[n], stages=True)
+        for name in ("enc1.conv1", "enc1.act1"):
+            assert _same(st[name][n], ref_st[name]), (name, n)
+        assert _same(logits[n], want), n
+    # the production path (no stage dumps, batch parts on two streams)
+    assert _same(eng.forward_batch(x), logits)
+    eng.close()
+
+
 def test_golden_from_reference(tmp_path, golden):
     """stage hashes and logits recorded from the reference's own C"""
     meta, arrays = golden
