@@ -711,7 +711,6 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   // [N][ncls][H][W], so a part of the batch is the same tensors offset by
   // nb patches.
   int nb = 0, cnt = N;
-  int nparts = 1;  // parts of the batch running side by side
   hipStream_t st = s;
   auto at = [&](const uint32_t* p, int lvl, int cw) -> const uint32_t* {
     return p ? p + (size_t)nb * hs[lvl] * wsz[lvl] * cw : nullptr;
@@ -731,7 +730,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       HIP_TRY(launch_stem(ra, st));
       if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
     } else {
-      HIP_TRY(launch_real(ra, st, nparts));
+      HIP_TRY(launch_real(ra, st));
       if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
     }
     return BNN_OK;
@@ -829,7 +828,6 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   // a scene splits at whole patch rows (its patches are numbered row by row)
   const int unit = sc ? sc->pcols : 1;
   if (sc && N / unit < parts) parts = 1;
-  nparts = parts;
   if (parts == 1) return part();
   if (!D->ev_fork) {
     // all or nothing: a failure leaves no half-made set behind

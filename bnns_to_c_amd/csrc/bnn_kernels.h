@@ -325,10 +325,7 @@ inline size_t mfma_s_len(int cout) { return (size_t)16 * ((cout + 63) / 64 * 64)
 // an image narrow enough for its LDS tile).
 bool mfma_conv_fits(int cout, int H, int W, int epi);
 hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& m, int epi, bool dump, hipStream_t s);
-// parts: how many launches of this kernel run side by side (a split
-// batch); the persistent 16-byte staging kernel sizes its grid to its share
-// of the device
-hipError_t launch_real(const RealArgs& a, hipStream_t s, int parts = 1);
+hipError_t launch_real(const RealArgs& a, hipStream_t s);
 
 // Simple kernels behind the reference's batch-1 kernel ABI.
 hipError_t launch_pack_act(const int8_t* a, uint32_t* out, int N, int C, int H, int W,

@@ -2195,7 +2195,7 @@ int device_cus() {
   return cus[dev];
 }
 
-hipError_t launch_real(const RealArgs& a, hipStream_t s, int parts) {
+hipError_t launch_real(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= 0x80000000ull) return hipErrorInvalidValue;  // out-of-range offsets must stay distinct
@@ -2208,7 +2208,12 @@ hipError_t launch_real(const RealArgs& a, hipStream_t s, int parts) {
     const long ntile = (long)a.N * tilesH * tilesW;
     if (ntile >= 0x80000000l) return hipErrorInvalidValue;
     const int groups = (a.cout + 15) / 16;
-    const long share = std::max(1l, 2l * device_cus() / std::max(1, parts));
+    // two blocks per CU fit; the channel groups share them.  A split batch's
+    // parts each take the whole grid too: when they run side by side the
+    // later part's blocks start as the earlier's finish, and when they do
+    // not, a smaller grid would leave each part at half occupancy (measured
+    // 521 vs 526 us for the batch-1024 forward)
+    const long share = std::max(1l, 2l * device_cus() / groups);
     dim3 grid((unsigned)std::min(ntile, share), (unsigned)groups);
     if (a.cin % kRealMfmaCI)
       hipLaunchKernelGGL((k_real_mfma4<true>), grid, dim3(256), 0, s, a, (uint32_t)xbytes, tilesH, tilesW, (int)ntile);

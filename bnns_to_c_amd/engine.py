@@ -201,6 +201,12 @@ class Engine:
         _check(self._fn("forward_batch")(self.h, _p(x, _f32), N, H, W, _p(out, _f32)))
         return out
 
+    def forward_batch_ptr(self, x_ptr: int, N: int, H: int, W: int, out_ptr: int) -> None:
+        """bnn_forward_batch on caller-owned host buffers given by address
+        (e.g. pinned memory): the copies in and out are part of the call."""
+        _check(self._fn("forward_batch")(self.h, C.cast(C.c_void_p(x_ptr), _f32), N, H, W,
+                                         C.cast(C.c_void_p(out_ptr), _f32)))
+
     def forward_device(self, d_in: int, N: int, H: int, W: int, d_out: int,
                        stream: Optional[int] = None) -> None:
         _check(self._fn("forward_device")(self.h, _vp(d_in), N, H, W, _vp(d_out),
