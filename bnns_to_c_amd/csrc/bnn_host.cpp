@@ -407,11 +407,14 @@ struct BnnDevice {
   size_t stage_in_cap = 0;
   float* stage_out = nullptr;
   size_t stage_out_cap = 0;
-  // scene pipeline: pinned host strips, their copy stream and events
+  // scene pipeline: pinned host strips, device strip buffers (cube rows in,
+  // map rows out), their copy stream and events
   float* pin[2] = {};
   size_t pin_cap = 0;
+  float *strip_in[2] = {}, *strip_out[2] = {};
+  size_t strip_in_cap[2] = {}, strip_out_cap[2] = {};
   hipStream_t copy = nullptr;
-  hipEvent_t ev_copied[2] = {}, ev_free[2] = {};
+  hipEvent_t ev_copied[2] = {}, ev_free[2] = {}, ev_done[2] = {};
   // the later parts of a large batch run their binary layers on these streams
   hipStream_t side[kSplitMax - 1] = {};
   hipEvent_t ev_fork = nullptr, ev_join[kSplitMax - 1] = {};
@@ -524,8 +527,11 @@ void release(BnnDevice* D) {
   if (D->copy) (void)hipStreamSynchronize(D->copy);
   for (int k = 0; k < 2; ++k) {
     if (D->pin[k]) (void)hipHostFree(D->pin[k]);
+    if (D->strip_in[k]) (void)hipFree(D->strip_in[k]);
+    if (D->strip_out[k]) (void)hipFree(D->strip_out[k]);
     if (D->ev_copied[k]) (void)hipEventDestroy(D->ev_copied[k]);
     if (D->ev_free[k]) (void)hipEventDestroy(D->ev_free[k]);
+    if (D->ev_done[k]) (void)hipEventDestroy(D->ev_done[k]);
   }
   if (D->copy) (void)hipStreamDestroy(D->copy);
   if (D->ev_fork) (void)hipEventDestroy(D->ev_fork);
@@ -864,21 +870,48 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   return BNN_OK;
 }
 
+// The kernels address a launch's tensors with 32-bit byte offsets, so a
+// launch covers at most this many patches (its input under 2 GiB, less the
+// margin the out-of-range offsets use); larger batches run as several.
+int patches_per_launch(const Model* m, int H, int W) {
+  const size_t per = (size_t)m->n_bands * H * W * 4;
+  return (int)std::min<size_t>(0x7FFFFFF0ull / per, 1u << 30);
+}
+
 int check_shape(const Model* m, int N, int H, int W) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   if (N < 0) return set_err(BNN_EARG, "negative batch");
   if (H < 16 || W < 16)
     return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
-  if ((size_t)N * m->n_bands * H * W * 4 >= 0x80000000ull)
-    return set_err(BNN_EARG, "batch too large for one launch (%zu input bytes >= 2 GiB)",
-                   (size_t)N * m->n_bands * H * W * 4);
+  if (patches_per_launch(m, H, W) < 1)
+    return set_err(BNN_EARG, "one %dx%d patch of %d bands exceeds a launch (2 GiB)", H, W, m->n_bands);
   return BNN_OK;
 }
 
+int run_device_launch(const Model* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+                      Dumps* dmp);
+
+// A batch past the per-launch limit runs as consecutive launches of whole
+// sub-batches (the input and logits offset by their first patch), in order
+// on the stream.
 int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
                Dumps* dmp) {
   int rc;
   if ((rc = check_shape(m, N, H, W))) return rc;
+  const int per = patches_per_launch(m, H, W);
+  if (N > per && dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes at most %d patches of %dx%d", per, H, W);
+  for (int n0 = 0; n0 < N; n0 += per) {
+    const int n = std::min(per, N - n0);
+    if ((rc = run_device_launch(m, d_in + (size_t)n0 * m->n_bands * H * W, n, H, W,
+                                d_logits + (size_t)n0 * m->n_classes * H * W, s, dmp)))
+      return rc;
+  }
+  return BNN_OK;
+}
+
+int run_device_launch(const Model* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+                      Dumps* dmp) {
+  int rc;
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
   if ((rc = ensure_ws(m, D, D->ws, N, H, W))) return rc;
@@ -911,11 +944,14 @@ int check_scene(const Model* m, int H, int W, int P) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   if (P < 16 || P % 16) return set_err(BNN_EARG, "patch size %d: must be a positive multiple of 16 (four 2x2 pools)", P);
   if (H < 1 || W < 1) return set_err(BNN_EARG, "scene %dx%d is empty", H, W);
-  if ((size_t)m->n_bands * H * W * 4 >= 0x80000000ull)
-    return set_err(BNN_EARG, "scene too large for one launch (%zu cube bytes >= 2 GiB)",
-                   (size_t)m->n_bands * H * W * 4);
+  // one patch row of the cube must fit a launch (strips are whole patch rows)
+  if ((size_t)m->n_bands * P * W * 4 >= 0x7FFFFFF0ull)
+    return set_err(BNN_EARG, "one row of %dx%d patches of a %d-wide scene exceeds a launch (2 GiB)", P, P, W);
   return BNN_OK;
 }
+
+// a cube the kernels can address in place (32-bit byte offsets)
+bool scene_in_place(const Model* m, int H, int W) { return (size_t)m->n_bands * H * W * 4 < 0x7FFFFFF0ull; }
 
 // patch rows [prow0, prow0 + nrows) of the scene
 int run_scene_rows(const Model* m, const float* d_cube, int H, int W, float* d_map, int P, int prow0, int nrows,
@@ -943,11 +979,16 @@ int run_scene_rows(const Model* m, const float* d_cube, int H, int W, float* d_m
   return rc;
 }
 
-// Host cube -> host map.  The cube goes to the device in strips of whole
-// patch rows through two pinned buffers: host threads fill one buffer while
-// the copy stream moves the other and the model's stream runs the strip
-// before; the map comes back once at the end.
-int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, int P) {
+// Scene by strips: R whole patch rows at a time, each staged as its own
+// [nb][rows][W] sub-cube (rows = R*P, fewer at the bottom edge) and run as a
+// scene of `rows` rows; its map rows [ncls][rows][W] go to the full map with
+// one 2-D copy.  Every launch then addresses at most one strip, so cubes of
+// any size run, and device memory holds two strips.  A host cube is copied
+// through two pinned buffers (host threads fill one while the copy stream
+// moves the other and the model's stream runs the strip before); a device
+// cube is copied strip by strip on the model's stream.
+int run_scene_strips(const Model* m, const float* cube, bool host_cube, int H, int W, float* map, bool host_map,
+                     int P, hipStream_t s) {
   int rc;
   if ((rc = check_scene(m, H, W, P))) return rc;
   BnnDevice* D = m->dev;
@@ -956,10 +997,12 @@ int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, 
   // strips of about 32 MB of input
   const size_t row_bytes = (size_t)nb * P * W * 4;
   const int R = std::max(1, (int)std::min<size_t>(prows, (32u << 20) / row_bytes));
-  const size_t strip_bytes = row_bytes * R;
-  if ((rc = grow(&D->stage_in, &D->stage_in_cap, (size_t)nb * H * W * 4))) return rc;
-  if ((rc = grow(&D->stage_out, &D->stage_out_cap, (size_t)ncls * H * W * 4))) return rc;
-  if (D->pin_cap < strip_bytes) {
+  const size_t strip_bytes = row_bytes * R, smap_bytes = (size_t)ncls * R * P * W * 4;
+  for (int k = 0; k < 2; ++k) {
+    if ((rc = grow(&D->strip_in[k], &D->strip_in_cap[k], strip_bytes))) return rc;
+    if ((rc = grow(&D->strip_out[k], &D->strip_out_cap[k], smap_bytes))) return rc;
+  }
+  if (host_cube && D->pin_cap < strip_bytes) {
     HIP_TRY(hipDeviceSynchronize());
     for (int k = 0; k < 2; ++k) {
       if (D->pin[k]) (void)hipHostFree(D->pin[k]);
@@ -974,6 +1017,7 @@ int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, 
     for (int k = 0; k < 2; ++k) {
       HIP_TRY(hipEventCreateWithFlags(&D->ev_copied[k], hipEventDisableTiming));
       HIP_TRY(hipEventCreateWithFlags(&D->ev_free[k], hipEventDisableTiming));
+      HIP_TRY(hipEventCreateWithFlags(&D->ev_done[k], hipEventDisableTiming));
     }
   }
   const unsigned nthr = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
@@ -981,27 +1025,41 @@ int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, 
     const int b = k & 1;
     const int nr = std::min(R, prows - pr0);
     const int r0 = pr0 * P, rows = std::min(nr * P, H - r0);
-    if (k >= 2) HIP_TRY(hipEventSynchronize(D->ev_free[b]));  // its copy two strips ago is done
-    // [nb][rows][W] of the strip into the pinned buffer, bands split over threads
-    float* dst = D->pin[b];
-    auto fill = [&](int b0, int b1) {
-      for (int band = b0; band < b1; ++band)
-        memcpy(dst + (size_t)band * rows * W, cube + ((size_t)band * H + r0) * W, (size_t)rows * W * 4);
-    };
-    std::vector<std::thread> th;
-    for (unsigned t = 1; t < nthr; ++t) th.emplace_back(fill, nb * t / nthr, nb * (t + 1) / nthr);
-    fill(0, nb / nthr);
-    for (auto& t : th) t.join();
-    HIP_TRY(hipMemcpy2DAsync(D->stage_in + (size_t)r0 * W, (size_t)H * W * 4, dst, (size_t)rows * W * 4,
-                             (size_t)rows * W * 4, nb, hipMemcpyHostToDevice, D->copy));
-    HIP_TRY(hipEventRecord(D->ev_free[b], D->copy));
-    HIP_TRY(hipEventRecord(D->ev_copied[b], D->copy));
-    HIP_TRY(hipStreamWaitEvent(D->stream, D->ev_copied[b], 0));
-    if ((rc = run_scene_rows(m, D->stage_in, H, W, D->stage_out, P, pr0, nr, D->stream))) return rc;
+    const size_t band = (size_t)rows * W;  // floats of one band of the strip
+    if (host_cube) {
+      if (k >= 2) HIP_TRY(hipEventSynchronize(D->ev_free[b]));  // its copy two strips ago is done
+      // [nb][rows][W] of the strip into the pinned buffer, bands split over threads
+      float* dst = D->pin[b];
+      auto fill = [&](int b0, int b1) {
+        for (int c = b0; c < b1; ++c) memcpy(dst + (size_t)c * band, cube + ((size_t)c * H + r0) * W, band * 4);
+      };
+      std::vector<std::thread> th;
+      for (unsigned t = 1; t < nthr; ++t) th.emplace_back(fill, nb * t / nthr, nb * (t + 1) / nthr);
+      fill(0, nb / nthr);
+      for (auto& t : th) t.join();
+      // the strip buffer is free once the strip two before has run
+      if (k >= 2) HIP_TRY(hipStreamWaitEvent(D->copy, D->ev_done[b], 0));
+      HIP_TRY(hipMemcpyAsync(D->strip_in[b], dst, band * nb * 4, hipMemcpyHostToDevice, D->copy));
+      HIP_TRY(hipEventRecord(D->ev_free[b], D->copy));
+      HIP_TRY(hipEventRecord(D->ev_copied[b], D->copy));
+      HIP_TRY(hipStreamWaitEvent(s, D->ev_copied[b], 0));
+    } else {
+      HIP_TRY(hipMemcpy2DAsync(D->strip_in[b], band * 4, cube + (size_t)r0 * W, (size_t)H * W * 4, band * 4, nb,
+                               hipMemcpyDeviceToDevice, s));
+    }
+    if ((rc = run_scene_rows(m, D->strip_in[b], rows, W, D->strip_out[b], P, 0, nr, s))) return rc;
+    HIP_TRY(hipMemcpy2DAsync(map + (size_t)r0 * W, (size_t)H * W * 4, D->strip_out[b], band * 4, band * 4, ncls,
+                             host_map ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipEventRecord(D->ev_done[b], s));
   }
-  HIP_TRY(hipMemcpyAsync(map, D->stage_out, (size_t)ncls * H * W * 4, hipMemcpyDeviceToHost, D->stream));
-  HIP_TRY(hipStreamSynchronize(D->stream));
+  if (host_map) HIP_TRY(hipStreamSynchronize(s));
   return BNN_OK;
+}
+
+// Host cube -> host map, strip by strip.
+int run_scene_host(const Model* m, const float* cube, int H, int W, float* map, int P) {
+  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+  return run_scene_strips(m, cube, true, H, W, map, true, P, m->dev->stream);
 }
 
 int grow(float** p, size_t* cap, size_t bytes) {
@@ -1014,17 +1072,25 @@ int grow(float** p, size_t* cap, size_t bytes) {
   return BNN_OK;
 }
 
+// Host input -> host logits, in sub-batches of at most one launch each
+// (staging buffers of one sub-batch, so device memory stays bounded).
 int run_host(const Model* m, const float* input, int N, int H, int W, float* logits, Dumps* dmp) {
   int rc;
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
-  const size_t ib = (size_t)N * m->n_bands * H * W * 4, ob = (size_t)N * m->n_classes * H * W * 4;
-  if ((rc = grow(&D->stage_in, &D->stage_in_cap, ib))) return rc;
-  if ((rc = grow(&D->stage_out, &D->stage_out_cap, ob))) return rc;
-  HIP_TRY(hipMemcpyAsync(D->stage_in, input, ib, hipMemcpyHostToDevice, D->stream));
-  if ((rc = run_device(m, D->stage_in, N, H, W, D->stage_out, D->stream, dmp))) return rc;
-  HIP_TRY(hipMemcpyAsync(logits, D->stage_out, ob, hipMemcpyDeviceToHost, D->stream));
+  const int per = patches_per_launch(m, H, W);
+  if (N > per && dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes at most %d patches of %dx%d", per, H, W);
+  const int nc = std::min(N, per);
+  const size_t pin = (size_t)m->n_bands * H * W * 4, pout = (size_t)m->n_classes * H * W * 4;
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, pin * nc))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, pout * nc))) return rc;
+  for (int n0 = 0; n0 < N; n0 += nc) {
+    const int n = std::min(nc, N - n0);
+    HIP_TRY(hipMemcpyAsync(D->stage_in, (const char*)input + pin * n0, pin * n, hipMemcpyHostToDevice, D->stream));
+    if ((rc = run_device_launch(m, D->stage_in, n, H, W, D->stage_out, D->stream, dmp))) return rc;
+    HIP_TRY(hipMemcpyAsync((char*)logits + pout * n0, D->stage_out, pout * n, hipMemcpyDeviceToHost, D->stream));
+  }
   HIP_TRY(hipStreamSynchronize(D->stream));
   return BNN_OK;
 }
@@ -1120,7 +1186,10 @@ int bnn_forward_patched_device(const Model* m, const float* d_input, int H, int 
                                void* stream) {
   int rc;
   if ((rc = check_scene(m, H, W, P))) return rc;
-  return run_scene_rows(m, d_input, H, W, d_logits, P, 0, (H + P - 1) / P, (hipStream_t)stream);
+  // in place when the kernels can address the cube, else strip by strip
+  if (scene_in_place(m, H, W))
+    return run_scene_rows(m, d_input, H, W, d_logits, P, 0, (H + P - 1) / P, (hipStream_t)stream);
+  return run_scene_strips(m, d_input, false, H, W, d_logits, false, P, (hipStream_t)stream);
 }
 
 int bnn_forward_debug(const Model* m, const float* input, int N, int H, int W, float* logits, bnn_stage_cb cb,

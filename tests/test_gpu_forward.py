@@ -274,3 +274,26 @@ def test_default_stream_is_ordered(tmp_path):
         eng.forward_device(dx.data_ptr(), N, 32, 32, dy.data_ptr(), None)
         assert _same(dy.cpu().numpy(), want)
     eng.close()
+
+
+def test_batch_past_launch_limit(tmp_path):
+    """4400 patches, 2.16 GB of input: more than the 2 GiB one launch
+    addresses, so the batch runs as two launches (4369 + 31 patches), from
+    host pointers (bnn_forward_batch, staged one launch at a time) and from
+    device pointers (bnn_forward_device); both equal batches of 1024 bit
+    for bit."""
+    import torch
+    b = synth.make_blob(seed=13)
+    eng, _ = _engine(tmp_path, b)
+    N = 4400
+    x = synth.make_input(14, N)
+    assert x.nbytes >= 2 ** 31
+    small = np.concatenate([eng.forward_batch(x[i:i + 1024]) for i in range(0, N, 1024)])
+    assert _same(eng.forward_batch(x), small)
+    d_x = torch.from_numpy(x).cuda()
+    del x
+    d_o = torch.full((N, b.n_classes, 32, 32), float("nan"), device="cuda")
+    eng.forward_device(d_x.data_ptr(), N, 32, 32, d_o.data_ptr())
+    torch.cuda.synchronize()
+    assert _same(d_o.cpu().numpy(), small)
+    eng.close()

@@ -88,3 +88,49 @@ def test_scene_split_at_patch_rows(tmp_path, orc):
     assert _same(d_map.cpu().numpy(), want)
     assert _same(eng.forward_patched(cube, P), want)
     eng.close()
+
+
+def test_scene_cfg3_geometry(tmp_path, orc):
+    """Benchmark config 3 at its exact geometry: a 956 x 684 x 120 cube
+    (N(0,1) plus a per-band offset) cut into 30 x 22 = 660 patches of 32 x 32,
+    the last patch row and column zero past the scene, run as two parts of
+    whole patch rows.  Device and host-pointer maps against the checker's
+    per-patch forward, stitched."""
+    import torch
+    b = synth.make_blob(seed=0, base=16)
+    eng = _engine(tmp_path, b)
+    H, W, P = 956, 684, 32
+    assert scene.grid(H, W, P) == (30, 22)
+    cube = _cube(40, H, W)
+    want = scene.stitch(orc.parse(B.to_bytes(b)).forward_batch(scene.cut(cube, P)), H, W)
+    d_cube = torch.from_numpy(cube).cuda()
+    d_map = torch.full((3, H, W), float("nan"), device="cuda")
+    s = torch.cuda.Stream()
+    eng.forward_patched_device(d_cube.data_ptr(), H, W, d_map.data_ptr(), P, s.cuda_stream)
+    torch.cuda.synchronize()
+    assert _same(d_map.cpu().numpy(), want)
+    assert _same(eng.forward_patched(cube, P), want)
+    eng.close()
+
+
+def test_scene_past_launch_limit(tmp_path):
+    """A 2080 x 2160 x 120 cube, 2.16 GB: past what one launch addresses, so
+    both the host-pointer and the device-pointer scene calls run it in strips
+    of whole patch rows, each staged as its own sub-cube.  Their maps equal
+    the batch forward of the host-cut patches, stitched."""
+    import torch
+    b = synth.make_blob(seed=15)
+    eng = _engine(tmp_path, b)
+    H, W, P = 2080, 2160, 32
+    cube = _cube(16, H, W)
+    assert cube.nbytes >= 2 ** 31
+    want = scene.stitch(eng.forward_batch(scene.cut(cube, P)), H, W)
+    assert _same(eng.forward_patched(cube, P), want)
+    d_cube = torch.from_numpy(cube).cuda()
+    del cube
+    d_map = torch.full((3, H, W), float("nan"), device="cuda")
+    eng.forward_patched_device(d_cube.data_ptr(), H, W, d_map.data_ptr(), P,
+                               torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert _same(d_map.cpu().numpy(), want)
+    eng.close()
