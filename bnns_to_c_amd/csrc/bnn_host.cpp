@@ -311,7 +311,6 @@ int validate(const Model* m, const StemPart* st = nullptr) {
     c = c2.Cout;
   }
   if (m->head_Cin != c || m->head_Cout != m->n_classes) return set_err(BNN_EBLOB, "head does not chain");
-  if (c > 32) return set_err(BNN_EBLOB, "head input width %d > 32 is not supported by the fused head", c);
   return BNN_OK;
 }
 
@@ -812,6 +811,20 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     if ((rc = bconv(D->d1[i], EPI_FOLD, w.skip[lvl], x, lvl, xl, w.d1[i], nullptr, nullptr, dec_c1[i]))) return rc;
     if (i < 3) {
       if ((rc = bconv(D->d2[i], EPI_FOLD, w.d1[i], nullptr, lvl, 0, w.d2[i], nullptr, nullptr, dec_c2[i]))) return rc;
+    } else if (D->d2[i].cout > 32) {
+      // a head over more than 32 channels: dec1.conv2's bits, then the head
+      // on its own (one epilogue group holds at most 32 channels)
+      if ((rc = bconv(D->d2[i], EPI_FOLD, w.d1[i], nullptr, lvl, 0, w.d2[i], nullptr, nullptr, dec_c2[i]))) return rc;
+      HeadArgs h{};
+      h.bits = at(w.d2[i], 0, words(D->d2[i].cout));
+      h.cw = words(D->d2[i].cout);
+      h.cin = D->d2[i].cout;
+      h.hw = D->hw; h.hb = D->hb; h.ncls = D->ncls;
+      h.N = cnt; h.H = H; h.W = W;
+      h.logits = sc ? d_logits : d_logits + (size_t)nb * D->ncls * H * W;
+      if (sc) { h.sH = sc->sH; h.sW = sc->sW; h.pcols = sc->pcols; h.prow0 = sc->prow0 + nb / sc->pcols; }
+      HIP_TRY(launch_head_sep(h, st));
+      if ((rc = mark("head", "head", (double)N * D->ncls * H * W, (double)h.cin))) return rc;
     } else {
       if ((rc = bconv(D->d2[i], EPI_HEAD, w.d1[i], nullptr, lvl, 0, dump ? w.d2[i] : nullptr, nullptr, d_logits,
                       dec_c2[i])))

@@ -347,6 +347,25 @@ hipError_t launch_fold_int(const int32_t* P, int8_t* out, int C, int HW,
 hipError_t launch_fold_real(const float* x, int8_t* out, int C, int HW, const float* A,
                             const float* B, const float* slope, const float* rsign,
                             hipStream_t s);
+// The 1x1 head as its own kernel (heads over more than 32 channels, which
+// one epilogue group cannot hold): input the head layer's packed bits
+// [N][H][W][cw] read as +-1 (v1), or its float planes (v3: element
+// (c, n, y, x) at c * plane + (n * H + y) * W + x, bits null).
+struct HeadArgs {
+  const uint32_t* bits;
+  int cw;
+  const float* planes;
+  size_t plane;
+  int cin;
+  const float* hw;  // [ncls][cin]
+  const float* hb;  // [ncls]
+  int ncls;
+  float* logits;    // [N][ncls][H][W], or the scene map [ncls][sH][sW]
+  int N, H, W;
+  int sH, sW, pcols, prow0;  // scene mode (pcols > 0), as in RealArgs
+};
+hipError_t launch_head_sep(const HeadArgs& a, hipStream_t s);
+
 hipError_t launch_head(const float* a, const float* W, const float* b, float* out,
                        int cin, int HW, int cout, hipStream_t s);
 

@@ -2092,6 +2092,46 @@ __global__ void k_head(const float* __restrict__ a, const float* __restrict__ W,
 
 inline unsigned blocks_for(long n, int bs = kBlock) { return (unsigned)((n + bs - 1) / bs); }
 
+// One pixel per lane: per class the bias, then one fused step per input
+// channel in order (csrc/bnn_head.c:21-34; csrc/bnn_react_opt.c:23-44, whose
+// x86 build contracts lo[p] += w * a[p] to one fma).  The weights come
+// through the constant address space (uniform scalar loads).
+template <bool BITS>
+__global__ __launch_bounds__(kBlock) void k_head_sep(const HeadArgs a) {
+  const long i = (long)blockIdx.x * kBlock + threadIdx.x;
+  const long HW = (long)a.H * a.W;
+  if (i >= (long)a.N * HW) return;
+  const int n = (int)(i / HW);
+  const long p = i - (long)n * HW;
+  const int y = (int)(p / a.W), x = (int)(p - (long)y * a.W);
+  size_t lbase = (size_t)n * a.ncls * HW + p, lstride = HW;
+  if (a.pcols > 0) {
+    const int pr = a.prow0 + n / a.pcols, pc = n % a.pcols;
+    const int sy = pr * a.H + y, sx = pc * a.W + x;
+    if (sy >= a.sH || sx >= a.sW) return;
+    lbase = (size_t)sy * a.sW + sx;
+    lstride = (size_t)a.sH * a.sW;
+  }
+  typedef const __attribute__((address_space(4))) float* const_hf;
+  const const_hf hw = (const_hf)a.hw, hb = (const_hf)a.hb;
+  const uint32_t* bw = BITS ? a.bits + i * a.cw : nullptr;
+#pragma unroll 1
+  for (int o = 0; o < a.ncls; ++o) {
+    float acc = hb[o];
+#pragma unroll 1
+    for (int c0 = 0; c0 < a.cin; c0 += 32) {
+      const uint32_t word = BITS ? bw[c0 >> 5] : 0u;
+      const int cn = min(32, a.cin - c0);
+#pragma unroll 4
+      for (int k = 0; k < cn; ++k) {
+        const float v = BITS ? (((word >> k) & 1u) ? 1.0f : -1.0f) : a.planes[(size_t)(c0 + k) * a.plane + i];
+        acc = __fmaf_rn(hw[o * a.cin + c0 + k], v, acc);
+      }
+    }
+    a.logits[lbase + (size_t)o * lstride] = acc;
+  }
+}
+
 template <int MT, int COG, int EPI, bool DUMP>
 hipError_t go_bconv(BconvArgs a, hipStream_t s) {
   const uint32_t tH = (uint32_t)(a.H + MT - 1) / MT, tW = (uint32_t)(a.W + MT - 1) / MT;
@@ -2441,6 +2481,15 @@ hipError_t launch_fold_real(const float* x, int8_t* out, int C, int HW, const fl
   const long n = (long)C * HW;
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_fold_real, dim3(blocks_for(n)), dim3(kBlock), 0, s, x, out, C, HW, A, B, slope, rsign);
+  return hipGetLastError();
+}
+
+hipError_t launch_head_sep(const HeadArgs& a, hipStream_t s) {
+  const long n = (long)a.N * a.H * a.W;
+  if (n <= 0) return hipSuccess;
+  if (a.bits ? a.cw != (a.cin + 31) / 32 : !a.planes) return hipErrorInvalidValue;
+  if (a.bits) hipLaunchKernelGGL(k_head_sep<true>, dim3(blocks_for(n)), dim3(kBlock), 0, s, a);
+  else hipLaunchKernelGGL(k_head_sep<false>, dim3(blocks_for(n)), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 

@@ -217,7 +217,6 @@ int validate(const ModelR* m) {
   if (m->head_Cin != prev || m->head_Cout != m->n_classes)
     return set_err(BNN_EBLOB, "head %dx%d does not match dec1 (%d) / n_classes (%d)", m->head_Cout, m->head_Cin,
                    prev, m->n_classes);
-  if (prev > 32) return set_err(BNN_EBLOB, "dec1 width %d: the fused head takes at most 32 channels", prev);
   if (m->n_bands <= 0 || m->n_classes <= 0) return set_err(BNN_EBLOB, "bad n_bands / n_classes");
   return BNN_OK;
 }
@@ -608,10 +607,26 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
       if ((rc = bconv(k, 2, EPI_RX, w.a2[k], nullptr, 0, w.h1[k], L.ea, D->blk[k + 1].t1b, w.h2[k], w.upb[k],
                       nullptr, nullptr, nullptr, nullptr)))
         return rc;
-    } else {
+    } else if (block_of(m, k).conv2.Cout <= 32) {
       if ((rc = bconv(k, 2, EPI_RXHEAD, w.a2[k], nullptr, 0, w.h1[k], L.ea, nullptr, dump ? w.h2[k] : nullptr,
                       nullptr, nullptr, nullptr, nullptr, nullptr)))
         return rc;
+    } else {
+      // a head over more than 32 channels: dec1's h2 planes, then the head
+      // on its own (one epilogue group holds at most 32 channels)
+      if ((rc = bconv(k, 2, EPI_RX, w.a2[k], nullptr, 0, w.h1[k], L.ea, nullptr, w.h2[k], nullptr, nullptr,
+                      nullptr, nullptr, nullptr)))
+        return rc;
+      HeadArgs h{};
+      h.planes = pl(w.h2[k], 0);
+      h.plane = (size_t)N * H * W;
+      h.cin = block_of(m, k).conv2.Cout;
+      h.hw = D->hw; h.hb = D->hb; h.ncls = D->ncls;
+      h.N = cnt; h.H = H; h.W = W;
+      h.logits = (d_logits && !sc) ? d_logits + (size_t)nb * D->ncls * H * W : d_logits;
+      if (sc) { h.sH = sc->sH; h.sW = sc->sW; h.pcols = sc->pcols; h.prow0 = sc->prow0 + nb / sc->pcols; }
+      HIP_TRY(launch_head_sep(h, st));
+      if ((rc = mark("head", "head", (double)N * D->ncls * H * W, (double)h.cin))) return rc;
     }
   }
   return BNN_OK;

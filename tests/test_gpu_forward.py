@@ -40,6 +40,8 @@ def _same(a, b):
     (7, 8, True, 2, 16, 16),
     (9, 32, False, 2, 32, 32),
     (12, 16, False, 1, 47, 33),
+    (13, 48, False, 2, 32, 32),   # head over 48 channels: dec1.conv2 then the separate head kernel
+    (14, 64, True, 1, 30, 34),    # head over 64 channels, odd sizes
 ])
 def test_stages_vs_checker(tmp_path, orc, seed, base, cov, N, H, W):
     b = synth.make_blob(seed=seed, base=base, coverage=cov)

@@ -66,6 +66,7 @@ def _check_stages(eng, model, x):
     (4, 16, 7, False, 2, 33, 47),
     (5, 8, 1, False, 1, 16, 16),      # one band
     (6, 16, 121, True, 1, 80, 36),    # taller than the reference's 64-row strips
+    (7, 48, 120, False, 1, 32, 32),   # head over 48 channels: dec1 then the separate head kernel
 ])
 def test_react_stages_vs_checker(tmp_path, rorc, seed, base, nb, cov, N, H, W):
     b = synth.make_blob_react(seed=seed, base=base, n_bands=nb, coverage=cov)

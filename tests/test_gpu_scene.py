@@ -29,7 +29,8 @@ def _cube(seed, H, W, nb=120):
     return (rng.standard_normal((nb, H, W), dtype=np.float32) + off).astype(np.float32)
 
 
-@pytest.mark.parametrize("seed,base,H,W,P", [(0, 16, 70, 100, 32), (4, 8, 40, 33, 16), (8, 16, 64, 64, 32)])
+@pytest.mark.parametrize("seed,base,H,W,P", [(0, 16, 70, 100, 32), (4, 8, 40, 33, 16), (8, 16, 64, 64, 32),
+                                             (9, 48, 50, 40, 32)])  # a 48-channel head writes the map
 def test_scene_vs_checker(tmp_path, orc, seed, base, H, W, P):
     b = synth.make_blob(seed=seed, base=base)
     eng = _engine(tmp_path, b)
