@@ -64,6 +64,7 @@ struct BconvArgs {
   int N, H, W;
   int cin, cout;        // true channel counts
   uint32_t ntiles;      // N * tiles per patch (set by launch_bconv)
+  int xorder;           // XCD-aware block order (set by launch_bconv)
   FastDiv dper, dtw;    // tiles per patch, tiles per row (set by launch_bconv)
   const uint32_t* wt;   // [cw0+cw1][cout][9], or (pair) [cout][5] then [cw1][cout][9]
   // a first segment (plain input, or a concat's skip part) of at most 16

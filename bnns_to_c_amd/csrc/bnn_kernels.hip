@@ -1332,7 +1332,32 @@ __device__ __forceinline__ void head_logits(const float* hw_, const float* hb_, 
 template <int MT, int COG, int EPI, bool DUMP>
 __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t bytes0, uint32_t bytes1) {
   constexpr int NP = MT + 2;
-  uint32_t tile = blockIdx.x * kBlock + threadIdx.x;
+  // Block order.  Plain: group g of tile block t is block g * ntb + t.
+  // XCD-aware (a.xorder, for outputs of two or more words per pixel):
+  // consecutive blocks go to the 8 XCDs in turn, so block b runs on XCD
+  // b % 8, and its index j = b / 8 there walks (tile block, channel group)
+  // with the group fastest, tile block (j / ngroups) * 8 + b % 8.  Every
+  // group of a tile block then runs on one XCD, one after the other, and
+  // the pieces of a pixel's output words they write merge in that XCD's L2:
+  // in the plain order they left L2 as separate partial writes, 8x the
+  // output bytes for 128 channels in groups of 16.  (Tile blocks are padded
+  // to a multiple of 8; a tile past the end is inactive.)  With one output
+  // word per pixel the plain order is kept: there the groups' byte stores
+  // to the same words at the same moment measured slower.
+  const uint32_t ngroups = (uint32_t)(a.cout + COG - 1) / COG;
+  uint32_t gidx, tile;
+  if (a.xorder) {
+    const uint32_t xj = blockIdx.x >> 3;
+    gidx = xj % ngroups;
+    tile = ((xj / ngroups) * 8u + (blockIdx.x & 7u)) * kBlock + threadIdx.x;
+  } else if (ngroups == 1) {
+    gidx = 0;
+    tile = blockIdx.x * kBlock + threadIdx.x;
+  } else {
+    const uint32_t ntb = (a.ntiles + kBlock - 1) / kBlock;
+    gidx = blockIdx.x / ntb;
+    tile = (blockIdx.x - gidx * ntb) * kBlock + threadIdx.x;
+  }
   const bool active = tile < a.ntiles;
   if (!active) tile = a.ntiles - 1;
   const uint32_t n = fdiv(tile, a.dper);
@@ -1340,7 +1365,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
   const uint32_t ty = fdiv(rr, a.dtw);
   const uint32_t tx = rr - ty * a.dtw.d;
   const int y0 = (int)ty * MT, x0 = (int)tx * MT;
-  const int co0 = blockIdx.y * COG;
+  const int co0 = (int)gidx * COG;
   const int coutp = (a.cout + 31) & ~31;  // weight rows are padded to 32
 
   // The (MT+2)^2 window around the tile: a row or column outside the image
@@ -1446,7 +1471,7 @@ __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t by
   if (EPI == EPI_P) return;
 
   // bytes of the pixel's words the last channel group zero-fills
-  const int zero_end = blockIdx.y == gridDim.y - 1 ? a.cwo * 4 : 0;
+  const int zero_end = gidx == ngroups - 1 ? a.cwo * 4 : 0;
 
   if constexpr (EPI == EPI_RX || EPI == EPI_RXPOOL || EPI == EPI_RXHEAD) {
     // h = RPReLU(fma(A, P, B + move1) + res): the fused step and the two
@@ -2147,8 +2172,11 @@ hipError_t go_bconv(BconvArgs a, hipStream_t s) {
   const uint32_t b1 = a.in1 ? (uint32_t)((size_t)(nrel * a.h1 * a.w1 + (a.padoff != 0x80000000u ? 1 : 0)) *
                                          a.cw1 * 4)
                             : 0u;
-  hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3(blocks_for((long)ntiles), groups), dim3(kBlock), 0, s,
-                     a, b0, b1);
+  a.xorder = (a.cwo >= 2 && groups > 1 && EPI != EPI_P) ? 1 : 0;
+  const uint64_t nblocks = (uint64_t)(a.xorder ? (blocks_for((long)ntiles) + 7) & ~7u : blocks_for((long)ntiles)) *
+                           groups;
+  if (nblocks >= 0x80000000ull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_bconv<MT, COG, EPI, DUMP>), dim3((unsigned)nblocks), dim3(kBlock), 0, s, a, b0, b1);
   return hipGetLastError();
 }
 
