@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdio>
@@ -374,7 +375,18 @@ struct DevBconv {
   MfmaConv mc{};  // int8 matrix-core tables when cout % 64 == 0 (mc.w null otherwise)
   int mfma = 0;   // mfma_conv_mode() at creation
   int pair = 0;   // cin <= 16, no concat: wt holds tap pairs, 5 words per channel
+  uint32_t* mw = nullptr;  // the fused middle's table [words][channel group][9][64] (mid layers only)
 };
+
+// The fused middle (launch_mid) replaces the ten convs from enc3.c1 to
+// dec3.c2 for patches whose level 2 is 8 x 8.  By default it is taken when
+// each layer's work fits a block's four waves in one or two passes (at most
+// 64 output channels at 8 x 8, 128 at 4 x 4, 256 at 2 x 2: the reference's
+// base width 16 and below); BNN_MID=0 keeps the per-layer kernels.
+bool mid_mode() {
+  const char* e = getenv("BNN_MID");
+  return !(e && !strcmp(e, "0"));
+}
 
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
   return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || mfma_nchunk(L.cw0, L.cw1) >= 4);
@@ -399,6 +411,7 @@ struct BnnDevice {
   uint64_t* rwm = nullptr;  // lane-mask weights (v1: all signs +-1, else null and rw is used)
   float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
+  bool mid = false;  // the fused middle applies (mid_fits at load, and mid_mode())
   float *hw = nullptr, *hb = nullptr;
   int ncls = 0;
   Workspace ws;
@@ -460,7 +473,9 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
   if (L->pair) wt = pair_taps(wt, c.Cout);
   int rc;
   if ((rc = dev_upload(D, &L->wt, wt.data(), wt.size()))) return rc;
-  const int coutp = pad32(c.Cout);
+  // rules padded to 64 channels (width 0 past cout): the fused middle reads
+  // one per lane of a 64-channel group
+  const int coutp = (c.Cout + 63) & ~63;
   if (a1 && (rc = upload_fold(D, &L->f1, *a1, coutp))) return rc;
   if (a2 && (rc = upload_fold(D, &L->f2, *a2, coutp))) return rc;
   L->mfma = mfma_conv_mode();
@@ -475,6 +490,39 @@ int upload_bconv(BnnDevice* D, DevBconv* L, const Conv& c, int cs, const Act* a1
     L->mc = MfmaConv{dw, ds, mfma_npair(L->cw0, L->cw1)};
   }
   return BNN_OK;
+}
+
+// the fused middle's weight table: repack_bin's [word][coutp32][tap] as
+// [word][channel group of 64][tap][64], zero past cout, so that the 64 lanes
+// of a group read consecutive words for one tap and the taps lie at fixed
+// distances
+int upload_mid_w(BnnDevice* D, DevBconv* L, const Conv& c, int cs) {
+  const std::vector<uint32_t> wt = repack_bin(c.packed, c.Cin, c.Cout, 9, cs);
+  const int nwd = L->cw0 + L->cw1, cp32 = pad32(c.Cout), ncg = (c.Cout + 63) / 64;
+  std::vector<uint32_t> mw((size_t)nwd * ncg * 9 * 64, 0u);
+  for (int w = 0; w < nwd; ++w)
+    for (int co = 0; co < c.Cout; ++co)
+      for (int t = 0; t < 9; ++t)
+        mw[(((size_t)w * ncg + co / 64) * 9 + t) * 64 + co % 64] = wt[((size_t)w * cp32 + co) * 9 + t];
+  return dev_upload(D, &L->mw, mw.data(), mw.size());
+}
+
+// the ten layers of the fused middle, in its order
+std::array<DevBconv*, kMidLayers> mid_layers(BnnDevice* D) {
+  return {&D->e1[2], &D->e2[2], &D->e1[3], &D->e2[3], &D->b1, &D->b2, &D->d1[0], &D->d2[0], &D->d1[1], &D->d2[1]};
+}
+
+// Whether the fused middle takes this model: widths within one or two
+// passes of a block's waves per layer, and the concat layers' word split
+// matching the tensors the kernel holds (skip words, then upsampled words).
+bool mid_fits(BnnDevice* D) {
+  const auto L = mid_layers(D);
+  // 8 x 8 layers, 4 x 4, 2 x 2, 4 x 4, 8 x 8
+  static const int cap[kMidLayers] = {64, 64, 128, 128, 256, 256, 128, 128, 64, 64};
+  for (int l = 0; l < kMidLayers; ++l)
+    if (L[l]->cout > cap[l]) return false;
+  return D->d1[0].cw0 == words(D->e2[3].cout) && D->d1[0].cw1 == words(D->b2.cout) &&
+         D->d1[1].cw0 == words(D->e2[2].cout) && D->d1[1].cw1 == words(D->d2[0].cout);
 }
 
 // real conv weights.  v2 stem: lane masks of the 1x1 matrix-core kernel
@@ -598,6 +646,15 @@ int build_device(Model* m, const StemPart* st = nullptr) {
     const int cs = m->enc_conv2[3 - i].Cout;
     if ((rc = upload_bconv(D, &D->d1[i], m->dec_conv1[i], cs, &m->dec_act1[i], nullptr))) return rc;
     if ((rc = upload_bconv(D, &D->d2[i], m->dec_conv2[i], 0, &m->dec_act2[i], nullptr))) return rc;
+  }
+  D->mid = mid_mode() && mid_fits(D);
+  if (D->mid) {
+    const auto L = mid_layers(D);
+    const Conv* cv[kMidLayers] = {&m->enc_conv1[2], &m->enc_conv2[2], &m->enc_conv1[3], &m->enc_conv2[3],
+                                  &m->bott_conv1,   &m->bott_conv2,   &m->dec_conv1[0],  &m->dec_conv2[0],
+                                  &m->dec_conv1[1], &m->dec_conv2[1]};
+    for (int l = 0; l < kMidLayers; ++l)
+      if ((rc = upload_mid_w(D, L[l], *cv[l], L[l]->cs))) return rc;
   }
   D->ncls = m->head_Cout;
   if ((rc = dev_upload(D, &D->hw, m->head_W, (size_t)m->head_Cout * m->head_Cin))) return rc;
@@ -786,6 +843,48 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     return mark(label, ot, (double)N * L.cout * a.H * a.W, (double)L.cin * 9);
   };
 
+  // enc3.c1 .. dec3.c2 as one kernel (level 2 is 8 x 8): input enc2's
+  // pooled bits, output dec3.c2's bits; the debug forward takes every
+  // intermediate tensor and P as the per-layer kernels would
+  const bool use_mid = D->mid && hs[2] == 8 && wsz[2] == 8;
+  auto mid = [&]() -> int {
+    const auto L = mid_layers(D);
+    uint32_t* T[kMidTensors] = {w.down[1], w.h[2], w.skip[2], w.down[2], w.h[3], w.skip[3], w.down[3],
+                                w.b1,      w.b2,   w.d1[0],   w.d2[0],   w.d1[1], w.d2[1]};
+    static const int lvl[kMidTensors] = {2, 2, 2, 3, 3, 3, 4, 4, 4, 3, 3, 2, 2};
+    const int cw[kMidTensors] = {words(D->e2[1].cout), words(L[0]->cout), words(L[1]->cout), words(L[1]->cout),
+                                 words(L[2]->cout),    words(L[3]->cout), words(L[3]->cout), words(L[4]->cout),
+                                 words(L[5]->cout),    words(L[6]->cout), words(L[7]->cout), words(L[8]->cout),
+                                 words(L[9]->cout)};
+    MidArgs a{};
+    double work = 0;
+    for (int l = 0; l < kMidLayers; ++l) {
+      MidLayer& ml = a.L[l];
+      ml.w = L[l]->mw;
+      ml.lo = L[l]->f1.lo; ml.wid = L[l]->f1.wid;
+      ml.lo2 = L[l]->f2.lo; ml.wid2 = L[l]->f2.wid;
+      ml.cin = L[l]->cin; ml.cout = L[l]->cout;
+      if (dump) {
+        ml.P = dmp->P[pi++];
+        if (l == 1 || l == 3) ml.P2 = dmp->P2[l == 1 ? 2 : 3];
+      }
+    }
+    int off = 0;
+    for (int i = 0; i < kMidTensors; ++i) {
+      a.t[i] = const_cast<uint32_t*>(at(T[i], lvl[i], cw[i]));
+      a.dim[i] = hs[lvl[i]];
+      a.cw[i] = cw[i];
+      a.off[i] = off;
+      off += hs[lvl[i]] * wsz[lvl[i]] * cw[i];
+    }
+    static const int d[kMidLayers] = {8, 8, 4, 4, 2, 2, 4, 4, 8, 8};
+    for (int l = 0; l < kMidLayers; ++l) work += (double)N * L[l]->cout * d[l] * d[l] * L[l]->cin * 9;
+    a.N = cnt;
+    a.ldsw = off;
+    HIP_TRY(launch_mid(a, dump, st));
+    return mark("enc3-dec3", "bconv_mid", work, 1.0);
+  };
+
   static const char* enc_c1[4] = {"enc1.c1", "enc2.c1", "enc3.c1", "enc4.c1"};
   static const char* enc_c2[4] = {"enc1.c2", "enc2.c2", "enc3.c2", "enc4.c2"};
   static const char* dec_c1[4] = {"dec4.c1", "dec3.c1", "dec2.c1", "dec1.c1"};
@@ -793,7 +892,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   auto part = [&]() -> int {
   if ((rc = first_conv())) return rc;
   const uint32_t* x = w.a1;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < (use_mid ? 2 : 4); ++i) {
     const uint32_t* hin = x;
     if (i || D->stem) {
       if ((rc = bconv(D->e1[i], EPI_FOLD, x, nullptr, i, 0, w.h[i], nullptr, nullptr, enc_c1[i]))) return rc;
@@ -802,11 +901,18 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     if ((rc = bconv(D->e2[i], EPI_POOL, hin, nullptr, i, 0, w.skip[i], w.down[i], nullptr, enc_c2[i]))) return rc;
     x = w.down[i];
   }
-  if ((rc = bconv(D->b1, EPI_FOLD, x, nullptr, 4, 0, w.b1, nullptr, nullptr, "bott.c1"))) return rc;
-  if ((rc = bconv(D->b2, EPI_FOLD, w.b1, nullptr, 4, 0, w.b2, nullptr, nullptr, "bott.c2"))) return rc;
-  x = w.b2;
-  int xl = 4;
-  for (int i = 0; i < 4; ++i) {
+  int xl = 4, i0 = 0;
+  if (use_mid) {
+    if ((rc = mid())) return rc;
+    x = w.d2[1];
+    xl = 2;
+    i0 = 2;
+  } else {
+    if ((rc = bconv(D->b1, EPI_FOLD, x, nullptr, 4, 0, w.b1, nullptr, nullptr, "bott.c1"))) return rc;
+    if ((rc = bconv(D->b2, EPI_FOLD, w.b1, nullptr, 4, 0, w.b2, nullptr, nullptr, "bott.c2"))) return rc;
+    x = w.b2;
+  }
+  for (int i = i0; i < 4; ++i) {
     const int lvl = 3 - i;
     if ((rc = bconv(D->d1[i], EPI_FOLD, w.skip[lvl], x, lvl, xl, w.d1[i], nullptr, nullptr, dec_c1[i]))) return rc;
     if (i < 3) {

@@ -348,6 +348,37 @@ hipError_t launch_fold_int(const int32_t* P, int8_t* out, int C, int HW,
 hipError_t launch_fold_real(const float* x, int8_t* out, int C, int HW, const float* A,
                             const float* B, const float* slope, const float* rsign,
                             hipStream_t s);
+// The middle of the v1 UNet for patches whose level 2 is 8 x 8 (32-35 px):
+// enc3.c1, enc3.c2 (+pool), enc4.c1, enc4.c2 (+pool), bott.c1, bott.c2,
+// dec4.c1 (concat), dec4.c2, dec3.c1 (concat), dec3.c2 in one kernel, one
+// block per patch (bnn_mid.hip).  Per layer: weights [words][9 taps][coutp]
+// (coutp = cout rounded up to 64, zero past cout; a concat's words are the
+// skip's, then the upsampled tensor's), the fold as canonical intervals
+// (lo, wid) padded to coutp with wid 0, the pool layers' second rule, and
+// the P dumps of the debug forward.
+constexpr int kMidLayers = 10, kMidTensors = 13;
+struct MidLayer {
+  const uint32_t* w;
+  const int32_t* lo;
+  const uint32_t* wid;
+  const int32_t* lo2;
+  const uint32_t* wid2;
+  int cin, cout;
+  int32_t* P;   // [N][cout][d][d] (debug forward)
+  int32_t* P2;  // pooled P (debug forward, pool layers)
+};
+// Tensors, [N][d][d][cw] words each: 0 enc2 pooled bits (input), 1 enc3.c1,
+// 2 enc3 skip, 3 enc3 down, 4 enc4.c1, 5 enc4 skip, 6 enc4 down, 7 bott.c1,
+// 8 bott.c2, 9 dec4.c1, 10 dec4.c2, 11 dec3.c1, 12 dec3.c2 (output).  off: a
+// tensor's word offset in the block's LDS (one patch), ldsw the total.
+struct MidArgs {
+  MidLayer L[kMidLayers];
+  uint32_t* t[kMidTensors];
+  int off[kMidTensors], dim[kMidTensors], cw[kMidTensors];
+  int N, ldsw;
+};
+hipError_t launch_mid(const MidArgs& a, bool dump, hipStream_t s);
+
 // The 1x1 head as its own kernel (heads over more than 32 channels, which
 // one epilogue group cannot hold): input the head layer's packed bits
 // [N][H][W][cw] read as +-1 (v1), or its float planes (v3: element

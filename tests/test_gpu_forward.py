@@ -42,6 +42,7 @@ def _same(a, b):
     (12, 16, False, 1, 47, 33),
     (13, 48, False, 2, 32, 32),   # head over 48 channels: dec1.conv2 then the separate head kernel
     (14, 64, True, 1, 30, 34),    # head over 64 channels, odd sizes
+    (15, 8, True, 2, 33, 35),     # fused middle at base 8 (enc3 of 32 channels), level 2 of 8 x 8
 ])
 def test_stages_vs_checker(tmp_path, orc, seed, base, cov, N, H, W):
     b = synth.make_blob(seed=seed, base=base, coverage=cov)
@@ -299,3 +300,36 @@ def test_batch_past_launch_limit(tmp_path):
     torch.cuda.synchronize()
     assert _same(d_o.cpu().numpy(), small)
     eng.close()
+
+
+def _ops(eng, x):
+    E.prof_reset()
+    E.prof_enable(True)
+    try:
+        eng.forward_batch(x)
+    finally:
+        E.prof_enable(False)
+    return {lab: op for lab, op, _ms, _w in E.prof_records()}
+
+
+@pytest.mark.parametrize("base,H,W,fused", [(16, 32, 32, True), (8, 35, 32, True), (16, 28, 32, False),
+                                            (32, 32, 32, False)])
+def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, fused):
+    """enc3.c1 .. dec3.c2 run as one kernel when level 2 is 8 x 8 and the
+    widths fit (base <= 16); BNN_MID=0 keeps the per-layer kernels, with
+    the same logits bit for bit."""
+    b = synth.make_blob(seed=40 + base, base=base)
+    x = synth.make_input(41, 37, 120, H, W)
+    monkeypatch.delenv("BNN_MID", raising=False)
+    eng, _ = _engine(tmp_path, b)
+    ops = _ops(eng, x)
+    assert ("enc3-dec3" in ops) == fused, ops
+    assert ("bott.c1" in ops) == (not fused), ops
+    got = eng.forward_batch(x)
+    eng.close()
+    monkeypatch.setenv("BNN_MID", "0")
+    eng, _ = _engine(tmp_path, b, "m0.blob")
+    assert "enc3-dec3" not in _ops(eng, x)
+    want = eng.forward_batch(x)
+    eng.close()
+    assert _same(got, want)

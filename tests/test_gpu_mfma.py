@@ -64,6 +64,7 @@ def _check_stages(eng, model, x):
 ])
 def test_forced_mfma_stages_vs_checker(tmp_path, orc, monkeypatch, seed, base, N, H, W):
     monkeypatch.setenv("BNN_BCONV_MFMA", "2")
+    monkeypatch.setenv("BNN_MID", "0")  # the fused middle would take base 16's matrix-core layers
     b = synth.make_blob(seed=seed, base=base)
     p = tmp_path / "m.blob"
     p.write_bytes(B.to_bytes(b))
