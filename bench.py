@@ -248,6 +248,8 @@ def main() -> int:
     ap.add_argument("--settle", type=int, default=120,
                     help="untimed forwards before the warmup steps, for the GPU clocks to settle")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="the headline forward and its per-kernel pass only (for profiler runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -279,226 +281,227 @@ def main() -> int:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-    # benchmark config 1: the isolated binary conv, 64->64 at 64x64, batch
-    # 256, int32 P out (268 MB, the accumulator the reference's bconv
-    # returns)
-    N1, S1, C1 = 256, 64, 64
-    a1 = synth.make_bits(20, N1, S1, S1, C1)
-    L1 = engine.ConvLayer(blob.pack_kidx(synth.make_signs(21, C1, C1)), C1, C1)
-    da1 = torch.from_numpy(a1).cuda()
-    act1 = torch.empty((N1, S1, S1, C1 // 32), dtype=torch.int32, device="cuda")
-    engine.pack_act_device(da1.data_ptr(), act1.data_ptr(), N1, C1, S1, S1, sp)
-    del da1
-    P1 = torch.empty((N1, C1, S1, S1), dtype=torch.int32, device="cuda")
-    settle(lambda: L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp), torch)
-    for _ in range(3):
-        L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(20):
-        L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    c1_ms = e0.elapsed_time(e1) / 20
-    c1_bitmacs = N1 * C1 * S1 * S1 * C1 * 9
-    c1_rate = 2 * c1_bitmacs / (c1_ms / 1e3)
-    c1_bytes = N1 * S1 * S1 * (C1 // 8) + P1.numel() * 4  # packed bits in, int32 P out
-    log(f"cfg1 bconv 64->64 64x64 b{N1}, int32 P out: {c1_ms * 1e3:.1f} us, frac {c1_rate / valu_binop_peak():.3f} "
-        f"of VALU popcount peak, {c1_bytes / (c1_ms / 1e3) / 1e9:.0f} GB/s of algorithmic HBM bytes")
-    L1.close()
-    del act1, P1
+    if not args.headline_only:
+        # benchmark config 1: the isolated binary conv, 64->64 at 64x64, batch
+        # 256, int32 P out (268 MB, the accumulator the reference's bconv
+        # returns)
+        N1, S1, C1 = 256, 64, 64
+        a1 = synth.make_bits(20, N1, S1, S1, C1)
+        L1 = engine.ConvLayer(blob.pack_kidx(synth.make_signs(21, C1, C1)), C1, C1)
+        da1 = torch.from_numpy(a1).cuda()
+        act1 = torch.empty((N1, S1, S1, C1 // 32), dtype=torch.int32, device="cuda")
+        engine.pack_act_device(da1.data_ptr(), act1.data_ptr(), N1, C1, S1, S1, sp)
+        del da1
+        P1 = torch.empty((N1, C1, S1, S1), dtype=torch.int32, device="cuda")
+        settle(lambda: L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp), torch)
+        for _ in range(3):
+            L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(20):
+            L1.P_device(act1.data_ptr(), N1, S1, S1, P1.data_ptr(), sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        c1_ms = e0.elapsed_time(e1) / 20
+        c1_bitmacs = N1 * C1 * S1 * S1 * C1 * 9
+        c1_rate = 2 * c1_bitmacs / (c1_ms / 1e3)
+        c1_bytes = N1 * S1 * S1 * (C1 // 8) + P1.numel() * 4  # packed bits in, int32 P out
+        log(f"cfg1 bconv 64->64 64x64 b{N1}, int32 P out: {c1_ms * 1e3:.1f} us, frac {c1_rate / valu_binop_peak():.3f} "
+            f"of VALU popcount peak, {c1_bytes / (c1_ms / 1e3) / 1e9:.0f} GB/s of algorithmic HBM bytes")
+        L1.close()
+        del act1, P1
 
-    # fused bconv + fold + 2x2 max-pool, 128->128 at 32x32, batch 1024
-    C = 128
-    a = synth.make_bits(30, N, H, W, C)
-    w = synth.make_signs(31, C, C)
-    L = engine.ConvLayer(blob.pack_kidx(w), C, C, synth.make_thresholds(32, C, 288),
-                         synth.make_thresholds(33, C, 288))
-    da = torch.from_numpy(a).cuda()
-    act = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
-    engine.pack_act_device(da.data_ptr(), act.data_ptr(), N, C, H, W, sp)
-    del da
-    skip = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
-    down = torch.empty((N, H // 2, W // 2, C // 32), dtype=torch.int32, device="cuda")
-    reps = 20
-    settle(lambda: L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp), torch)
-    for _ in range(3):
-        L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(reps):
-        L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    pool_ms = e0.elapsed_time(e1) / reps
-    pool_bitmacs = N * C * H * W * C * 9
-    pool_rate = 2 * pool_bitmacs / (pool_ms / 1e3)
-    log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, "
-        f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
-    L.close()
+        # fused bconv + fold + 2x2 max-pool, 128->128 at 32x32, batch 1024
+        C = 128
+        a = synth.make_bits(30, N, H, W, C)
+        w = synth.make_signs(31, C, C)
+        L = engine.ConvLayer(blob.pack_kidx(w), C, C, synth.make_thresholds(32, C, 288),
+                             synth.make_thresholds(33, C, 288))
+        da = torch.from_numpy(a).cuda()
+        act = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
+        engine.pack_act_device(da.data_ptr(), act.data_ptr(), N, C, H, W, sp)
+        del da
+        skip = torch.empty((N, H, W, C // 32), dtype=torch.int32, device="cuda")
+        down = torch.empty((N, H // 2, W // 2, C // 32), dtype=torch.int32, device="cuda")
+        reps = 20
+        settle(lambda: L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp), torch)
+        for _ in range(3):
+            L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            L.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        pool_ms = e0.elapsed_time(e1) / reps
+        pool_bitmacs = N * C * H * W * C * 9
+        pool_rate = 2 * pool_bitmacs / (pool_ms / 1e3)
+        log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, "
+            f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
+        L.close()
 
-    # benchmark config 4: large tiles, 256 x 256 x 120, batch 64, base 32
-    # (wide layers, 512 channels at the bottleneck); the int8 matrix-core
-    # conv takes the binary convs with at least 4 chunks of 64 input
-    # channels, the popcount kernel the rest
-    b4 = synth.make_blob(seed=0, base=32)
-    p4 = os.path.join(td, "bench_cfg4.blob")
-    blob.write(b4, p4)
-    eng4 = engine.Engine(p4)
-    N4, S4 = 64, 256
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(4)
-    x4 = torch.randn((N4, b4.n_bands, S4, S4), generator=gen, device="cuda", dtype=torch.float32)
-    y4 = torch.empty((N4, b4.n_classes, S4, S4), dtype=torch.float32, device="cuda")
-    settle(lambda: eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp), torch)
-    for _ in range(2):
-        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-    torch.cuda.synchronize()
-    reps4 = 5
-    e0.record(stream)
-    for _ in range(reps4):
-        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    cfg4_ms = e0.elapsed_time(e1) / reps4
-    engine.prof_reset()
-    engine.prof_enable(True)
-    for _ in range(reps4):
-        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-    torch.cuda.synchronize()
-    engine.prof_enable(False)
-    agg4 = {}
-    for lab, op, ms, work in engine.prof_records():
-        a4 = agg4.setdefault(lab, [op, 0.0, 0, work])
-        a4[1] += ms
-        a4[2] += 1
-    cfg4_kern = []
-    for lab, (op, tot, cnt, work) in agg4.items():
-        us = tot / cnt * 1e3
-        k4 = {"label": lab, "op": op, "us": round(us, 2)}
-        if op.endswith("_mfma"):
-            k4["mac_s"] = round(work / (us / 1e6), 1)  # bit-MACs = int8 MACs
-            k4["frac_int8_peak"] = round(work / (us / 1e6) / PEAK_INT8_MACS, 4)
-        cfg4_kern.append(k4)
-    log(f"cfg4 256x256x120 b{N4} base 32: {cfg4_ms:.3f} ms/step, {N4 / cfg4_ms * 1e3:,.0f} patches/s")
-    for k4 in cfg4_kern:
-        extra = f"  {k4['frac_int8_peak']:.3f} of int8 peak" if "mac_s" in k4 else ""
-        log(f"  {k4['label']:10s} {k4['op']:16s} {k4['us']:9.1f} us{extra}")
-    eng4.close()
-    del x4, y4
+        # benchmark config 4: large tiles, 256 x 256 x 120, batch 64, base 32
+        # (wide layers, 512 channels at the bottleneck); the int8 matrix-core
+        # conv takes the binary convs with at least 4 chunks of 64 input
+        # channels, the popcount kernel the rest
+        b4 = synth.make_blob(seed=0, base=32)
+        p4 = os.path.join(td, "bench_cfg4.blob")
+        blob.write(b4, p4)
+        eng4 = engine.Engine(p4)
+        N4, S4 = 64, 256
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(4)
+        x4 = torch.randn((N4, b4.n_bands, S4, S4), generator=gen, device="cuda", dtype=torch.float32)
+        y4 = torch.empty((N4, b4.n_classes, S4, S4), dtype=torch.float32, device="cuda")
+        settle(lambda: eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp), torch)
+        for _ in range(2):
+            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+        torch.cuda.synchronize()
+        reps4 = 5
+        e0.record(stream)
+        for _ in range(reps4):
+            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cfg4_ms = e0.elapsed_time(e1) / reps4
+        engine.prof_reset()
+        engine.prof_enable(True)
+        for _ in range(reps4):
+            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+        torch.cuda.synchronize()
+        engine.prof_enable(False)
+        agg4 = {}
+        for lab, op, ms, work in engine.prof_records():
+            a4 = agg4.setdefault(lab, [op, 0.0, 0, work])
+            a4[1] += ms
+            a4[2] += 1
+        cfg4_kern = []
+        for lab, (op, tot, cnt, work) in agg4.items():
+            us = tot / cnt * 1e3
+            k4 = {"label": lab, "op": op, "us": round(us, 2)}
+            if op.endswith("_mfma"):
+                k4["mac_s"] = round(work / (us / 1e6), 1)  # bit-MACs = int8 MACs
+                k4["frac_int8_peak"] = round(work / (us / 1e6) / PEAK_INT8_MACS, 4)
+            cfg4_kern.append(k4)
+        log(f"cfg4 256x256x120 b{N4} base 32: {cfg4_ms:.3f} ms/step, {N4 / cfg4_ms * 1e3:,.0f} patches/s")
+        for k4 in cfg4_kern:
+            extra = f"  {k4['frac_int8_peak']:.3f} of int8 peak" if "mac_s" in k4 else ""
+            log(f"  {k4['label']:10s} {k4['op']:16s} {k4['us']:9.1f} us{extra}")
+        eng4.close()
+        del x4, y4
 
-    # benchmark config 3: a 956 x 684 x 120 scene (N(0,1) plus a per-band
-    # offset U(-0.5, 0.5)) cut into 32 x 32 patches, 30 x 22 = 660 with the
-    # edge patches zero past the scene; the device call reads the patches
-    # straight out of the cube, the host call adds the strip-wise PCIe copy
-    SH, SW, PS = 956, 684, 32
-    rng = np.random.default_rng(40)
-    cube = rng.standard_normal((b.n_bands, SH, SW), dtype=np.float32)
-    cube += rng.uniform(-0.5, 0.5, (b.n_bands, 1, 1)).astype(np.float32)
-    npatch = ((SH + PS - 1) // PS) * ((SW + PS - 1) // PS)
-    d_cube = torch.from_numpy(cube).cuda()
-    d_map = torch.empty((b.n_classes, SH, SW), dtype=torch.float32, device="cuda")
-    settle(lambda: eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp), torch)
-    for _ in range(3):
-        eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
-    torch.cuda.synchronize()
-    reps = 10
-    e0.record(stream)
-    for _ in range(reps):
-        eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    scene_dev_ms = e0.elapsed_time(e1) / reps
-    host_map = eng.forward_patched(cube, PS)
-    assert np.array_equal(host_map.view(np.uint32), d_map.cpu().numpy().view(np.uint32))
-    t0 = time.perf_counter()
-    for _ in range(3):
-        eng.forward_patched(cube, PS)
-    scene_host_ms = (time.perf_counter() - t0) / 3 * 1e3
-    log(f"scene {SH}x{SW}x{b.n_bands} ({npatch} patches): device {scene_dev_ms:.3f} ms "
-        f"({npatch / scene_dev_ms * 1e3:,.0f} patches/s), host pointers {scene_host_ms:.2f} ms "
-        f"({cube.nbytes / scene_host_ms / 1e6:.1f} GB/s of input)")
-    del d_cube, d_map
+        # benchmark config 3: a 956 x 684 x 120 scene (N(0,1) plus a per-band
+        # offset U(-0.5, 0.5)) cut into 32 x 32 patches, 30 x 22 = 660 with the
+        # edge patches zero past the scene; the device call reads the patches
+        # straight out of the cube, the host call adds the strip-wise PCIe copy
+        SH, SW, PS = 956, 684, 32
+        rng = np.random.default_rng(40)
+        cube = rng.standard_normal((b.n_bands, SH, SW), dtype=np.float32)
+        cube += rng.uniform(-0.5, 0.5, (b.n_bands, 1, 1)).astype(np.float32)
+        npatch = ((SH + PS - 1) // PS) * ((SW + PS - 1) // PS)
+        d_cube = torch.from_numpy(cube).cuda()
+        d_map = torch.empty((b.n_classes, SH, SW), dtype=torch.float32, device="cuda")
+        settle(lambda: eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp), torch)
+        for _ in range(3):
+            eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
+        torch.cuda.synchronize()
+        reps = 10
+        e0.record(stream)
+        for _ in range(reps):
+            eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        scene_dev_ms = e0.elapsed_time(e1) / reps
+        host_map = eng.forward_patched(cube, PS)
+        assert np.array_equal(host_map.view(np.uint32), d_map.cpu().numpy().view(np.uint32))
+        t0 = time.perf_counter()
+        for _ in range(3):
+            eng.forward_patched(cube, PS)
+        scene_host_ms = (time.perf_counter() - t0) / 3 * 1e3
+        log(f"scene {SH}x{SW}x{b.n_bands} ({npatch} patches): device {scene_dev_ms:.3f} ms "
+            f"({npatch / scene_dev_ms * 1e3:,.0f} patches/s), host pointers {scene_host_ms:.2f} ms "
+            f"({cube.nbytes / scene_host_ms / 1e6:.1f} GB/s of input)")
+        del d_cube, d_map
 
-    # the v2 spectral-stem model (csrc/bnn_model_stem.c): 16-channel stem
-    # (the reference exporter's default), base 16, same batch and input
-    bs = synth.make_blob_v2(seed=0, base=16, stem=16)
-    stem_path = os.path.join(td, "bench_stem.blob")
-    blob.write(bs, stem_path)
-    seng = engine.StemEngine(stem_path)
+        # the v2 spectral-stem model (csrc/bnn_model_stem.c): 16-channel stem
+        # (the reference exporter's default), base 16, same batch and input
+        bs = synth.make_blob_v2(seed=0, base=16, stem=16)
+        stem_path = os.path.join(td, "bench_stem.blob")
+        blob.write(bs, stem_path)
+        seng = engine.StemEngine(stem_path)
 
-    def sstep():
-        seng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+        def sstep():
+            seng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
 
-    settle(sstep, torch)
-    for _ in range(args.warmup):
-        sstep()
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        sstep()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    v2_ms = e0.elapsed_time(e1) / args.steps
-    engine.prof_reset()
-    engine.prof_enable(True)
-    for _ in range(args.steps):
-        sstep()
-    torch.cuda.synchronize()
-    engine.prof_enable(False)
-    stem_ms = [ms for lab, op, ms, work in engine.prof_records() if lab == "stem.conv"]
-    stem_ms = sum(stem_ms) / len(stem_ms)
-    # algorithmic bytes: every input float once, one 32-bit word of stem bits per pixel out
-    stem_bytes = N * bs.n_bands * H * W * 4 + N * H * W * 4
-    stem_rate = stem_bytes / (stem_ms / 1e3)
-    log(f"v2 stem model: {v2_ms:.4f} ms/step, {N / v2_ms * 1e3:,.0f} patches/s; stem kernel "
-        f"{stem_ms * 1e3:.1f} us, {stem_rate / 1e9:.0f} GB/s ({stem_rate / PEAK_HBM:.3f} of HBM peak)")
-    seng.close()
+        settle(sstep, torch)
+        for _ in range(args.warmup):
+            sstep()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            sstep()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        v2_ms = e0.elapsed_time(e1) / args.steps
+        engine.prof_reset()
+        engine.prof_enable(True)
+        for _ in range(args.steps):
+            sstep()
+        torch.cuda.synchronize()
+        engine.prof_enable(False)
+        stem_ms = [ms for lab, op, ms, work in engine.prof_records() if lab == "stem.conv"]
+        stem_ms = sum(stem_ms) / len(stem_ms)
+        # algorithmic bytes: every input float once, one 32-bit word of stem bits per pixel out
+        stem_bytes = N * bs.n_bands * H * W * 4 + N * H * W * 4
+        stem_rate = stem_bytes / (stem_ms / 1e3)
+        log(f"v2 stem model: {v2_ms:.4f} ms/step, {N / v2_ms * 1e3:,.0f} patches/s; stem kernel "
+            f"{stem_ms * 1e3:.1f} us, {stem_rate / 1e9:.0f} GB/s ({stem_rate / PEAK_HBM:.3f} of HBM peak)")
+        seng.close()
 
-    # the v3 ReActNet model (csrc/bnn_model_react.c): float highway, taps,
-    # 1x1 projections, RPReLU epilogues; base 16, same batch and input
-    from bnns_to_c_amd import blob_react
-    br = synth.make_blob_react(seed=0, base=16)
-    react_path = os.path.join(td, "bench_react.blob")
-    blob_react.write(br, react_path)
-    reng = engine.ReactEngine(react_path)
+        # the v3 ReActNet model (csrc/bnn_model_react.c): float highway, taps,
+        # 1x1 projections, RPReLU epilogues; base 16, same batch and input
+        from bnns_to_c_amd import blob_react
+        br = synth.make_blob_react(seed=0, base=16)
+        react_path = os.path.join(td, "bench_react.blob")
+        blob_react.write(br, react_path)
+        reng = engine.ReactEngine(react_path)
 
-    def rstep():
-        reng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+        def rstep():
+            reng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
 
-    settle(rstep, torch)
-    for _ in range(args.warmup):
-        rstep()
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        rstep()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    v3_ms = e0.elapsed_time(e1) / args.steps
-    engine.prof_reset()
-    engine.prof_enable(True)
-    for _ in range(args.steps):
-        rstep()
-    torch.cuda.synchronize()
-    engine.prof_enable(False)
-    ragg = {}
-    for lab, op, ms, work in engine.prof_records():
-        a = ragg.setdefault(lab, [op, 0.0, 0, work])
-        a[1] += ms
-        a[2] += 1
-    rkern = [{"label": lab, "op": op, "us": round(tot / cnt * 1e3, 2)} for lab, (op, tot, cnt, _) in ragg.items()]
-    in_us = ragg["enc1.u1"][1] / ragg["enc1.u1"][2] * 1e3
-    # enc1 unit 1: the 3x3 conv (1,080 FMAs per output) and the projection
-    # (120 per output), 16 channels x 32 x 32 per patch
-    in_flops = 2.0 * N * br.enc[0].conv1.cout * H * W * br.n_bands * 10
-    in_rate = in_flops / (in_us / 1e6)
-    v3_cpu = None if args.no_cpu else cpu_baseline_react(react_path, args.cpu_budget / 2)
-    log(f"v3 ReActNet model: {v3_ms:.4f} ms/step, {N / v3_ms * 1e3:,.0f} patches/s; enc1 unit-1 kernel "
-        f"{in_us:.1f} us, {in_rate / 1e12:.1f} TFLOP/s ({in_rate / PEAK_FP32_FLOPS:.3f} of peak)")
-    for k in rkern:
-        log(f"  {k['label']:10s} {k['op']:10s} {k['us']:9.1f} us")
-    reng.close()
+        settle(rstep, torch)
+        for _ in range(args.warmup):
+            rstep()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            rstep()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        v3_ms = e0.elapsed_time(e1) / args.steps
+        engine.prof_reset()
+        engine.prof_enable(True)
+        for _ in range(args.steps):
+            rstep()
+        torch.cuda.synchronize()
+        engine.prof_enable(False)
+        ragg = {}
+        for lab, op, ms, work in engine.prof_records():
+            a = ragg.setdefault(lab, [op, 0.0, 0, work])
+            a[1] += ms
+            a[2] += 1
+        rkern = [{"label": lab, "op": op, "us": round(tot / cnt * 1e3, 2)} for lab, (op, tot, cnt, _) in ragg.items()]
+        in_us = ragg["enc1.u1"][1] / ragg["enc1.u1"][2] * 1e3
+        # enc1 unit 1: the 3x3 conv (1,080 FMAs per output) and the projection
+        # (120 per output), 16 channels x 32 x 32 per patch
+        in_flops = 2.0 * N * br.enc[0].conv1.cout * H * W * br.n_bands * 10
+        in_rate = in_flops / (in_us / 1e6)
+        v3_cpu = None if args.no_cpu else cpu_baseline_react(react_path, args.cpu_budget / 2)
+        log(f"v3 ReActNet model: {v3_ms:.4f} ms/step, {N / v3_ms * 1e3:,.0f} patches/s; enc1 unit-1 kernel "
+            f"{in_us:.1f} us, {in_rate / 1e12:.1f} TFLOP/s ({in_rate / PEAK_FP32_FLOPS:.3f} of peak)")
+        for k in rkern:
+            log(f"  {k['label']:10s} {k['op']:10s} {k['us']:9.1f} us")
+        reng.close()
 
     # the headline, measured last: the configurations above have kept the
     # GPU busy for several seconds by now, so its clocks have settled
@@ -570,26 +573,27 @@ def main() -> int:
     bin_work = sum(agg[k["label"]][3] for k in kernels if k["op"] != "conv_real")
     bin_rate = 2 * bin_work / (bin_ms / 1e3)
 
-    # the same batch from and to host memory (pinned buffers): the copies in
-    # and out over PCIe are part of each call (bnn_forward_batch)
-    xh = torch.from_numpy(synth.make_input(1, N)).pin_memory()
-    yh = torch.empty((N, b.n_classes, H, W), dtype=torch.float32).pin_memory()
-    for _ in range(2):
-        eng.forward_batch_ptr(xh.data_ptr(), N, H, W, yh.data_ptr())
-    host_ms = []
-    for _ in range(max(3, min(args.steps, 10))):
-        h0 = time.perf_counter()
-        eng.forward_batch_ptr(xh.data_ptr(), N, H, W, yh.data_ptr())
-        host_ms.append((time.perf_counter() - h0) * 1e3)
-    pcie_ms = float(np.median(host_ms))
-    assert np.array_equal(yh.numpy().view(np.uint32), y.cpu().numpy().view(np.uint32))
-    log(f"forward with host buffers (pinned, copies in and out included): {pcie_ms:.3f} ms, "
-        f"{N / pcie_ms * 1e3:,.0f} patches/s ({xh.numel() * 4 / pcie_ms / 1e6:.1f} GB/s of input)")
-    del xh, yh
+    if not args.headline_only:
+        # the same batch from and to host memory (pinned buffers): the copies in
+        # and out over PCIe are part of each call (bnn_forward_batch)
+        xh = torch.from_numpy(synth.make_input(1, N)).pin_memory()
+        yh = torch.empty((N, b.n_classes, H, W), dtype=torch.float32).pin_memory()
+        for _ in range(2):
+            eng.forward_batch_ptr(xh.data_ptr(), N, H, W, yh.data_ptr())
+        host_ms = []
+        for _ in range(max(3, min(args.steps, 10))):
+            h0 = time.perf_counter()
+            eng.forward_batch_ptr(xh.data_ptr(), N, H, W, yh.data_ptr())
+            host_ms.append((time.perf_counter() - h0) * 1e3)
+        pcie_ms = float(np.median(host_ms))
+        assert np.array_equal(yh.numpy().view(np.uint32), y.cpu().numpy().view(np.uint32))
+        log(f"forward with host buffers (pinned, copies in and out included): {pcie_ms:.3f} ms, "
+            f"{N / pcie_ms * 1e3:,.0f} patches/s ({xh.numel() * 4 / pcie_ms / 1e6:.1f} GB/s of input)")
+        del xh, yh
 
     cpu = None
     cpu_cfg = {}
-    if not args.no_cpu:
+    if not args.no_cpu and not args.headline_only:
         log("cpu baseline ...")
         cpu = cpu_baseline(blob_path, args.cpu_budget)
         log(f"cpu baseline: {cpu}")
@@ -641,44 +645,48 @@ def main() -> int:
                      "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": measured_traffic(),
                      "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, calibrated)",
                      "algorithmic": f"{real_flops:.4g} FLOP/launch = 2 x 17,694,720 MAC x {N} patches"},
-        "bconv": {"kernels": 17, "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
+        "bconv": {"layers": 17, "kernels": sum(1 for k in kernels if k["op"] != "conv_real"),
+                  "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
                   "frac": round(bin_rate / valu_binop_peak(), 4), "ms": round(bin_ms, 5),
                   "unit": "binary-op/s (2 per bit-MAC, border taps counted)"},
-        "with_copies": {"config": "the same batch from and to pinned host memory (bnn_forward_batch: copies in "
-                                  "and out over PCIe included)",
-                        "ms_per_step": round(pcie_ms, 4), "patches_s": round(N / pcie_ms * 1e3, 1)},
-        "cpu_configs": cpu_cfg,
-        "cfg1": {"config": "isolated bconv 64->64, 64x64, batch 256, int32 P out (benchmark config 1)",
-                 "us": round(c1_ms * 1e3, 2), "binary_op_s": round(c1_rate, 1),
-                 "frac": round(c1_rate / valu_binop_peak(), 4),
-                 "hbm_GB_s": round(c1_bytes / (c1_ms / 1e3) / 1e9, 1),
-                 "hbm_frac": round(c1_bytes / (c1_ms / 1e3) / PEAK_HBM, 4)},
-        "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
-                       "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
-                       "frac": round(pool_rate / valu_binop_peak(), 4)},
-        "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
-                 "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
-                 "kernels": cfg4_kern,
-                 "int8_mfma_rule": "binary convs with >= 4 chunks of 64 input channels and 8 <= W <= 64"},
-        "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
-                            "past the scene), benchmark config 3",
-                  "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
-                  "host_ms": round(scene_host_ms, 3),
-                  "host_note": "host cube in, host map out: strips through pinned buffers over PCIe"},
-        "v2_stem": {"config": "v2 spectral-stem model, 16-channel 1x1 stem, base 16, 32x32x120, batch 1024",
-                    "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),
-                    "stem_kernel_us": round(stem_ms * 1e3, 2), "stem_bytes": stem_bytes,
-                    "stem_hbm_GB_s": round(stem_rate / 1e9, 1), "stem_frac": round(stem_rate / PEAK_HBM, 4)},
-        "v3_react": {"config": "v3 ReActNet real-highway model, base 16, 32x32x120, batch 1024",
-                     "ms_per_step": round(v3_ms, 5), "patches_s": round(N / v3_ms * 1e3, 1),
-                     "enc1_kernel_us": round(in_us, 2), "enc1_tflops": round(in_rate / 1e12, 3),
-                     "enc1_frac": round(in_rate / PEAK_FP32_FLOPS, 4),
-                     "enc1_algorithmic": f"{in_flops:.4g} FLOP/launch = 2 x 16 x 1024 px x 120 x (9 + 1) "
-                                         f"x {N} patches",
-                     "kernels": rkern, "cpu_baseline": v3_cpu},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
+    if not args.headline_only:
+        out.update({
+            "with_copies": {"config": "the same batch from and to pinned host memory (bnn_forward_batch: copies "
+                                      "in and out over PCIe included)",
+                            "ms_per_step": round(pcie_ms, 4), "patches_s": round(N / pcie_ms * 1e3, 1)},
+            "cpu_configs": cpu_cfg,
+            "cfg1": {"config": "isolated bconv 64->64, 64x64, batch 256, int32 P out (benchmark config 1)",
+                     "us": round(c1_ms * 1e3, 2), "binary_op_s": round(c1_rate, 1),
+                     "frac": round(c1_rate / valu_binop_peak(), 4),
+                     "hbm_GB_s": round(c1_bytes / (c1_ms / 1e3) / 1e9, 1),
+                     "hbm_frac": round(c1_bytes / (c1_ms / 1e3) / PEAK_HBM, 4)},
+            "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
+                           "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
+                           "frac": round(pool_rate / valu_binop_peak(), 4)},
+            "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
+                     "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
+                     "kernels": cfg4_kern,
+                     "int8_mfma_rule": "binary convs with >= 4 chunks of 64 input channels and 8 <= W <= 64"},
+            "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
+                                "past the scene), benchmark config 3",
+                      "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
+                      "host_ms": round(scene_host_ms, 3),
+                      "host_note": "host cube in, host map out: strips through pinned buffers over PCIe"},
+            "v2_stem": {"config": "v2 spectral-stem model, 16-channel 1x1 stem, base 16, 32x32x120, batch 1024",
+                        "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),
+                        "stem_kernel_us": round(stem_ms * 1e3, 2), "stem_bytes": stem_bytes,
+                        "stem_hbm_GB_s": round(stem_rate / 1e9, 1), "stem_frac": round(stem_rate / PEAK_HBM, 4)},
+            "v3_react": {"config": "v3 ReActNet real-highway model, base 16, 32x32x120, batch 1024",
+                         "ms_per_step": round(v3_ms, 5), "patches_s": round(N / v3_ms * 1e3, 1),
+                         "enc1_kernel_us": round(in_us, 2), "enc1_tflops": round(in_rate / 1e12, 3),
+                         "enc1_frac": round(in_rate / PEAK_FP32_FLOPS, 4),
+                         "enc1_algorithmic": f"{in_flops:.4g} FLOP/launch = 2 x 16 x 1024 px x 120 x (9 + 1) "
+                                             f"x {N} patches",
+                         "kernels": rkern, "cpu_baseline": v3_cpu},
+        })
     print(json.dumps(out), flush=True)
     return 0
 
