@@ -1167,8 +1167,18 @@ int run_scene_strips(const Model* m, const float* cube, bool host_cube, int H, i
                                hipMemcpyDeviceToDevice, s));
     }
     if ((rc = run_scene_rows(m, D->strip_in[b], rows, W, D->strip_out[b], P, 0, nr, s))) return rc;
-    HIP_TRY(hipMemcpy2DAsync(map + (size_t)r0 * W, (size_t)H * W * 4, D->strip_out[b], band * 4, band * 4, ncls,
-                             host_map ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice, s));
+    // the strip's map rows span the full width, so each class is one
+    // contiguous run of the map; a host map takes plain copies per class
+    // (a strided copy into pageable memory lost its order behind the
+    // strip's kernels under the profiler's kernel tracing)
+    if (host_map) {
+      for (int c = 0; c < ncls; ++c)
+        HIP_TRY(hipMemcpyAsync(map + ((size_t)c * H + r0) * W, D->strip_out[b] + (size_t)c * band, band * 4,
+                               hipMemcpyDeviceToHost, s));
+    } else {
+      HIP_TRY(hipMemcpy2DAsync(map + (size_t)r0 * W, (size_t)H * W * 4, D->strip_out[b], band * 4, band * 4, ncls,
+                               hipMemcpyDeviceToDevice, s));
+    }
     HIP_TRY(hipEventRecord(D->ev_done[b], s));
   }
   if (host_map) HIP_TRY(hipStreamSynchronize(s));
