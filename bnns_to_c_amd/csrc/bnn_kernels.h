@@ -223,6 +223,30 @@ inline void react_proj_lanes(const float* W, int cout, int cin, float* out) {
 // v3 enc1 unit 1: 3x3 conv (lane masks) + projection + epilogue -> h planes and tap bits
 hipError_t launch_react_in(const RealArgs& a, hipStream_t s);
 
+// v3 enc1 unit 1 when its Cout is not a multiple of 8.  The reference then
+// runs the general real conv (csrc/bnn_model_react.c:152-158: per output the
+// taps in row-major order, each a chain over ci, then alpha * acc), which
+// is the v1 order: launch_real writes that conv into `conv` first.  This
+// kernel adds the projection (one fma chain over ci from +0 per output,
+// csrc/bnn_react_ops.c:117-133), the real epilogue
+// (csrc/bnn_react_epi.c:57-77) and the tap of unit 2, a thread per pixel.
+struct ReactTailArgs {
+  const float* x;      // the input, as RealArgs::x (batch, or a scene cube with the fields below)
+  const float* pw;     // projection weights [cout rounded up to 16][cin], zero past cout
+  const float* conv;   // alpha * conv, [N][cout][H][W]
+  const float* A;      // epilogue A, B (= B + move1), slope (PReLU weight), the next tap's rsign;
+  const float* B;      // padded to 32 channels
+  const float* slope;
+  const float* rsign;
+  int N, H, W, cin, cout;
+  uint32_t* out;       // tap bits [N*H*W][ceil(cout/32)]
+  float* hout;         // h planes [cout][ntot*H*W], this call's first patch at column 0
+  int ntot;            // patches in a plane row (0: N)
+  float* f32b;         // projection output [N][cout][H][W] (debug forward); may be null
+  int sH, sW, pcols, prow0;
+};
+hipError_t launch_react_in_tail(const ReactTailArgs& a, hipStream_t s);
+
 // v3 1x1 projection of binary blocks (no bias), on the matrix cores:
 // out[co][q] = chain over ci from 0 of W[co][ci] * x[ci][q] over the planes
 // of x (q = (n*H + y)*W + x).  With x1 set, channels >= c0 come from the

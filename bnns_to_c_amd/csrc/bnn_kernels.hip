@@ -2398,6 +2398,76 @@ hipError_t launch_react_in(const RealArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// v3 enc1 unit 1, general-order conv already in a.conv: projection chains,
+// real epilogue, h planes and the tap bits of unit 2, a thread per pixel.
+// The input column of a channel is read once for 16 output channels (their
+// chains advance together, each over ci from 0 in order).
+__global__ __launch_bounds__(kBlock) void k_react_in_tail(const ReactTailArgs a) {
+  const long i = (long)blockIdx.x * kBlock + threadIdx.x;
+  const long HW = (long)a.H * a.W;
+  if (i >= (long)a.N * HW) return;
+  const int n = (int)(i / HW);
+  const long p = i - (long)n * HW;
+  const int y = (int)(p / a.W), x = (int)(p - (long)y * a.W);
+  // the input column: batch [N][cin][H][W], or a patch of the scene cube
+  // (rows and columns past the cube read 0)
+  const float* xc;
+  long cstride;
+  bool inside = true;
+  if (a.pcols > 0) {
+    const int sy = (a.prow0 + n / a.pcols) * a.H + y, sx = (n % a.pcols) * a.W + x;
+    inside = sy < a.sH && sx < a.sW;
+    xc = a.x + (inside ? (long)sy * a.sW + sx : 0);
+    cstride = (long)a.sH * a.sW;
+  } else {
+    xc = a.x + (long)n * a.cin * HW + p;
+    cstride = HW;
+  }
+  typedef const __attribute__((address_space(4))) float* const_f;
+  const const_f pw = (const_f)a.pw;
+  const long plane = (long)(a.ntot ? a.ntot : a.N) * HW;
+  const int cw = (a.cout + 31) >> 5;
+  uint32_t word = 0;
+#pragma unroll 1
+  for (int c0 = 0; c0 < a.cout; c0 += 16) {
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+#pragma unroll 1
+    for (int ci = 0; ci < a.cin; ++ci) {
+      const float v = inside ? xc[ci * cstride] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = __fmaf_rn(pw[(c0 + j) * a.cin + ci], v, acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int co = c0 + j;
+      if (co >= a.cout) break;
+      const long at = ((long)n * a.cout + co) * HW + p;
+      const float res = acc[j];
+      if (a.f32b) a.f32b[at] = res;
+      const float t = __fadd_rn(__fmaf_rn(a.A[co], a.conv[at], a.B[co]), res);
+      const float h = t >= 0.0f ? t : __fmul_rn(a.slope[co], t);
+      a.hout[co * plane + (long)n * HW + p] = h;
+      word |= (__fadd_rn(h, a.rsign[co]) > 0.0f ? 1u : 0u) << (co & 31);
+      if ((co & 31) == 31 || co == a.cout - 1) {
+        a.out[i * cw + (co >> 5)] = word;
+        word = 0;
+      }
+    }
+  }
+}
+
+hipError_t launch_react_in_tail(const ReactTailArgs& a, hipStream_t s) {
+  const long n = (long)a.N * a.H * a.W;
+  if (n <= 0) return hipSuccess;
+  if (!a.x || !a.pw || !a.conv || !a.A || !a.B || !a.slope || !a.rsign || !a.out || !a.hout || a.cout <= 0 ||
+      a.cin <= 0 || (a.ntot && a.ntot < a.N))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_react_in_tail, dim3(blocks_for(n)), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
 int stem_groups_per_wave(int cout) { return std::min(4, (cout + 15) / 16); }
 
 #ifndef BNN_STEM_NQ4

@@ -8,6 +8,8 @@
 // 190-274, 395-438, one kernel per fused stage over a batch of N
 // independent patches:
 //   enc1   launch_react_in: conv + projection + epilogue -> h1 and tap2 bits
+//          (Cout % 8 != 0: launch_real's general-order conv, then
+//          launch_react_in_tail for the projection, epilogue and tap)
 //   unit 1 launch_proj (res), then the binary conv of the tap1 bits with the
 //          RPReLU epilogue -> h1 and its tap2 bits
 //   unit 2 the binary conv of the tap2 bits; down blocks: skip h and the
@@ -182,9 +184,11 @@ int parse_blob(const char* path, ModelR** out) {
 // What this engine runs beyond the reader's checks: the widths chain as the
 // forward uses them (the reference trusts them), every conv is 3x3 / pad 1
 // / stride 1 (the reference's binary path exits otherwise,
-// csrc/bnn_model_react.c:146-151), enc1.conv1 takes the reference's
+// csrc/bnn_model_react.c:146-151), and an enc1.conv1 on the reference's
 // register-blocked path (Cout % 8 == 0, csrc/bnn_model_react.c:152-158)
-// with +-1 signs, and the head fits one work-item's channel group.
+// has +-1 signs (its matrix-core kernel holds them as lane masks).  With
+// Cout % 8 != 0 the reference's general conv runs instead, here the v1
+// first-conv kernels, which take any int8 signs.
 int validate(const ModelR* m) {
   auto k3 = [](const ConvR& c) {
     return c.kh == 3 && c.kw == 3 && c.pad == 1 && c.stride == 1 &&
@@ -200,8 +204,8 @@ int validate(const ModelR* m) {
     prev = b.conv2.Cout;
   }
   const ConvR& r = m->enc[0].conv1;
-  if (r.Cout % 8) return set_err(BNN_EBLOB, "enc1.conv1: Cout %d is not a multiple of 8", r.Cout);
-  if (!real_conv_signs_only(r.wsign, r.Cout, r.Cin)) return set_err(BNN_EBLOB, "enc1.conv1: signs must be +-1");
+  if (r.Cout % 8 == 0 && !real_conv_signs_only(r.wsign, r.Cout, r.Cin))
+    return set_err(BNN_EBLOB, "enc1.conv1: signs must be +-1 when Cout is a multiple of 8");
   const BlockR& bt = m->bott;
   if (bt.conv1.Cin != prev || bt.conv2.Cin != bt.conv1.Cout || bt.conv2.Cout != bt.conv1.Cout)
     return set_err(BNN_EBLOB, "bottleneck: channel widths do not chain");
@@ -263,6 +267,11 @@ struct BnnReactDevice {
   int rcin = 0, rcout = 0;
   uint64_t* rwm = nullptr;
   float *ralpha = nullptr, *rpw = nullptr;
+  // enc1.conv1 with Cout % 8 != 0: the general-order conv (launch_real, lane
+  // masks in rwm when every sign is +-1, else floats in rw) and the
+  // projection as plain rows for launch_react_in_tail (rpw)
+  bool rgen = false;
+  float* rw = nullptr;
   DevBlock blk[9];  // enc1..4, bott, dec4..1
   float *hw = nullptr, *hb = nullptr;
   int ncls = 0;
@@ -342,12 +351,26 @@ int build_device(ModelR* m) {
   {
     const ConvR& c = m->enc[0].conv1;
     D->rcin = c.Cin; D->rcout = c.Cout;
-    std::vector<uint64_t> wm(real_conv_masks_len(c.Cout, c.Cin));
-    real_conv_masks(c.wsign, c.Cout, c.Cin, wm.data());
-    if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
-    std::vector<float> pw(react_proj_lanes_len(c.Cout, c.Cin));
-    react_proj_lanes(m->enc[0].proj1.W, c.Cout, c.Cin, pw.data());
-    if ((rc = dev_upload(D, &D->rpw, pw.data(), pw.size()))) return rc;
+    D->rgen = c.Cout % 8 != 0;
+    if (!D->rgen || real_conv_signs_only(c.wsign, c.Cout, c.Cin)) {
+      std::vector<uint64_t> wm(real_conv_masks_len(c.Cout, c.Cin));
+      real_conv_masks(c.wsign, c.Cout, c.Cin, wm.data());
+      if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
+    } else {
+      std::vector<float> w(real_conv_weights_len(c.Cout, c.Cin));
+      real_conv_weights(c.wsign, c.Cout, c.Cin, w.data());
+      if ((rc = dev_upload(D, &D->rw, w.data(), w.size()))) return rc;
+    }
+    if (D->rgen) {
+      const int cp = (c.Cout + 15) / 16 * 16;
+      std::vector<float> pw((size_t)cp * c.Cin, 0.0f);
+      std::copy(m->enc[0].proj1.W, m->enc[0].proj1.W + (size_t)c.Cout * c.Cin, pw.begin());
+      if ((rc = dev_upload(D, &D->rpw, pw.data(), pw.size()))) return rc;
+    } else {
+      std::vector<float> pw(react_proj_lanes_len(c.Cout, c.Cin));
+      react_proj_lanes(m->enc[0].proj1.W, c.Cout, c.Cin, pw.data());
+      if ((rc = dev_upload(D, &D->rpw, pw.data(), pw.size()))) return rc;
+    }
     if ((rc = upload_pad(D, &D->ralpha, c.alpha, c.Cout))) return rc;
   }
   for (int k = 0; k < 9; ++k) {
@@ -405,7 +428,8 @@ int ensure_ws(const ModelR* m, BnnReactDevice* D, RWorkspace& w, int N, int H, i
   for (int k = 0; k < 9; ++k) {
     const int lvl = level_of(k), c = block_of(m, k).conv1.Cout;
     planes(&w.h1[k], lvl, c);
-    if (k) planes(&w.res[k], lvl, c);
+    // res[0]: enc1's general-order conv output ([N][C][H][W]) when it runs
+    if (k || D->rgen) planes(&w.res[k], lvl, c);
     bits(&w.a2[k], lvl, c);
     if (k < 4) {
       planes(&w.skip[k], lvl, c);
@@ -496,7 +520,28 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
     ra.f32 = dump ? dmp->conv : nullptr;
     ra.f32b = dump ? dmp->proj : nullptr;
     if (sc) { ra.sH = sc->sH; ra.sW = sc->sW; ra.pcols = sc->pcols; ra.prow0 = sc->prow0 + nb / sc->pcols; }
-    HIP_TRY(launch_react_in(ra, st));
+    if (D->rgen) {
+      // the general-order conv, then projection + epilogue + tap
+      ra.wm = D->rwm;
+      ra.w = D->rw;
+      float* conv = dump ? dmp->conv + (size_t)nb * D->rcout * H * W : w.res[0] + (size_t)nb * D->rcout * H * W;
+      RealArgs rc1 = ra;
+      rc1.out = nullptr;
+      rc1.f32 = conv;
+      rc1.pw = nullptr;
+      rc1.hout = nullptr;
+      HIP_TRY(launch_real(rc1, st));
+      ReactTailArgs ta{};
+      ta.x = ra.x; ta.pw = D->rpw; ta.conv = conv;
+      ta.A = L.e1.A; ta.B = L.e1.B; ta.slope = L.e1.W; ta.rsign = L.t2;
+      ta.N = cnt; ta.H = H; ta.W = W; ta.cin = D->rcin; ta.cout = D->rcout;
+      ta.out = ra.out; ta.hout = ra.hout; ta.ntot = N;
+      ta.f32b = dump ? dmp->proj + (size_t)nb * D->rcout * H * W : nullptr;
+      ta.sH = ra.sH; ta.sW = ra.sW; ta.pcols = ra.pcols; ta.prow0 = ra.prow0;
+      HIP_TRY(launch_react_in_tail(ta, st));
+    } else {
+      HIP_TRY(launch_react_in(ra, st));
+    }
     if ((rc = mark("enc1.u1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 10))) return rc;
   }
   auto proj = [&](int k, const float* x0, int c0, const float* x1, int lvl1, float* out) -> int {

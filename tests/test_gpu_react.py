@@ -67,6 +67,8 @@ def _check_stages(eng, model, x):
     (5, 8, 1, False, 1, 16, 16),      # one band
     (6, 16, 121, True, 1, 80, 36),    # taller than the reference's 64-row strips
     (7, 48, 120, False, 1, 32, 32),   # head over 48 channels: dec1 then the separate head kernel
+    (8, 12, 120, False, 2, 32, 32),   # enc1 Cout % 8 != 0: the general-order conv, then the tail kernel
+    (9, 20, 13, True, 2, 30, 34),     # the same with two channel groups, a partial chunk, odd sizes
 ])
 def test_react_stages_vs_checker(tmp_path, rorc, seed, base, nb, cov, N, H, W):
     b = synth.make_blob_react(seed=seed, base=base, n_bands=nb, coverage=cov)
@@ -76,6 +78,35 @@ def test_react_stages_vs_checker(tmp_path, rorc, seed, base, nb, cov, N, H, W):
     x = synth.make_input(seed + 300, N, nb, H, W)
     _check_stages(eng, model, x)
     eng.close()
+
+
+def test_react_enc1_general_signs(tmp_path, rorc):
+    """enc1.conv1 with Cout % 8 != 0 runs the reference's general real conv
+    (csrc/bnn_model_react.c:152-158) for any int8 sign, here 0 and +-2 (the
+    products stay exact): the engine's vector-ALU first conv, then the tail
+    kernel; every stage matches the checker.  With Cout % 8 == 0 the
+    register-blocked path needs +-1 signs, and such a blob is refused."""
+    for base, ok in ((12, True), (16, False)):
+        b = synth.make_blob_react(seed=30 + base, base=base)
+        w = b.enc[0].conv1.wsign.copy()
+        flat = w.reshape(-1)
+        rng = np.random.default_rng(31)
+        idx = rng.choice(flat.size, 64, replace=False)
+        flat[idx[:32]] = 0
+        flat[idx[32:48]] = 2
+        flat[idx[48:]] = -2
+        b.enc[0].conv1.wsign = w
+        if not ok:
+            p = tmp_path / "m16.blob"
+            p.write_bytes(R.to_bytes(b))
+            with pytest.raises(E.BnnError) as e:
+                E.ReactEngine(str(p))
+            assert e.value.code == E.BNN_EBLOB and "+-1" in str(e.value)
+            continue
+        eng, _ = _engine(tmp_path, b)
+        x = synth.make_input(32, 2, 120, 32, 32)
+        _check_stages(eng, rorc.parse(R.to_bytes(b)), x)
+        eng.close()
 
 
 def _sha(a):

@@ -289,7 +289,8 @@ def test_bconv_i16_vs_oracle(orc, rref):
 
 @pytest.mark.parametrize("seed,base,cov,H,W", [
     (0, 16, False, 32, 32), (1, 8, True, 17, 23), (2, 8, False, 80, 36), (3, 32, False, 16, 16),
-    (4, 8, True, 33, 47), (5, 16, True, 32, 32)])
+    (4, 8, True, 33, 47), (5, 16, True, 32, 32),
+    (6, 12, False, 32, 32), (7, 20, True, 17, 23)])  # enc1 Cout % 8 != 0: the general real conv
 def test_forward_vs_reference(rorc, rref, tmp_path, seed, base, cov, H, W):
     """Whole forward bit-exact with the reference bnn_forward_react, odd
     sizes and (80 rows) its strip-wise enc1/dec1 included."""
