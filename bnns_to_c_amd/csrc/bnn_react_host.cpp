@@ -278,6 +278,10 @@ struct BnnReactDevice {
   RWorkspace ws;
   float *stage_in = nullptr, *stage_out = nullptr;
   size_t stage_in_cap = 0, stage_out_cap = 0;
+  // one strip of whole patch rows of a cube of 2 GiB or more, staged as a
+  // sub-cube [nb][rows][W], and its map rows
+  float *strip_in = nullptr, *strip_out = nullptr;
+  size_t strip_in_cap = 0, strip_out_cap = 0;
   // pinned row strips of a streamed input file, filled in turn
   float* strip[2] = {nullptr, nullptr};
   hipEvent_t strip_done[2] = {nullptr, nullptr};
@@ -322,6 +326,8 @@ void release(BnnReactDevice* D) {
   D->allocs.clear();
   if (D->ws.base) (void)hipFree(D->ws.base);
   if (D->stage_in) (void)hipFree(D->stage_in);
+  if (D->strip_in) (void)hipFree(D->strip_in);
+  if (D->strip_out) (void)hipFree(D->strip_out);
   if (D->stage_out) (void)hipFree(D->stage_out);
   for (int k = 0; k < 2; ++k) {
     if (D->strip[k]) (void)hipHostFree(D->strip[k]);
@@ -709,21 +715,28 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
   return BNN_OK;
 }
 
+// A launch addresses its input with 32-bit byte offsets, so one launch
+// takes less than 2 GiB of it: a batch runs in sub-batches of that size
+// (patches_per_launch), a cube of 2 GiB or more in strips of whole patch
+// rows (run_patched_strips).  One image of 2 GiB or more is refused.
+constexpr size_t kLaunchBytes = 0x7FFFFFF0ull;
+int patches_per_launch(const ModelR* m, int H, int W) {
+  return (int)std::min<size_t>(1 << 30, (kLaunchBytes - 1) / ((size_t)m->n_bands * H * W * 4));
+}
+
 int check_shape(const ModelR* m, int N, int H, int W) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   if (N < 0) return set_err(BNN_EARG, "negative batch");
   if (H < 16 || W < 16) return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
-  if ((size_t)N * m->n_bands * H * W * 4 >= 0x7FFFFFF0ull)
-    return set_err(BNN_EARG, "batch too large for one launch (%zu input bytes >= 2 GiB)",
-                   (size_t)N * m->n_bands * H * W * 4);
+  if (patches_per_launch(m, H, W) < 1)
+    return set_err(BNN_EARG, "one %dx%dx%d image exceeds a launch (2 GiB of input)", m->n_bands, H, W);
   return BNN_OK;
 }
 
-int run_device(const ModelR* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
-               Dumps* dmp, const Scene* sc = nullptr) {
+// One launch's forward (N below patches_per_launch).
+int run_device_launch(const ModelR* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+                      Dumps* dmp, const Scene* sc) {
   int rc;
-  if ((rc = check_shape(m, N, H, W))) return rc;
-  if (N == 0) return BNN_OK;
   BnnReactDevice* D = m->dev;
   if ((rc = ensure_ws(m, D, D->ws, N, H, W))) return rc;
   if (!prof_enabled()) return enqueue_forward(m, D, D->ws, d_in, N, H, W, d_logits, s, dmp, nullptr, nullptr, sc);
@@ -742,6 +755,24 @@ int run_device(const ModelR* m, const float* d_in, int N, int H, int W, float* d
   return rc;
 }
 
+// A batch in sub-batches of one launch each (the debug forward's dumps
+// cover the whole batch and take one launch).
+int run_device(const ModelR* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+               Dumps* dmp, const Scene* sc = nullptr) {
+  int rc;
+  if ((rc = check_shape(m, N, H, W))) return rc;
+  if (N == 0) return BNN_OK;
+  const int per = patches_per_launch(m, H, W);
+  if ((dmp && dmp->on) || sc || N <= per) return run_device_launch(m, d_in, N, H, W, d_logits, s, dmp, sc);
+  for (int n0 = 0; n0 < N; n0 += per) {
+    const int cnt = std::min(per, N - n0);
+    if ((rc = run_device_launch(m, d_in + (size_t)n0 * m->n_bands * H * W, cnt, H, W,
+                                d_logits + (size_t)n0 * m->n_classes * H * W, s, nullptr, nullptr)))
+      return rc;
+  }
+  return BNN_OK;
+}
+
 int grow(float** p, size_t* cap, size_t bytes) {
   if (*cap >= bytes) return BNN_OK;
   if (*p) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(*p); *p = nullptr; *cap = 0; }
@@ -750,18 +781,27 @@ int grow(float** p, size_t* cap, size_t bytes) {
   return BNN_OK;
 }
 
+// Host input -> host logits, in sub-batches of at most one launch each
+// (staging buffers of one sub-batch, so device memory stays bounded).
 int run_host(const ModelR* m, const float* input, int N, int H, int W, float* logits, Dumps* dmp) {
   int rc;
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
   BnnReactDevice* D = m->dev;
-  const size_t nin = (size_t)N * m->n_bands * H * W, nout = (size_t)N * m->n_classes * H * W;
-  if ((rc = grow(&D->stage_in, &D->stage_in_cap, nin * 4))) return rc;
-  if ((rc = grow(&D->stage_out, &D->stage_out_cap, nout * 4))) return rc;
-  HIP_TRY(hipMemcpyAsync(D->stage_in, input, nin * 4, hipMemcpyHostToDevice, D->stream));
-  if ((rc = run_device(m, D->stage_in, N, H, W, D->stage_out, D->stream, dmp))) return rc;
-  HIP_TRY(hipMemcpyAsync(logits, D->stage_out, nout * 4, hipMemcpyDeviceToHost, D->stream));
-  HIP_TRY(hipStreamSynchronize(D->stream));
+  const bool dump = dmp && dmp->on;
+  const int per = dump ? N : std::min(N, patches_per_launch(m, H, W));
+  const size_t pin = (size_t)m->n_bands * H * W, pout = (size_t)m->n_classes * H * W;
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, per * pin * 4))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, per * pout * 4))) return rc;
+  for (int n0 = 0; n0 < N; n0 += per) {
+    const int cnt = std::min(per, N - n0);
+    HIP_TRY(hipMemcpyAsync(D->stage_in, input + (size_t)n0 * pin, cnt * pin * 4, hipMemcpyHostToDevice,
+                           D->stream));
+    if ((rc = run_device_launch(m, D->stage_in, cnt, H, W, D->stage_out, D->stream, dmp, nullptr))) return rc;
+    HIP_TRY(hipMemcpyAsync(logits + (size_t)n0 * pout, D->stage_out, cnt * pout * 4, hipMemcpyDeviceToHost,
+                           D->stream));
+    HIP_TRY(hipStreamSynchronize(D->stream));
+  }
   return BNN_OK;
 }
 
@@ -770,11 +810,20 @@ int run_host(const ModelR* m, const float* input, int N, int H, int W, float* lo
 // its own image, its logits inside the image stitched into the map.  The
 // enc1 kernel reads the patches straight out of the cube and the head
 // writes the map (scene mode), in launches of whole patch rows.
-int run_patched_device(const ModelR* m, const float* d_cube, int H, int W, float* d_map, int P, hipStream_t s) {
+int check_patched(const ModelR* m, int H, int W, int P) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   if (P < 16 || P % 16) return set_err(BNN_EARG, "patch size %d must be a positive multiple of 16", P);
   if (H <= 0 || W <= 0) return set_err(BNN_EARG, "bad image size %dx%d", H, W);
-  if ((size_t)m->n_bands * H * W * 4 >= 0x7FFFFFF0ull) return set_err(BNN_EARG, "cube >= 2 GiB");
+  // one row of patches must fit a launch (strips are whole patch rows)
+  if ((size_t)m->n_bands * P * W * 4 >= kLaunchBytes)
+    return set_err(BNN_EARG, "one row of %dx%d patches of a %d-wide image exceeds a launch (2 GiB)", P, P, W);
+  return BNN_OK;
+}
+
+// a cube the kernels can address in place (32-bit byte offsets)
+bool cube_in_place(const ModelR* m, int H, int W) { return (size_t)m->n_bands * H * W * 4 < kLaunchBytes; }
+
+int run_patched_rows(const ModelR* m, const float* d_cube, int H, int W, float* d_map, int P, hipStream_t s) {
   const int prows = (H + P - 1) / P, pcols = (W + P - 1) / P;
   // about 1024 patches per launch
   const int rows_per = std::max(1, 1024 / pcols);
@@ -787,15 +836,61 @@ int run_patched_device(const ModelR* m, const float* d_cube, int H, int W, float
   return BNN_OK;
 }
 
-int run_patched_host(const ModelR* m, const float* cube, int H, int W, float* map, int P) {
-  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+// A cube of 2 GiB or more, by strips: R whole patch rows (R*P image rows,
+// fewer at the bottom edge) at a time, copied into a sub-cube [nb][rows][W]
+// and run as an image of `rows` rows; its map rows [ncls][rows][W] go to the
+// full map, one contiguous run per class since a strip spans the width.
+// Every launch then addresses at most one strip.  A host cube is copied
+// band by band (each band's strip rows are contiguous).
+int run_patched_strips(const ModelR* m, const float* cube, bool host_cube, int H, int W, float* map, bool host_map,
+                       int P, hipStream_t s) {
   BnnReactDevice* D = m->dev;
-  const size_t nin = (size_t)m->n_bands * H * W, nout = (size_t)m->n_classes * H * W;
+  const int nb = m->n_bands, ncls = m->n_classes;
+  const int prows = (H + P - 1) / P;
+  const size_t row_bytes = (size_t)nb * P * W * 4;
+  // strips of about 256 MB of input
+  const int R = std::max(1, (int)std::min<size_t>(prows, (256u << 20) / row_bytes));
   int rc;
+  if ((rc = grow(&D->strip_in, &D->strip_in_cap, row_bytes * R))) return rc;
+  if ((rc = grow(&D->strip_out, &D->strip_out_cap, (size_t)ncls * R * P * W * 4))) return rc;
+  for (int pr0 = 0; pr0 < prows; pr0 += R) {
+    const int nr = std::min(R, prows - pr0);
+    const int r0 = pr0 * P, rows = std::min(nr * P, H - r0);
+    const size_t band = (size_t)rows * W;
+    if (host_cube) {
+      for (int b = 0; b < nb; ++b)
+        HIP_TRY(hipMemcpyAsync(D->strip_in + b * band, cube + ((size_t)b * H + r0) * W, band * 4,
+                               hipMemcpyHostToDevice, s));
+    } else {
+      HIP_TRY(hipMemcpy2DAsync(D->strip_in, band * 4, cube + (size_t)r0 * W, (size_t)H * W * 4, band * 4, nb,
+                               hipMemcpyDeviceToDevice, s));
+    }
+    if ((rc = run_patched_rows(m, D->strip_in, rows, W, D->strip_out, P, s))) return rc;
+    for (int c = 0; c < ncls; ++c)
+      HIP_TRY(hipMemcpyAsync(map + ((size_t)c * H + r0) * W, D->strip_out + c * band, band * 4,
+                             host_map ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice, s));
+    if (host_map) HIP_TRY(hipStreamSynchronize(s));
+  }
+  return BNN_OK;
+}
+
+int run_patched_device(const ModelR* m, const float* d_cube, int H, int W, float* d_map, int P, hipStream_t s) {
+  int rc;
+  if ((rc = check_patched(m, H, W, P))) return rc;
+  if (cube_in_place(m, H, W)) return run_patched_rows(m, d_cube, H, W, d_map, P, s);
+  return run_patched_strips(m, d_cube, false, H, W, d_map, false, P, s);
+}
+
+int run_patched_host(const ModelR* m, const float* cube, int H, int W, float* map, int P) {
+  int rc;
+  if ((rc = check_patched(m, H, W, P))) return rc;
+  BnnReactDevice* D = m->dev;
+  if (!cube_in_place(m, H, W)) return run_patched_strips(m, cube, true, H, W, map, true, P, D->stream);
+  const size_t nin = (size_t)m->n_bands * H * W, nout = (size_t)m->n_classes * H * W;
   if ((rc = grow(&D->stage_in, &D->stage_in_cap, nin * 4))) return rc;
   if ((rc = grow(&D->stage_out, &D->stage_out_cap, nout * 4))) return rc;
   HIP_TRY(hipMemcpyAsync(D->stage_in, cube, nin * 4, hipMemcpyHostToDevice, D->stream));
-  if ((rc = run_patched_device(m, D->stage_in, H, W, D->stage_out, P, D->stream))) return rc;
+  if ((rc = run_patched_rows(m, D->stage_in, H, W, D->stage_out, P, D->stream))) return rc;
   HIP_TRY(hipMemcpyAsync(map, D->stage_out, nout * 4, hipMemcpyDeviceToHost, D->stream));
   HIP_TRY(hipStreamSynchronize(D->stream));
   return BNN_OK;
@@ -848,7 +943,7 @@ int run_file(const ModelR* m, FILE* f, int H, int W, float* logits, int P) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   int rc;
   if (!P && (rc = check_shape(m, 1, H, W))) return rc;
-  if (P && (size_t)m->n_bands * H * W * 4 >= 0x7FFFFFF0ull) return set_err(BNN_EARG, "cube >= 2 GiB");
+  if (P && (rc = check_patched(m, H, W, P))) return rc;
   BnnReactDevice* D = m->dev;
   const size_t nout = (size_t)m->n_classes * H * W;
   if ((rc = stream_cube(D, f, m->n_bands, H, W))) return rc;

@@ -171,6 +171,42 @@ def test_react_patched(tmp_path, rorc):
     eng.close()
 
 
+def test_react_past_launch_limit(tmp_path):
+    """Inputs past the 2 GiB one launch addresses: a batch of 4400 patches
+    (2.16 GB) runs as two launches from host and from device pointers, and a
+    2080 x 2160 x 120 cube (2.16 GB) runs patch-wise in strips of whole patch
+    rows, each staged as a sub-cube.  The batch equals batches of 1024 bit
+    for bit, the maps the batch forward of the host-cut patches, stitched."""
+    import torch
+    from bnns_to_c_amd import scene
+    b = synth.make_blob_react(seed=40, base=8)
+    eng, _ = _engine(tmp_path, b)
+    N = 4400
+    x = synth.make_input(41, N)
+    assert x.nbytes >= 2 ** 31
+    small = np.concatenate([eng.forward_batch(x[i:i + 1024]) for i in range(0, N, 1024)])
+    assert _same(eng.forward_batch(x), small)
+    d_x = torch.from_numpy(x).cuda()
+    del x
+    d_o = torch.full((N, 3, 32, 32), float("nan"), device="cuda")
+    eng.forward_device(d_x.data_ptr(), N, 32, 32, d_o.data_ptr())
+    torch.cuda.synchronize()
+    assert _same(d_o.cpu().numpy(), small)
+    del d_x, d_o, small
+    H, W, P = 2080, 2160, 32
+    cube = np.random.default_rng(42).standard_normal((120, H, W), dtype=np.float32)
+    assert cube.nbytes >= 2 ** 31
+    want = scene.stitch(eng.forward_batch(scene.cut(cube, P)), H, W)
+    assert _same(eng.forward_patched(cube, P), want)
+    d_cube = torch.from_numpy(cube).cuda()
+    del cube
+    d_map = torch.full((3, H, W), float("nan"), device="cuda")
+    eng.forward_patched_device(d_cube.data_ptr(), H, W, d_map.data_ptr(), P)
+    torch.cuda.synchronize()
+    assert _same(d_map.cpu().numpy(), want)
+    eng.close()
+
+
 def test_react_device_batch(tmp_path, rorc):
     import torch
     b = synth.make_blob_react(seed=14, base=16)
