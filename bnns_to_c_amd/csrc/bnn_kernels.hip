@@ -2442,7 +2442,7 @@ __global__ __launch_bounds__(kBlock) void k_react_in_tail(const ReactTailArgs a)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int co = c0 + j;
-      if (co >= a.cout) break;
+      if (co >= a.cout) continue;
       const long at = ((long)n * a.cout + co) * HW + p;
       const float res = acc[j];
       if (a.f32b) a.f32b[at] = res;
