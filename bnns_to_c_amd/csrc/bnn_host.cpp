@@ -388,6 +388,15 @@ bool mid_mode() {
   return !(e && !strcmp(e, "0"));
 }
 
+// The certified first conv (launch_real_cert) makes the v1 enc1.conv1 bits
+// whenever its shape fits (real_cert_fits); BNN_CERT=0 keeps the exact-order
+// matrix-core kernel for them.  The debug forward's float conv output always
+// comes from the exact-order kernel.
+bool cert_mode() {
+  const char* e = getenv("BNN_CERT");
+  return !(e && !strcmp(e, "0"));
+}
+
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
   return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || mfma_nchunk(L.cw0, L.cw1) >= 4);
 }
@@ -410,6 +419,10 @@ struct BnnDevice {
   int rcin = 0, rcout = 0;
   uint64_t* rwm = nullptr;  // lane-mask weights (v1: all signs +-1, else null and rw is used)
   float *rw = nullptr, *ralpha = nullptr, *rA = nullptr, *rB = nullptr, *rslope = nullptr, *rrsign = nullptr;
+  // the certified first conv's tables (v1, all signs +-1, cin <= 128, cin % 4 == 0), and cert_mode()
+  uint16_t* rcwb = nullptr;
+  uint32_t* rcws = nullptr;
+  bool cert = false;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   bool mid = false;  // the fused middle applies (mid_fits at load, and mid_mode())
   float *hw = nullptr, *hb = nullptr;
@@ -547,6 +560,13 @@ int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
     std::vector<uint64_t> wm(real_conv_masks_len(c.Cout, c.Cin));
     real_conv_masks(c.wsign, c.Cout, c.Cin, wm.data());
     if ((rc = dev_upload(D, &D->rwm, wm.data(), wm.size()))) return rc;
+    if (c.Cin <= 128 && c.Cin % 4 == 0) {
+      std::vector<uint16_t> cb(real_cert_b_len(c.Cout));
+      std::vector<uint32_t> cs(real_cert_s_len(c.Cout));
+      real_cert_tables(c.wsign, c.Cout, c.Cin, cb.data(), cs.data());
+      if ((rc = dev_upload(D, &D->rcwb, cb.data(), cb.size()))) return rc;
+      if ((rc = dev_upload(D, &D->rcws, cs.data(), cs.size()))) return rc;
+    }
   } else {
     std::vector<float> w(real_conv_weights_len(c.Cout, c.Cin));
     real_conv_weights(c.wsign, c.Cout, c.Cin, w.data());
@@ -648,6 +668,7 @@ int build_device(Model* m, const StemPart* st = nullptr) {
     if ((rc = upload_bconv(D, &D->d2[i], m->dec_conv2[i], 0, &m->dec_act2[i], nullptr))) return rc;
   }
   D->mid = mid_mode() && mid_fits(D);
+  D->cert = cert_mode() && D->rcwb && D->rcws;
   if (D->mid) {
     const auto L = mid_layers(D);
     const Conv* cv[kMidLayers] = {&m->enc_conv1[2], &m->enc_conv2[2], &m->enc_conv1[3], &m->enc_conv2[3],
@@ -791,6 +812,17 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     if (D->stem) {
       HIP_TRY(launch_stem(ra, st));
       if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
+    } else if (D->cert && real_cert_fits(D->rcin, W, sc ? sc->sW : W)) {
+      if (dump) {
+        RealArgs rf = ra;
+        rf.out = nullptr;
+        HIP_TRY(launch_real(rf, st));
+      }
+      ra.f32 = nullptr;
+      ra.cwb = D->rcwb;
+      ra.cws = D->rcws;
+      HIP_TRY(launch_real_cert(ra, st));
+      if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
     } else {
       HIP_TRY(launch_real(ra, st));
       if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;

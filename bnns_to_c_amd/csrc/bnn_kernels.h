@@ -105,6 +105,10 @@ struct RealArgs {
   const float* x;
   const float* w;       // [ceil(cout/G)][cin][9][G] (vector-ALU kernel)
   const uint64_t* wm;   // [ceil(cout/16)][cin padded][3] lane masks (matrix-core kernel), or null
+  // certified fp16 matrix-core kernel (launch_real_cert): operand table and
+  // sign masks, real_cert_tables(); null leaves that kernel unused
+  const uint16_t* cwb;
+  const uint32_t* cws;
   const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;
@@ -177,6 +181,38 @@ inline void real_conv_masks(const int8_t* wsign, int cout, int cin, uint64_t* ou
       for (int t = 0; t < 9; ++t)
         if (wsign[((size_t)co * cin + ci) * 9 + t] > 0)
           out[((size_t)(co / 16) * cp + ci) * 3 + t / 4] |= 1ull << (16 * (t % 4) + co % 16);
+}
+
+// Tables of the certified first conv (all signs +-1, cin <= 128):
+//  * operand table [16-channel group][wave w][tap][lane][8] fp16 bit
+//    patterns: lane l holds output channel 16 g + l % 16 and, in element j,
+//    input channel cin / 4 * w + 4 j + l / 16 when 4 j + l / 16 < cin / 4
+//    (+1 -> 0x3C00, -1 -> 0xBC00; other elements and channels past cout -> 0);
+//  * sign masks [cout padded to 16][tap][4] words: bit ci % 32 of word
+//    ci / 32 set iff the weight is +1.
+inline size_t real_cert_b_len(int cout) { return (size_t)((cout + 15) / 16) * 4 * 9 * 64 * 8; }
+inline size_t real_cert_s_len(int cout) { return (size_t)((cout + 15) / 16) * 16 * 9 * 4; }
+inline void real_cert_tables(const int8_t* wsign, int cout, int cin, uint16_t* b, uint32_t* s) {
+  const int ng = (cout + 15) / 16;
+  for (int g = 0; g < ng; ++g)
+    for (int w = 0; w < 4; ++w)
+      for (int t = 0; t < 9; ++t)
+        for (int l = 0; l < 64; ++l)
+          for (int j = 0; j < 8; ++j) {
+            const int co = 16 * g + l % 16, cl = 4 * j + l / 16, ci = cin / 4 * w + cl;
+            uint16_t v = 0;
+            if (co < cout && cl < cin / 4) v = wsign[((size_t)co * cin + ci) * 9 + t] > 0 ? 0x3C00 : 0xBC00;
+            b[((((size_t)g * 4 + w) * 9 + t) * 64 + l) * 8 + j] = v;
+          }
+  for (size_t i = 0; i < real_cert_s_len(cout); ++i) s[i] = 0;
+  for (int co = 0; co < cout; ++co)
+    for (int t = 0; t < 9; ++t)
+      for (int ci = 0; ci < cin && ci < 128; ++ci)
+        if (wsign[((size_t)co * cin + ci) * 9 + t] > 0) s[((size_t)co * 9 + t) * 4 + ci / 32] |= 1u << (ci % 32);
+}
+// whether launch_real_cert takes a layer of this shape
+inline bool real_cert_fits(int cin, int W, int rowlen) {
+  return cin >= 4 && cin <= 128 && cin % 4 == 0 && W >= 4 && W <= 32 && W % 4 == 0 && rowlen % 4 == 0;
 }
 
 // 1x1 stem weights (v2 models; signs +1, -1 or 0): 64-bit lane masks
@@ -402,6 +438,9 @@ struct MidArgs {
   int N, ldsw;
 };
 hipError_t launch_mid(const MidArgs& a, bool dump, hipStream_t s);
+
+// the certified first conv (bits only; RealArgs with cwb, cws, out, no f32)
+hipError_t launch_real_cert(const RealArgs& a, hipStream_t s);
 
 // The 1x1 head as its own kernel (heads over more than 32 channels, which
 // one epilogue group cannot hold): input the head layer's packed bits

@@ -44,33 +44,6 @@ namespace {
 constexpr int kBlock = 256;
 
 
-// Where the real conv finds patch n: in a batch [N][cin][H][W], or in one
-// scene cube [cin][sH][sW] cut into H x W patches (pcols per row), where the
-// rows and columns of an edge patch past the cube count as outside (0).
-struct InGeom {
-  size_t base, cstride;  // element offsets: patch origin, one channel
-  int rstride;           // one row
-  int ylim, xlim;        // rows / columns of the patch inside the input
-};
-__device__ __forceinline__ InGeom in_geom(const RealArgs& a, int n) {
-  InGeom g;
-  if (a.pcols > 0) {
-    const int pr = a.prow0 + n / a.pcols, pc = n % a.pcols;
-    g.base = (size_t)pr * a.H * a.sW + (size_t)pc * a.W;
-    g.cstride = (size_t)a.sH * a.sW;
-    g.rstride = a.sW;
-    g.ylim = min(a.H, a.sH - pr * a.H);
-    g.xlim = min(a.W, a.sW - pc * a.W);
-  } else {
-    g.base = (size_t)n * a.cin * a.H * a.W;
-    g.cstride = (size_t)a.H * a.W;
-    g.rstride = a.W;
-    g.ylim = a.H;
-    g.xlim = a.W;
-  }
-  return g;
-}
-
 // ------------------------------------------------------------------------
 // real-input conv + real fold
 // ------------------------------------------------------------------------

@@ -1,0 +1,487 @@
+// bnn_real_cert.hip - the v1 first conv (real input, +-1 weights, 3x3,
+// pad 1, real fold) with certified output bits on the fp16 matrix cores.
+//
+// The reference sums each in-image tap's input channels in order, then the
+// taps in row-major order, all in fp32 (csrc/bnn_conv_realin.c:98-111),
+// scales by alpha and folds (csrc/bnn_fold.c:62-77); only the fold's bit
+// leaves the layer.  This kernel computes an approximation v' of the tap sum
+// v together with a bound E >= |v' - v| that holds for every input, and
+// evaluates the fold at v' - E and v' + E.  alpha * v, A * o + B, the PReLU
+// branch and the final add are each monotone on either side of z = 0, so
+// when both ends land on the same side with the same bit, that bit is the
+// reference's.  Any other output is recomputed in the reference's order from
+// the input rows the block still holds in LDS.
+//
+// v': per input row and wave (32 input channels), x is scaled by 2^(10 - e),
+// e the exponent of the largest |x| there, and split into two integer digits
+// d1 = rint(u), d0 = rint((u - d1) * 2048), |d1| <= 2048, |d0| <= 1024, each
+// exact in fp16.  The f32 16x16x32 f16 MFMA sums digits times +-1 over three
+// taps and 32 channels: every partial sum is an integer below 2^18, so the
+// matrix core's result is exact whatever its internal order.  The digit sums
+// are recombined (2048 Zh + Zl) and scaled back by 2^(e - 21) in fp32.
+//
+// E = (cin + 16) 2^-24 (1 + 2^-8) A + (1 + 2^-8) Q + 2^-110, rounded up, with
+//  * A = sum |x| over the output's 3 x 3 x cin window;
+//  * Q = half a grid step 2^(e-21) per term: 48 * 2^(e-21) per (input row,
+//    wave) of the window;
+//  * the reference's roundings: a tap's sequential sum of cin terms is
+//    within gamma(cin - 1) A_tap of the exact one, the tap sum adds
+//    gamma(8) A (gamma(n) = n 2^-24 / (1 - n 2^-24));
+//  * this kernel's: recombination, two row adds, three adds of the
+//    four-wave reduction (each at most 2^-24 (A + Q)); 2^-8 covers the
+//    gamma denominators and the roundings of A itself, 2^-110 underflow.
+//
+// Work split: one block of four waves per (patch, 16-channel group); wave w
+// converts a quarter of the input channels.  Rows stream through a ring of
+// four LDS row buffers by 16-byte LDS DMA, one row ahead.  Each step
+// converts one input row into digits (the shifted operands of the kx = 0 and
+// kx = 2 taps come from DPP row shifts, the 16-lane rows being the operand's
+// pixel rows), runs 36 MFMAs into per-ky digit sums and adds them into three
+// rolling output-row partials.  An output row is complete one step after its
+// last input row: each wave writes its partial, its window sum of |x| and
+// its Q to LDS (plain stores; float atomics on LDS are several times slower
+// here), and after a barrier each wave adds the four in wave order for a
+// quarter of the row, folds, certifies and writes the bits.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bnn_device.h"
+#include "bnn_kernels.h"
+
+namespace bnn {
+namespace {
+
+typedef _Float16 cert_f16x8 __attribute__((ext_vector_type(8)));
+typedef float cert_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t cert_u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kCertRing = 4;                  // input rows in LDS
+constexpr uint32_t kCertFar = 0x7FFFFFF0u;    // DMA offset that reads zeros
+
+__device__ __forceinline__ cert_f16x8 as_h8(cert_u32x4 v) { return __builtin_bit_cast(cert_f16x8, v); }
+
+template <int CTRL, bool ZERO>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, 0xF, 0xF, ZERO);
+}
+constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121, kRor15 = 0x12F;
+
+// Operands of the pixel to the left (kx = 0) and right (kx = 2): lane p of a
+// 16-lane row holds pixel 16 s + p of segment s.  Pixel -1 and pixel 32 are
+// outside every row of width <= 32 and read 0.
+__device__ __forceinline__ void shift_left(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[0][i] = dpp<kShr1, true>(0u, a[0][i]);
+    o[1][i] = dpp<kShr1, false>(dpp<kRor1, false>(0u, a[0][i]), a[1][i]);
+  }
+}
+__device__ __forceinline__ void shift_right(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[0][i] = dpp<kShl1, false>(dpp<kRor15, false>(0u, a[1][i]), a[0][i]);
+    o[1][i] = dpp<kShl1, true>(0u, a[1][i]);
+  }
+}
+
+__device__ __forceinline__ float f32_of(uint32_t b) { return __builtin_bit_cast(float, b); }
+__device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// the reference's real fold of tap sum v (csrc/bnn_fold.c:62-77, A * o + B
+// fused as the reference build does); z is the value before the PReLU branch
+__device__ __forceinline__ bool fold_bit(float v, float al, float A, float B, float sl, float rs, float& z) {
+  const float o = __fmul_rn(al, v);
+  z = __fmaf_rn(A, o, B);
+  const float h = z < 0.0f ? __fmul_rn(sl, z) : z;
+  return __fadd_rn(h, rs) > 0.0f;
+}
+
+// the LDS byte offset of (channel ci, column x) in a row buffer: 16-byte
+// column groups of channels with bit 1 set are swapped in halves (group
+// g -> g ^ 4), which puts the four lane rows of an operand read in four
+// different 16-bank quarters
+__device__ __forceinline__ uint32_t row_off(int ci, int x) {
+  return (uint32_t)ci * 128u + ((uint32_t)((x >> 2) ^ (((ci >> 1) & 1) << 2)) << 4) + (uint32_t)(x & 3) * 4u;
+}
+__device__ __forceinline__ void block_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// s_waitcnt with lgkmcnt 0 and vmcnt untouched (63), or vmcnt N (< 16) and
+// lgkmcnt 0
+constexpr int kWaitLgkm0 = 0xF | (7 << 4) | (0 << 8) | (3 << 14);
+
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (0 << 8));
+}
+extern __shared__ __attribute__((aligned(16))) float cert_lds[];
+
+// sum over the four 16-lane rows, in every lane (two permlane swaps)
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto r16 = __builtin_amdgcn_permlane16_swap(bits_of(x), bits_of(x), false, false);
+  const float y = __fadd_rn(f32_of(r16[0]), f32_of(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(bits_of(y), bits_of(y), false, false);
+  return __fadd_rn(f32_of(r32[0]), f32_of(r32[1]));
+}
+// per-pixel value (segment s in v[s]) plus its left and right neighbours
+__device__ __forceinline__ void window3(const float (&v)[2], float (&o)[2]) {
+  const uint32_t a0 = bits_of(v[0]), a1 = bits_of(v[1]);
+  const float l0 = f32_of(dpp<kShr1, true>(0u, a0));
+  const float l1 = f32_of(dpp<kShr1, false>(dpp<kRor1, false>(0u, a0), a1));
+  const float r0 = f32_of(dpp<kShl1, false>(dpp<kRor15, false>(0u, a1), a0));
+  const float r1 = f32_of(dpp<kShl1, true>(0u, a1));
+  o[0] = __fadd_rn(__fadd_rn(l0, v[0]), r0);
+  o[1] = __fadd_rn(__fadd_rn(l1, v[1]), r1);
+}
+// a wave's partial of one output row: (pixel, channel) at
+// ((px / 4) * 16 + c) * 4 + px % 4, so a lane's four MFMA result rows are
+// one 16-byte store
+__device__ __forceinline__ int part_idx(int px, int c) { return ((px >> 2) * 16 + c) * 4 + (px & 3); }
+
+// Wave w converts input channels cpw * w .. cpw * w + cpw - 1 (cpw = cin / 4):
+// element j of lane (p, gq) is channel cpw * w + 4 j + gq, column 16 s + p;
+// elements past the wave's channels read as 0.  GUARD: such elements may
+// occur for j < 7 (cpw < 28); otherwise only element 7 can be one.
+template <bool GUARD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int p = lane & 15, gq = lane >> 4;
+  const int n = blockIdx.x, grp = blockIdx.y;
+  const int H = a.H, W = a.W, cin = a.cin, cpw = cin >> 2;
+  const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
+  float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [wave][512]
+  float* absw = opart + 4 * 512;                         // [wave][32]
+  float* qw = absw + 4 * 32;                             // [wave]
+  typedef __attribute__((address_space(3))) float* lds_f32;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_f32)cert_lds;
+
+  // this wave's operand table: B[t] for tap t
+  cert_f16x8 Bw[9];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(a.cwb) + ((size_t)(grp * 4 + wv) * 9) * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const uint4 v = src[t * 64];
+      Bw[t] = as_h8((cert_u32x4){v.x, v.y, v.z, v.w});
+    }
+  }
+
+  // DMA: wave w issues the row's 1 KiB loads k = w, w + 4, ... < nld; lane L
+  // of load k fetches 16 bytes: channel 8 k + L / 8, column group (L % 8)
+  // swapped as in row_off
+  const InGeom ig = in_geom(a, n);
+  const uint32_t rstr4 = (uint32_t)ig.rstride * 4u;
+  uint32_t doff[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int k = wv + 4 * m;
+    const int ci = 8 * k + (lane >> 3);
+    const int g4 = (lane & 7) ^ (((ci >> 1) & 1) << 2);
+    const bool ok = k < nld && ci < cin && 4 * g4 < ig.xlim;
+    doff[m] = ok ? (uint32_t)(ig.base + (size_t)ci * ig.cstride + 4 * g4) * 4u : kCertFar;
+  }
+  const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
+  auto uni = [](uint32_t v) __attribute__((always_inline)) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+  typedef uint32_t dma_u32x4 __attribute__((ext_vector_type(4)));
+  const dma_u32x4 xsrc = {uni((uint32_t)xaddr), uni((uint32_t)(xaddr >> 32) & 0xFFFFu), uni(xbytes), 0x00020000u};
+  auto issue = [&](int y) __attribute__((always_inline)) {
+    const uint32_t slot = lds0 + (uint32_t)(y % kCertRing) * rb;
+    const bool inrow = y < ig.ylim;
+    const uint32_t ro = (uint32_t)y * rstr4;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int k = wv + 4 * m;
+      if (k >= nld) break;
+      const uint32_t m0v = uni(slot + (uint32_t)k * 1024u);
+      const uint32_t vo = (inrow && doff[m] != kCertFar) ? doff[m] + ro : kCertFar;
+      const dma_u32x4 rd = xsrc;
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :
+                   : "s"(m0v), "v"(vo), "s"(rd)
+                   : "memory");
+    }
+  };
+
+  // conversion reads and the lane's valid elements
+  uint32_t rdoff[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) rdoff[s] = row_off(cpw * wv + gq, 16 * s + p);
+  uint32_t jvalid = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) jvalid |= (4 * j + gq < cpw ? 1u : 0u) << j;
+
+  // finalize: lane -> output channel fc, pixels fpx0 and fpx0 + 1
+  const int fc = lane & 15, fq = lane >> 4;
+  const int fpx0 = 8 * wv + 2 * fq;
+  const int co = 16 * grp + fc;
+  const bool chan = co < a.cout;
+  const float f_al = a.alpha[co], f_A = a.A[co], f_B = a.B[co], f_sl = a.slope[co], f_rs = a.rsign[co];
+  // (cin + 16) 2^-24 (1 + 2^-9), rounding up (the 2^-9 also covers the
+  // round-to-nearest steps of A, Q and E below)
+  const float cA = (float)(cin + 16) * 0x1p-24f * (1.0f + 0x1p-9f);
+  const int cwo = (a.cout + 31) >> 5;
+  const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
+  typedef const __attribute__((address_space(4))) uint32_t* const_u32;
+  const const_u32 wsg = (const_u32)a.cws;
+
+  issue(0);
+
+  cert_f32x4 op[2], oc[2], on[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) op[s] = oc[s] = on[s] = (cert_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  float ab1[2] = {0.0f, 0.0f}, ab2[2] = {0.0f, 0.0f};  // window sums of rows yi - 1, yi - 2
+  float q1 = 0.0f, q2 = 0.0f;
+
+  for (int yi = 0; yi <= H; ++yi) {
+    const bool has = yi < H;
+    // row yi landed, this wave's LDS traffic done, then every wave's
+    wait_vm_lgkm<0>();
+    block_barrier();
+    if (yi + 1 < H) issue(yi + 1);
+
+    float abn[2] = {0.0f, 0.0f}, qn = 0.0f;
+    if (has) {
+      const float* row = cert_lds + (size_t)(yi % kCertRing) * rb / 4;
+      float xv[2][8];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = row[(rdoff[s] + (uint32_t)j * 512u) / 4];
+          xv[s][j] = (GUARD || j == 7) ? ((jvalid >> j) & 1u ? v : 0.0f) : v;
+        }
+      // the wave's largest |x|: within each 16-lane row by rotation, then the
+      // four rows through scalar registers (|x| bits order as unsigned
+      // integers; a NaN input reaches v' as NaN and is recomputed)
+      float m = 0.0f, as[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        m = fmaxf(m, fmaxf(fabsf(xv[0][j]), fabsf(xv[1][j])));
+        as[0] = __fadd_rn(as[0], fabsf(xv[0][j]));
+        as[1] = __fadd_rn(as[1], fabsf(xv[1][j]));
+      }
+      uint32_t mb = bits_of(m);
+      mb = max(mb, dpp<0x128, false>(mb, mb));  // row_ror:8
+      mb = max(mb, dpp<0x124, false>(mb, mb));  // row_ror:4
+      mb = max(mb, dpp<0x122, false>(mb, mb));  // row_ror:2
+      mb = max(mb, dpp<kRor1, false>(mb, mb));
+      const uint32_t mw = max(max((uint32_t)__builtin_amdgcn_readlane((int)mb, 0), (uint32_t)__builtin_amdgcn_readlane((int)mb, 16)),
+                              max((uint32_t)__builtin_amdgcn_readlane((int)mb, 32), (uint32_t)__builtin_amdgcn_readlane((int)mb, 48)));
+      const bool finite = mw < 0x7F800000u;
+      const int e = finite ? max((int)(mw >> 23) - 127, -100) : 127;
+      const float sc = f32_of((uint32_t)(127 + 10 - e) << 23);
+      const float sb = f32_of((uint32_t)(127 + e - 21) << 23);
+      qn = finite ? 48.0f * sb : __builtin_inff();
+      // sum |x| over the wave's channels per pixel, then over the three taps
+      // of a row
+      float ap[2] = {rows_sum(as[0]), rows_sum(as[1])};
+      window3(ap, abn);
+
+      // digits, packed two per register
+      cert_u32x4 hi[2], lo[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float u0 = __fmul_rn(xv[s][2 * i], sc), u1 = __fmul_rn(xv[s][2 * i + 1], sc);
+          const float d10 = __builtin_rintf(u0), d11 = __builtin_rintf(u1);
+          const float d00 = __builtin_rintf(__fmul_rn(__fsub_rn(u0, d10), 2048.0f));
+          const float d01 = __builtin_rintf(__fmul_rn(__fsub_rn(u1, d11), 2048.0f));
+          hi[s][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d10, d11));
+          lo[s][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d00, d01));
+        }
+      // digit sums per ky (taps ky * 3 + kx), kx = 1 first
+      cert_f32x4 zh[3][2], zl[3][2];
+      const cert_f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[s]), Bw[ky * 3 + 1], z4, 0, 0, 0);
+          zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[s]), Bw[ky * 3 + 1], z4, 0, 0, 0);
+        }
+      {
+        cert_u32x4 sh[2], sl[2];
+        shift_left(hi, sh);
+        shift_left(lo, sl);
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sh[s]), Bw[ky * 3], zh[ky][s], 0, 0, 0);
+            zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sl[s]), Bw[ky * 3], zl[ky][s], 0, 0, 0);
+          }
+      }
+      {
+        cert_u32x4 sh[2], sl[2];
+        shift_right(hi, sh);
+        shift_right(lo, sl);
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sh[s]), Bw[ky * 3 + 2], zh[ky][s], 0, 0, 0);
+            zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sl[s]), Bw[ky * 3 + 2], zl[ky][s], 0, 0, 0);
+          }
+      }
+      // input row yi feeds output rows yi + 1 (ky 0), yi (ky 1), yi - 1 (ky 2)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          on[s][r] = __fmul_rn(__fmaf_rn(zh[0][s][r], 2048.0f, zl[0][s][r]), sb);
+          oc[s][r] = __fmaf_rn(__fmaf_rn(zh[1][s][r], 2048.0f, zl[1][s][r]), sb, oc[s][r]);
+          op[s][r] = __fmaf_rn(__fmaf_rn(zh[2][s][r], 2048.0f, zl[2][s][r]), sb, op[s][r]);
+        }
+    }
+
+    if (yi >= 1) {
+      // output row r = yi - 1 is complete in op: each wave leaves its partial,
+      // its window sum of |x| and its quantisation bound in LDS
+      const int r = yi - 1;
+      float* mine = opart + wv * 512;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        *reinterpret_cast<float4*>(&mine[part_idx(16 * s + 4 * gq, p)]) = make_float4(op[s][0], op[s][1], op[s][2], op[s][3]);
+      if (gq == 0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) absw[wv * 32 + 16 * s + p] = __fadd_rn(__fadd_rn(ab2[s], ab1[s]), abn[s]);
+      }
+      if (lane == 0) qw[wv] = __fadd_rn(__fadd_rn(q2, q1), qn);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      block_barrier();
+
+      // finalize: the four partials in wave order
+      float v[2] = {0.0f, 0.0f}, Aw[2] = {0.0f, 0.0f};
+      const int i0 = part_idx(fpx0, fc);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float2 t = *reinterpret_cast<const float2*>(&opart[w * 512 + i0]);
+        const float2 u = *reinterpret_cast<const float2*>(&absw[w * 32 + fpx0]);
+        v[0] = __fadd_rn(v[0], t.x);
+        v[1] = __fadd_rn(v[1], t.y);
+        Aw[0] = __fadd_rn(Aw[0], u.x);
+        Aw[1] = __fadd_rn(Aw[1], u.y);
+      }
+      const float4 qq = *reinterpret_cast<const float4*>(qw);
+      const float Qs = __fadd_rn(__fadd_rn(qq.x, qq.y), __fadd_rn(qq.z, qq.w));
+      bool bit[2], unc[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        // E, then room for rounding v -+ E to nearest
+        const float E = __fadd_rn(__fmaf_rn(cA, Aw[k], __fmul_rn(Qs, 1.0f + 0x1p-9f)), 0x1p-110f);
+        const float Ev = __fmaf_rn(fabsf(v[k]), 0x1p-22f, __fmul_rn(E, 1.0f + 0x1p-20f));
+        float zl_, zh_;
+        const bool bl = fold_bit(__fsub_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zl_);
+        const bool bh = fold_bit(__fadd_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zh_);
+        const bool ok = bl == bh && (zl_ < 0.0f) == (zh_ < 0.0f) && !__builtin_isnan(zl_) && !__builtin_isnan(zh_);
+        bit[k] = bl && chan;
+        unc[k] = !ok && chan && fpx0 + k < W;
+      }
+      uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
+      uint64_t um[2] = {__ballot(unc[0]), __ballot(unc[1])};
+
+      // uncertain outputs: the reference's order, lane t < 9 summing tap t
+      // over the channels from the LDS rows r - 1 .. r + 1
+      while (um[0] | um[1]) {
+        const int which = um[0] ? 0 : 1;
+        const int li = __builtin_ctzll(um[which]);
+        um[which] &= um[which] - 1;
+        const int upx = 8 * wv + 2 * (li >> 4) + which, uco = 16 * grp + (li & 15);
+        // the channel's 36 sign-mask words in one batch of scalar loads; lane
+        // t takes tap t's four
+        uint32_t mw36[36];
+#pragma unroll
+        for (int i = 0; i < 36; ++i) mw36[i] = wsg[(size_t)uco * 36 + i];
+        uint32_t wk[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t t4 = 0u;
+#pragma unroll
+          for (int t = 0; t < 9; ++t) t4 = lane == t ? mw36[t * 4 + k] : t4;
+          wk[k] = t4;
+        }
+        float st = 0.0f;
+        const int ky = lane / 3, kx = lane - 3 * (lane / 3);
+        const int iy = r + ky - 1, ix = upx + kx - 1;
+        if (lane < 9 && iy >= 0 && iy < H && ix >= 0 && ix < W) {
+          // channels 4 m, 4 m + 1 use column offset c0, 4 m + 2, 4 m + 3 the
+          // swapped one (row_off)
+          const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
+          const float* c0 = rowp + (row_off(0, ix) >> 2);
+          const float* c1 = rowp + (row_off(2, ix) >> 2) - 64;
+#pragma unroll 4
+          for (int c4 = 0; c4 < cin; c4 += 4) {
+            const float x0 = c0[c4 * 32], x1 = c0[c4 * 32 + 32], x2 = c1[c4 * 32 + 64], x3 = c1[c4 * 32 + 96];
+            const uint32_t wd = (c4 < 32 ? wk[0] : c4 < 64 ? wk[1] : c4 < 96 ? wk[2] : wk[3]) >> (c4 & 31);
+            st = __fadd_rn(st, (wd & 1u) ? x0 : -x0);
+            st = __fadd_rn(st, (wd & 2u) ? x1 : -x1);
+            st = __fadd_rn(st, (wd & 4u) ? x2 : -x2);
+            st = __fadd_rn(st, (wd & 8u) ? x3 : -x3);
+          }
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) acc = __fadd_rn(acc, f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(st), t)));
+        // the channel's fold parameters from lane li, which holds them
+        auto from_li = [&](float f) __attribute__((always_inline)) {
+          return f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(f), li));
+        };
+        float zz;
+        const bool ub = fold_bit(acc, from_li(f_al), from_li(f_A), from_li(f_B), from_li(f_sl), from_li(f_rs), zz);
+        bm[which] = ub ? (bm[which] | (1ull << li)) : (bm[which] & ~(1ull << li));
+      }
+
+      // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k
+      if (fc < 2 && fpx0 + fc < W) {
+        const uint32_t word = (uint32_t)((fc ? bm[1] : bm[0]) >> (16 * fq)) & 0xFFFFu;
+        const int HW = H * W;
+        uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)r * W + fpx0 + fc) * cwo) + grp * 2;
+        if (whole_word) *reinterpret_cast<uint32_t*>(dst) = word;
+        else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      op[s] = oc[s];
+      oc[s] = on[s];
+      ab2[s] = ab1[s];
+      ab1[s] = abn[s];
+    }
+    q2 = q1;
+    q1 = qn;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
+  if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
+  if (!a.cwb || !a.cws || !a.out || a.f32 || a.hout) return hipErrorInvalidValue;
+  const int rowlen = a.pcols > 0 ? a.sW : a.W;
+  if (!real_cert_fits(a.cin, a.W, rowlen) || (uintptr_t)a.x % 16) return hipErrorInvalidValue;
+  const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
+  if (xbytes >= kCertFar) return hipErrorInvalidValue;
+  if (a.N >= 0x7FFFFFFF) return hipErrorInvalidValue;
+  const int nld = (a.cin + 7) / 8;
+  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4) * 4;
+  const bool guard = a.cin / 4 < 28;
+  static bool attr[2] = {false, false};
+  if (!attr[guard]) {
+    hipError_t e = guard ? hipFuncSetAttribute((const void*)k_real_cert<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)
+                         : hipFuncSetAttribute((const void*)k_real_cert<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr[guard] = true;
+  }
+  dim3 grid((unsigned)a.N, (unsigned)((a.cout + 15) / 16));
+  if (guard) hipLaunchKernelGGL((k_real_cert<true>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
+  else hipLaunchKernelGGL((k_real_cert<false>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
+  return hipGetLastError();
+}
+
+}  // namespace bnn

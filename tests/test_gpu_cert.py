@@ -1,0 +1,137 @@
+"""The certified first conv (launch_real_cert, csrc/bnn_real_cert.hip): the
+enc1.act1 bits it writes equal the checker's (csrc/bnn_conv_realin.c:98-111
+then csrc/bnn_fold.c:62-77), on inputs built so that the approximation's
+bound cannot decide many outputs and the reference-order recompute must:
+
+* every band +-1, so tap sums are integers, and each channel's fold placed
+  exactly on one integer sum: about one output in a hundred sits on z = 0;
+* bands scaled by 2^-20 .. 2^20, zero rows, and an infinity and a NaN;
+* the scene path (edge patches partly outside the cube).
+
+The debug forward reports the act1 bits of the certified kernel (its float
+conv output comes from the exact-order kernel); the plain forward's logits
+must match too, and a model loaded with BNN_CERT=0 (exact-order kernel for
+the bits) must give bit-identical logits on a larger batch.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from bnns_to_c_amd import blob as B
+from bnns_to_c_amd import engine as E
+from bnns_to_c_amd import scene
+from bnns_to_c_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _engine(tmp_path, b, name="m.blob", cert=True):
+    p = tmp_path / name
+    p.write_bytes(B.to_bytes(b))
+    old = os.environ.get("BNN_CERT")
+    if cert:
+        os.environ.pop("BNN_CERT", None)
+    else:
+        os.environ["BNN_CERT"] = "0"
+    try:
+        return E.Engine(str(p))
+    finally:
+        if old is None:
+            os.environ.pop("BNN_CERT", None)
+        else:
+            os.environ["BNN_CERT"] = old
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32) if a.dtype == np.float32 else a,
+                          np.asarray(b).view(np.uint32) if b.dtype == np.float32 else b)
+
+
+def _check(eng, model, x):
+    logits, st = eng.forward_debug(x)
+    plain = eng.forward_batch(x)
+    for n in range(x.shape[0]):
+        want, ref = model.forward(x[n], stages=True)
+        assert np.array_equal(st["enc1.act1"][n], ref["enc1.act1"]), ("enc1.act1", n)
+        assert _bits_equal(logits[n], want), ("logits", n)
+        assert _bits_equal(plain[n], want), ("plain logits", n)
+
+
+def test_cert_threshold_ties(tmp_path, orc):
+    b = synth.make_blob(seed=41)
+    rng = np.random.default_rng(42)
+    N = 2
+    x = rng.choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, 32, 32))
+    model = orc.parse(B.to_bytes(b))
+    _, ref = model.forward(x[0], stages=True)
+    conv = ref["enc1.conv1"]  # alpha * tap sum, [16][32][32]
+    act = b.enc_act1[0]
+    A = act.A.astype(np.float32)
+    Bv = act.B.copy()
+    rs = act.rsign.copy()
+    for c in range(conv.shape[0]):
+        o0 = conv[c, 5 + c, 3 + c]  # one of the patch's own outputs
+        Bv[c] = np.float32(-(A[c] * o0))
+        rs[c] = np.float32(0.0) if c % 2 == 0 else np.float32(1e-30)
+    act.B = Bv.astype(np.float32)
+    act.rsign = rs.astype(np.float32)
+    model = orc.parse(B.to_bytes(b))
+    # how many outputs the fold puts on (or within a few ulps of) z = 0
+    _, ref = model.forward(x[0], stages=True)
+    z = A[:, None, None] * ref["enc1.conv1"] + Bv[:, None, None]
+    assert (np.abs(z) <= 1e-5).sum() > 50
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
+def test_cert_wide_range_and_nonfinite(tmp_path, orc):
+    b = synth.make_blob(seed=43)
+    rng = np.random.default_rng(44)
+    N = 3
+    x = rng.standard_normal((N, 120, 32, 32), dtype=np.float32)
+    x *= (2.0 ** rng.integers(-20, 21, size=(1, 120, 1, 1))).astype(np.float32)
+    x[0, :, 7, :] = 0.0          # a zero row
+    x[1, :, :, 12] = 0.0         # a zero column
+    x[1, 3, 20, 20] = np.inf     # non-finite inputs reach the recompute
+    x[2, 77, 9, 30] = np.nan
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
+@pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16)])
+def test_cert_shapes(tmp_path, orc, base, H, W):
+    b = synth.make_blob(seed=45 + base, base=base)
+    x = synth.make_input(46 + H, 2, 120, H, W)
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
+def test_cert_vs_exact_order_batch(tmp_path):
+    b = synth.make_blob(seed=47)
+    x = synth.make_input(48, 96, 120, 32, 32)
+    x[5] *= np.float32(1e-3)
+    x[6] += np.float32(3.0)
+    fast = _engine(tmp_path, b, "a.blob", cert=True)
+    exact = _engine(tmp_path, b, "b.blob", cert=False)
+    assert _bits_equal(fast.forward_batch(x), exact.forward_batch(x))
+    fast.close()
+    exact.close()
+
+
+def test_cert_scene(tmp_path, orc):
+    b = synth.make_blob(seed=49)
+    rng = np.random.default_rng(50)
+    cube = rng.standard_normal((120, 70, 100), dtype=np.float32)
+    cube += rng.uniform(-0.5, 0.5, (120, 1, 1)).astype(np.float32)
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    got = eng.forward_patched(cube, 32)
+    want = scene.stitch(model.forward_batch(scene.cut(cube, 32)), 70, 100)
+    assert _bits_equal(got, want)
+    eng.close()
