@@ -157,6 +157,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [wave][512]
   float* absw = opart + 4 * 512;                         // [wave][32]
   float* qw = absw + 4 * 32;                             // [wave]
+  uint32_t* wsl = reinterpret_cast<uint32_t*>(qw + 4);   // [channel][tap][4] sign masks
   typedef __attribute__((address_space(3))) float* lds_f32;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_f32)cert_lds;
 
@@ -170,6 +171,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
       Bw[t] = as_h8((cert_u32x4){v.x, v.y, v.z, v.w});
     }
   }
+
+  // the group's sign masks (16 channels x 9 taps x 4 words) for the
+  // reference-order recompute; the first row barrier orders them
+  for (int i = tid; i < 16 * 36; i += 256) wsl[i] = a.cws[(size_t)grp * 16 * 36 + i];
 
   // DMA: wave w issues the row's 1 KiB loads k = w, w + 4, ... < nld; lane L
   // of load k fetches 16 bytes: channel 8 k + L / 8, column group (L % 8)
@@ -221,13 +226,16 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   const int co = 16 * grp + fc;
   const bool chan = co < a.cout;
   const float f_al = a.alpha[co], f_A = a.A[co], f_B = a.B[co], f_sl = a.slope[co], f_rs = a.rsign[co];
+  // with a slope >= 0 the PReLU branch is non-decreasing in z (both pieces
+  // are, and meet at 0), so the bit is monotone in v and equal bits at
+  // v - E and v + E decide it; a negative or NaN slope also needs both ends
+  // on one side of z = 0
+  const bool mono = f_sl >= 0.0f;
   // (cin + 16) 2^-24 (1 + 2^-9), rounding up (the 2^-9 also covers the
   // round-to-nearest steps of A, Q and E below)
   const float cA = (float)(cin + 16) * 0x1p-24f * (1.0f + 0x1p-9f);
   const int cwo = (a.cout + 31) >> 5;
   const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
-  typedef const __attribute__((address_space(4))) uint32_t* const_u32;
-  const const_u32 wsg = (const_u32)a.cws;
 
   issue(0);
 
@@ -379,7 +387,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         float zl_, zh_;
         const bool bl = fold_bit(__fsub_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zl_);
         const bool bh = fold_bit(__fadd_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zh_);
-        const bool ok = bl == bh && (zl_ < 0.0f) == (zh_ < 0.0f) && !__builtin_isnan(zl_) && !__builtin_isnan(zh_);
+        const bool ok = bl == bh && (mono || (zl_ < 0.0f) == (zh_ < 0.0f)) && !__builtin_isnan(zl_) && !__builtin_isnan(zh_);
         bit[k] = bl && chan;
         unc[k] = !ok && chan && fpx0 + k < W;
       }
@@ -392,37 +400,47 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         const int which = um[0] ? 0 : 1;
         const int li = __builtin_ctzll(um[which]);
         um[which] &= um[which] - 1;
-        const int upx = 8 * wv + 2 * (li >> 4) + which, uco = 16 * grp + (li & 15);
-        // the channel's 36 sign-mask words in one batch of scalar loads; lane
-        // t takes tap t's four
-        uint32_t mw36[36];
-#pragma unroll
-        for (int i = 0; i < 36; ++i) mw36[i] = wsg[(size_t)uco * 36 + i];
-        uint32_t wk[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint32_t t4 = 0u;
-#pragma unroll
-          for (int t = 0; t < 9; ++t) t4 = lane == t ? mw36[t * 4 + k] : t4;
-          wk[k] = t4;
-        }
+        const int upx = 8 * wv + 2 * (li >> 4) + which;
         float st = 0.0f;
         const int ky = lane / 3, kx = lane - 3 * (lane / 3);
         const int iy = r + ky - 1, ix = upx + kx - 1;
         if (lane < 9 && iy >= 0 && iy < H && ix >= 0 && ix < W) {
-          // channels 4 m, 4 m + 1 use column offset c0, 4 m + 2, 4 m + 3 the
-          // swapped one (row_off)
+          // lane t sums tap t: its four sign-mask words, then the channels
+          // in batches of 32 read ahead of their adds (channels 4 m, 4 m + 1
+          // at column offset c0, 4 m + 2, 4 m + 3 at the swapped one, as
+          // row_off lays them out).  A last partial batch reads up to 28
+          // channels past cin, inside the block's LDS (a row buffer holds
+          // at least cin channels and 11 KiB of partials follow the ring),
+          // and adds +0 for them, which leaves a sum that started at +0
+          // unchanged.
+          const uint4 m4 = *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4]);
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
           const float* c0 = rowp + (row_off(0, ix) >> 2);
           const float* c1 = rowp + (row_off(2, ix) >> 2) - 64;
-#pragma unroll 4
-          for (int c4 = 0; c4 < cin; c4 += 4) {
-            const float x0 = c0[c4 * 32], x1 = c0[c4 * 32 + 32], x2 = c1[c4 * 32 + 64], x3 = c1[c4 * 32 + 96];
-            const uint32_t wd = (c4 < 32 ? wk[0] : c4 < 64 ? wk[1] : c4 < 96 ? wk[2] : wk[3]) >> (c4 & 31);
-            st = __fadd_rn(st, (wd & 1u) ? x0 : -x0);
-            st = __fadd_rn(st, (wd & 2u) ? x1 : -x1);
-            st = __fadd_rn(st, (wd & 4u) ? x2 : -x2);
-            st = __fadd_rn(st, (wd & 8u) ? x3 : -x3);
+          for (int cb = 0; cb < cin; cb += 32) {
+            float xb[32];
+#pragma unroll
+            for (int j = 0; j < 32; j += 4) {
+              const int c4 = cb + j;
+              xb[j] = c0[c4 * 32];
+              xb[j + 1] = c0[c4 * 32 + 32];
+              xb[j + 2] = c1[c4 * 32 + 64];
+              xb[j + 3] = c1[c4 * 32 + 96];
+            }
+            // -x for a clear mask bit: bit j of the inverted word moved to
+            // the sign position
+            const uint32_t nw = ~(cb < 32 ? m4.x : cb < 64 ? m4.y : cb < 96 ? m4.z : m4.w);
+            if (cin - cb >= 32) {
+#pragma unroll
+              for (int j = 0; j < 32; ++j) st = __fadd_rn(st, f32_of(bits_of(xb[j]) ^ ((nw << (31 - j)) & 0x80000000u)));
+            } else {
+              const uint32_t live = (1u << (cin - cb)) - 1u;
+#pragma unroll
+              for (int j = 0; j < 32; ++j) {
+                const float v = f32_of(bits_of(xb[j]) ^ ((nw << (31 - j)) & 0x80000000u));
+                st = __fadd_rn(st, ((live >> j) & 1u) ? v : 0.0f);
+              }
+            }
           }
         }
         float acc = 0.0f;
@@ -469,7 +487,7 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if (xbytes >= kCertFar) return hipErrorInvalidValue;
   if (a.N >= 0x7FFFFFFF) return hipErrorInvalidValue;
   const int nld = (a.cin + 7) / 8;
-  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4) * 4;
+  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4;
   const bool guard = a.cin / 4 < 28;
   static bool attr[2] = {false, false};
   if (!attr[guard]) {
