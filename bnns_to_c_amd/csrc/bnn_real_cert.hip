@@ -20,16 +20,20 @@
 // matrix core's result is exact whatever its internal order.  The digit sums
 // are recombined (2048 Zh + Zl) and scaled back by 2^(e - 21) in fp32.
 //
-// E = (cin + 16) 2^-24 (1 + 2^-8) A + (1 + 2^-8) Q + 2^-110, rounded up, with
-//  * A = sum |x| over the output's 3 x 3 x cin window;
+// E = 2^-24 (1 + 2^-8) A + (1 + 2^-8) Q + 2^-110, rounded up, with
+//  * A = sum over the output's 3 x 3 x cin window of (cin - ci + 16) |x|,
+//    ci the input channel;
 //  * Q = half a grid step 2^(e-21) per term: 48 * 2^(e-21) per (input row,
 //    wave) of the window;
-//  * the reference's roundings: a tap's sequential sum of cin terms is
-//    within gamma(cin - 1) A_tap of the exact one, the tap sum adds
-//    gamma(8) A (gamma(n) = n 2^-24 / (1 - n 2^-24));
+//  * the reference's roundings: a tap's sum s_k = fl(s_(k-1) + t_k) over
+//    channels k = 1 .. cin, started at 0, is off the exact sum by at most
+//    sum_(k >= 2) 2^-24 |s_k|, and |s_k| <= (1 + 2^-24)^k sum_(i <= k) |t_i|,
+//    so by at most 2^-24 (1 + 2^-16) sum_i (cin - i + 1) |t_i|; the nine
+//    tap sums add 8 2^-24 (1 + 2^-16) sum |x| more;
 //  * this kernel's: recombination, two row adds, three adds of the
-//    four-wave reduction (each at most 2^-24 (A + Q)); 2^-8 covers the
-//    gamma denominators and the roundings of A itself, 2^-110 underflow.
+//    four-wave reduction (each at most 2^-24 (sum |x| + Q)); the weight's
+//    "+ 16" covers these and the tap adds, 2^-8 the (1 + 2^-16) factors and
+//    the roundings of A itself, 2^-110 underflow.
 //
 // Work split: one block of four waves per (patch, 16-channel group); wave w
 // converts a quarter of the input channels.  Rows stream through a ring of
@@ -219,6 +223,11 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   uint32_t jvalid = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) jvalid |= (4 * j + gq < cpw ? 1u : 0u) << j;
+  // weight of element j's |x| in the window sum: cin - ci + 16 for its
+  // channel ci (the bound's weighted sum; exact small integers)
+  float wsum[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wsum[j] = (float)(cin + 16 - (cpw * wv + 4 * j + gq));
 
   // finalize: lane -> output channel fc, pixels fpx0 and fpx0 + 1
   const int fc = lane & 15, fq = lane >> 4;
@@ -231,9 +240,9 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   // v - E and v + E decide it; a negative or NaN slope also needs both ends
   // on one side of z = 0
   const bool mono = f_sl >= 0.0f;
-  // (cin + 16) 2^-24 (1 + 2^-9), rounding up (the 2^-9 also covers the
-  // round-to-nearest steps of A, Q and E below)
-  const float cA = (float)(cin + 16) * 0x1p-24f * (1.0f + 0x1p-9f);
+  // 2^-24 (1 + 2^-9) times the weighted window sum, rounding up (the 2^-9
+  // also covers the round-to-nearest steps of A, Q and E below)
+  const float cA = 0x1p-24f * (1.0f + 0x1p-9f);
   const int cwo = (a.cout + 31) >> 5;
   const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
 
@@ -270,8 +279,8 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         m = fmaxf(m, fmaxf(fabsf(xv[0][j]), fabsf(xv[1][j])));
-        as[0] = __fadd_rn(as[0], fabsf(xv[0][j]));
-        as[1] = __fadd_rn(as[1], fabsf(xv[1][j]));
+        as[0] = __fmaf_rn(fabsf(xv[0][j]), wsum[j], as[0]);
+        as[1] = __fmaf_rn(fabsf(xv[1][j]), wsum[j], as[1]);
       }
       uint32_t mb = bits_of(m);
       mb = max(mb, dpp<0x128, false>(mb, mb));  // row_ror:8
