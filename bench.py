@@ -19,10 +19,20 @@ before each other configuration.  Prints ONE JSON line on stdout:
   cpu_configs   configs 1-4 on the reference's own code on this host:
                 its kernels (cfg1, cfg2), its CLI per patch (cfg3 from the
                 config-0 number, cfg4 on one 256x256 patch), with speed-ups
-  roofline      the dominant kernel (the order-exact real first conv, on the
-                matrix cores): FP32 FMA work per launch / its mean
-                hipEvent-measured duration against the published dense FP32
-                matrix peak
+  roofline      the dominant kernel, enc1.conv1.  By default the certified
+                first conv (fp16 matrix-core digit sums with a rigorous
+                error bound, reference-order recompute of the outputs the
+                bound leaves open): its algorithmic bytes (the input once,
+                the output bits once) / its median hipEvent-measured
+                duration against the 8 TB/s HBM peak, the binding floor of
+                that formulation (its matrix-core work takes about half as
+                long at the fp16 peak); the FP32 FMA work of the same conv
+                per second is reported beside it as fp32_equivalent.  With
+                BNN_CERT=0 the order-exact kernel runs instead, and the
+                roofline is its FP32 FMA work against the dense FP32 matrix
+                peak
+  first_conv_exact  the order-exact first conv (a model loaded with
+                BNN_CERT=0): its time and FP32 rate against the matrix peak
   bconv         the 17 binary convs: binary-op/s (2 per bit-MAC, border taps
                 counted) against the VALU-popcount roofline
   cfg1          benchmark config 1: the isolated binary conv 64->64 at
@@ -569,6 +579,57 @@ def main() -> int:
     real_work = agg[real["label"]][3]
     real_flops = 2 * real_work
     achieved = real_flops / (real["ms"] / 1e3)
+    # which first-conv kernel ran: the certified one unless BNN_CERT=0 (its
+    # shape condition, cin <= 128 and W <= 32 in multiples of 4, holds here)
+    cert = os.environ.get("BNN_CERT") != "0"
+    real_bytes = N * 120 * H * W * 4 + N * H * W * 4  # input floats once, output words once
+    if cert:
+        rate_b = real_bytes / (real["ms"] / 1e3)
+        roofline = {"bound": "hbm",
+                    "kernel": "enc1.conv1 certified first conv + real fold (fp16 matrix-core integer-digit sums, "
+                              "rigorous error bound, reference-order recompute of undecided outputs)",
+                    "achieved": round(rate_b / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                    "frac": round(rate_b / PEAK_HBM, 4), "traffic": measured_traffic(),
+                    "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, "
+                                      "calibrated)",
+                    "algorithmic": f"{real_bytes} B/launch = {N} patches x (120 x 32 x 32 x 4 B in + 32 x 32 x 4 B "
+                                   "out)",
+                    "fp32_equivalent": {"tflops": round(achieved / 1e12, 3),
+                                        "of_fp32_matrix_peak": round(achieved / PEAK_FP32_FLOPS, 4),
+                                        "note": f"{real_flops:.4g} FLOP of the FP32 conv per launch / the same time"}}
+    else:
+        roofline = {"bound": "mfma", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32, K=1 MFMA)",
+                    "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
+                    "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": measured_traffic(),
+                    "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, "
+                                      "calibrated)",
+                    "algorithmic": f"{real_flops:.4g} FLOP/launch = 2 x 17,694,720 MAC x {N} patches"}
+    log(f"roofline: {roofline['kernel']}: {roofline['achieved']} {roofline['unit']}, frac {roofline['frac']}")
+
+    exact = None
+    if cert and not args.headline_only:
+        # the order-exact first conv on the same batch, from a model loaded
+        # with BNN_CERT=0 (the variable is read when a model is loaded)
+        os.environ["BNN_CERT"] = "0"
+        try:
+            xeng = engine.Engine(blob_path)
+        finally:
+            os.environ.pop("BNN_CERT", None)
+        settle(lambda: xeng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp), torch)
+        engine.prof_reset()
+        engine.prof_enable(True)
+        for _ in range(10):
+            xeng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), sp)
+        torch.cuda.synchronize()
+        engine.prof_enable(False)
+        xms = float(np.median([ms for lab, op, ms, work in engine.prof_records() if op == "conv_real"]))
+        xrate = real_flops / (xms / 1e3)
+        exact = {"kernel": "order-exact FP32 first conv (K=1 MFMA chains in the reference's order), BNN_CERT=0",
+                 "us": round(xms * 1e3, 2), "tflops": round(xrate / 1e12, 3),
+                 "frac": round(xrate / PEAK_FP32_FLOPS, 4), "peak": PEAK_FP32_FLOPS / 1e12}
+        log(f"order-exact first conv (BNN_CERT=0): {xms * 1e3:.1f} us, {xrate / 1e12:.1f} TFLOP/s, "
+            f"frac {xrate / PEAK_FP32_FLOPS:.3f} of the FP32 matrix peak")
+        xeng.close()
     bin_ms = sum(k["ms"] for k in kernels if k["op"] != "conv_real")
     bin_work = sum(agg[k["label"]][3] for k in kernels if k["op"] != "conv_real")
     bin_rate = 2 * bin_work / (bin_ms / 1e3)
@@ -635,16 +696,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 first conv + xnor-popcount (u32) binary convs",
+        "dtype": "fp32 first conv (certified: fp16 matrix-core digit sums, exact fp32 recompute where undecided) "
+                 "+ xnor-popcount (u32) binary convs",
         "data": "synthetic: seeded random blob (base 16, Bernoulli sign weights, U[-fan_in/4,fan_in/4] "
                 "ge/lt thresholds) and x ~ N(0,1) patches, resident in HBM",
         "config": {"workload": "v1 Bi-Real binary UNet forward (nearest upsampler), 32x32x120 patches",
                    "batch": N, "H": H, "W": W, "n_bands": 120, "n_classes": 3, "base_channels": 16},
-        "roofline": {"bound": "mfma", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32, K=1 MFMA)",
-                     "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_FLOPS, 4), "traffic": measured_traffic(),
-                     "traffic_source": "profiles/unet_b1024_hbm_traffic.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, calibrated)",
-                     "algorithmic": f"{real_flops:.4g} FLOP/launch = 2 x 17,694,720 MAC x {N} patches"},
+        "roofline": roofline,
         "bconv": {"layers": 17, "kernels": sum(1 for k in kernels if k["op"] != "conv_real"),
                   "binary_op_s": round(bin_rate, 1), "peak": valu_binop_peak(),
                   "frac": round(bin_rate / valu_binop_peak(), 4), "ms": round(bin_ms, 5),
@@ -658,6 +716,7 @@ def main() -> int:
                                       "in and out over PCIe included)",
                             "ms_per_step": round(pcie_ms, 4), "patches_s": round(N / pcie_ms * 1e3, 1)},
             "cpu_configs": cpu_cfg,
+            "first_conv_exact": exact,
             "cfg1": {"config": "isolated bconv 64->64, 64x64, batch 256, int32 P out (benchmark config 1)",
                      "us": round(c1_ms * 1e3, 2), "binary_op_s": round(c1_rate, 1),
                      "frac": round(c1_rate / valu_binop_peak(), 4),
