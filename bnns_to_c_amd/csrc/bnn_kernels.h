@@ -210,9 +210,10 @@ inline void real_cert_tables(const int8_t* wsign, int cout, int cin, uint16_t* b
       for (int ci = 0; ci < cin && ci < 128; ++ci)
         if (wsign[((size_t)co * cin + ci) * 9 + t] > 0) s[((size_t)co * 9 + t) * 4 + ci / 32] |= 1u << (ci % 32);
 }
-// whether launch_real_cert takes a layer of this shape
+// whether launch_real_cert takes a layer of this shape (rows wider than 32
+// run as tiles of 24 output columns)
 inline bool real_cert_fits(int cin, int W, int rowlen) {
-  return cin >= 4 && cin <= 128 && cin % 4 == 0 && W >= 4 && W <= 32 && W % 4 == 0 && rowlen % 4 == 0;
+  return cin >= 4 && cin <= 128 && cin % 4 == 0 && W >= 4 && W % 4 == 0 && rowlen % 4 == 0;
 }
 
 // 1x1 stem weights (v2 models; signs +1, -1 or 0): 64-bit lane masks

@@ -155,8 +155,14 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int p = lane & 15, gq = lane >> 4;
-  const int n = blockIdx.x, grp = blockIdx.y;
   const int H = a.H, W = a.W, cin = a.cin, cpw = cin >> 2;
+  // rows up to 32 wide: one block per patch, window column = image column;
+  // wider rows: tiles of 24 output columns, each block's 32-column window
+  // starting 4 columns before its tile (columns outside the image read 0)
+  const int ntile = W <= 32 ? 1 : (W + 23) / 24;
+  const int n = blockIdx.x / ntile, tile = blockIdx.x - n * ntile, grp = blockIdx.y;
+  const int wx0 = W <= 32 ? 0 : 24 * tile - 4;  // image column of window column 0
+  const int vlo = W <= 32 ? 0 : 4, vhi = W <= 32 ? W : min(28, W - wx0);  // output window columns
   const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
   float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [wave][512]
   float* absw = opart + 4 * 512;                         // [wave][32]
@@ -191,8 +197,9 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
     const int k = wv + 4 * m;
     const int ci = 8 * k + (lane >> 3);
     const int g4 = (lane & 7) ^ (((ci >> 1) & 1) << 2);
-    const bool ok = k < nld && ci < cin && 4 * g4 < ig.xlim;
-    doff[m] = ok ? (uint32_t)(ig.base + (size_t)ci * ig.cstride + 4 * g4) * 4u : kCertFar;
+    const int cg = wx0 + 4 * g4;  // image column of the 16-byte group
+    const bool ok = k < nld && ci < cin && cg >= 0 && cg < ig.xlim;
+    doff[m] = ok ? (uint32_t)(ig.base + (size_t)ci * ig.cstride + cg) * 4u : kCertFar;
   }
   const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
   auto uni = [](uint32_t v) __attribute__((always_inline)) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
@@ -398,7 +405,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         const bool bh = fold_bit(__fadd_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zh_);
         const bool ok = bl == bh && (mono || (zl_ < 0.0f) == (zh_ < 0.0f)) && !__builtin_isnan(zl_) && !__builtin_isnan(zh_);
         bit[k] = bl && chan;
-        unc[k] = !ok && chan && fpx0 + k < W;
+        unc[k] = !ok && chan && fpx0 + k >= vlo && fpx0 + k < vhi;
       }
       uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
       uint64_t um[2] = {__ballot(unc[0]), __ballot(unc[1])};
@@ -413,7 +420,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         float st = 0.0f;
         const int ky = lane / 3, kx = lane - 3 * (lane / 3);
         const int iy = r + ky - 1, ix = upx + kx - 1;
-        if (lane < 9 && iy >= 0 && iy < H && ix >= 0 && ix < W) {
+        if (lane < 9 && iy >= 0 && iy < H && wx0 + ix >= 0 && wx0 + ix < W) {
           // lane t sums tap t: its four sign-mask words, then the channels
           // in batches of 32 read ahead of their adds (channels 4 m, 4 m + 1
           // at column offset c0, 4 m + 2, 4 m + 3 at the swapped one, as
@@ -465,10 +472,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
       }
 
       // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k
-      if (fc < 2 && fpx0 + fc < W) {
+      if (fc < 2 && fpx0 + fc >= vlo && fpx0 + fc < vhi) {
         const uint32_t word = (uint32_t)((fc ? bm[1] : bm[0]) >> (16 * fq)) & 0xFFFFu;
         const int HW = H * W;
-        uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)r * W + fpx0 + fc) * cwo) + grp * 2;
+        uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)r * W + wx0 + fpx0 + fc) * cwo) + grp * 2;
         if (whole_word) *reinterpret_cast<uint32_t*>(dst) = word;
         else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
       }
@@ -494,7 +501,6 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if (!real_cert_fits(a.cin, a.W, rowlen) || (uintptr_t)a.x % 16) return hipErrorInvalidValue;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= kCertFar) return hipErrorInvalidValue;
-  if (a.N >= 0x7FFFFFFF) return hipErrorInvalidValue;
   const int nld = (a.cin + 7) / 8;
   const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4;
   const bool guard = a.cin / 4 < 28;
@@ -505,7 +511,9 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
     if (e != hipSuccess) return e;
     attr[guard] = true;
   }
-  dim3 grid((unsigned)a.N, (unsigned)((a.cout + 15) / 16));
+  const long ntile = a.W <= 32 ? 1 : (a.W + 23) / 24;
+  if ((long)a.N * ntile >= 0x7FFFFFFF) return hipErrorInvalidValue;
+  dim3 grid((unsigned)((long)a.N * ntile), (unsigned)((a.cout + 15) / 16));
   if (guard) hipLaunchKernelGGL((k_real_cert<true>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
   else hipLaunchKernelGGL((k_real_cert<false>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
   return hipGetLastError();

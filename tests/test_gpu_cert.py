@@ -6,7 +6,8 @@ bound cannot decide many outputs and the reference-order recompute must:
 * every band +-1, so tap sums are integers, and each channel's fold placed
   exactly on one integer sum: about one output in a hundred sits on z = 0;
 * bands scaled by 2^-20 .. 2^20, zero rows, and an infinity and a NaN;
-* the scene path (edge patches partly outside the cube).
+* the scene path (edge patches partly outside the cube);
+* rows wider than 32 (tiles of 24 output columns with a 4-column margin).
 
 The debug forward reports the act1 bits of the certified kernel (its float
 conv output comes from the exact-order kernel); the plain forward's logits
@@ -58,14 +59,15 @@ def _check(eng, model, x):
         assert _bits_equal(plain[n], want), ("plain logits", n)
 
 
-def test_cert_threshold_ties(tmp_path, orc):
+@pytest.mark.parametrize("H,W", [(32, 32), (24, 76)])
+def test_cert_threshold_ties(tmp_path, orc, H, W):
     b = synth.make_blob(seed=41)
     rng = np.random.default_rng(42)
     N = 2
-    x = rng.choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, 32, 32))
+    x = rng.choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, H, W))
     model = orc.parse(B.to_bytes(b))
     _, ref = model.forward(x[0], stages=True)
-    conv = ref["enc1.conv1"]  # alpha * tap sum, [16][32][32]
+    conv = ref["enc1.conv1"]  # alpha * tap sum, [16][H][W]
     act = b.enc_act1[0]
     A = act.A.astype(np.float32)
     Bv = act.B.copy()
@@ -102,7 +104,8 @@ def test_cert_wide_range_and_nonfinite(tmp_path, orc):
     eng.close()
 
 
-@pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16)])
+@pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16),
+                                       (16, 16, 72), (8, 20, 100), (32, 16, 256), (16, 36, 36)])
 def test_cert_shapes(tmp_path, orc, base, H, W):
     b = synth.make_blob(seed=45 + base, base=base)
     x = synth.make_input(46 + H, 2, 120, H, W)
@@ -117,6 +120,20 @@ def test_cert_vs_exact_order_batch(tmp_path):
     x = synth.make_input(48, 96, 120, 32, 32)
     x[5] *= np.float32(1e-3)
     x[6] += np.float32(3.0)
+    fast = _engine(tmp_path, b, "a.blob", cert=True)
+    exact = _engine(tmp_path, b, "b.blob", cert=False)
+    assert _bits_equal(fast.forward_batch(x), exact.forward_batch(x))
+    fast.close()
+    exact.close()
+
+
+def test_cert_wide_vs_exact_order(tmp_path):
+    """Rows wider than 32 run as tiles of 24 output columns: the large-tile
+    configuration's shape (256 x 256, base 32: two 16-channel groups) against
+    the order-exact kernel."""
+    b = synth.make_blob(seed=51, base=32)
+    x = synth.make_input(52, 2, 120, 256, 256)
+    x[1, :, :, 100:140] *= np.float32(1e-4)  # a band of small values across tile edges
     fast = _engine(tmp_path, b, "a.blob", cert=True)
     exact = _engine(tmp_path, b, "b.blob", cert=False)
     assert _bits_equal(fast.forward_batch(x), exact.forward_batch(x))
