@@ -7,6 +7,8 @@ the full batches also through size-independent properties: P(-a) = -P(a),
 the parity and range of P, and the fused fold+pool agreeing with the plain
 P kernel followed by the rules (csrc/bnn_fold.c:37-60, bnn_maxpool.c:28-48).
 """
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 
@@ -86,8 +88,11 @@ def test_cfg1_full_batch(torch, orc):
     nv = torch.from_numpy(_nvalid(H, W, C)).cuda()
     assert bool(((P - nv) % 2 == 0).all()) and bool((P.abs() <= nv).all())
     got = P.cpu().numpy()
-    for n in (0, 1, 77, 128, 255):
-        assert np.array_equal(got[n], orc.bconv(a[n], bits, C)), n
+    # every patch against the checker (its C calls release the GIL)
+    with ThreadPoolExecutor(8) as ex:
+        bad = [n for n, ok in enumerate(ex.map(lambda n: np.array_equal(got[n], orc.bconv(a[n], bits, C)), range(N)))
+               if not ok]
+    assert not bad, bad[:8]
 
 
 def _host_fold(P, ty, t, lo, hi):
@@ -151,8 +156,18 @@ def test_cfg2_full_batch(torch, orc):
     pooled = Ph.reshape(N, C, H // 2, 2, W // 2, 2).max(axis=(3, 5))
     assert np.array_equal(E.unpack_bits_nhwc(skip.cpu().numpy().view(np.uint32), C), _host_fold(Ph, *f1))
     assert np.array_equal(E.unpack_bits_nhwc(down.cpu().numpy().view(np.uint32), C), _host_fold(pooled, *f2))
-    for n in (0, 511, 1023):
-        assert np.array_equal(Ph[n], orc.bconv(a[n], bits, C)), n
+    sk = E.unpack_bits_nhwc(skip.cpu().numpy().view(np.uint32), C)
+    dn = E.unpack_bits_nhwc(down.cpu().numpy().view(np.uint32), C)
+
+    def patch_ok(n):
+        Pn = orc.bconv(a[n], bits, C)
+        return (np.array_equal(Ph[n], Pn) and np.array_equal(sk[n], orc.fold_int(Pn, *f1))
+                and np.array_equal(dn[n], orc.fold_int(orc.maxpool(Pn), *f2)))
+
+    # every patch's P, skip bits and pooled bits against the checker
+    with ThreadPoolExecutor(8) as ex:
+        bad = [n for n, ok in enumerate(ex.map(patch_ok, range(N))) if not ok]
+    assert not bad, bad[:8]
 
 
 @pytest.mark.parametrize("C,H,W", [(8, 6, 6), (24, 5, 8), (40, 4, 4), (16, 32, 32)])
