@@ -115,6 +115,20 @@ def test_cert_shapes(tmp_path, orc, base, H, W):
     eng.close()
 
 
+@pytest.mark.parametrize("nb,base,H,W", [(4, 8, 16, 16), (16, 16, 32, 32), (28, 16, 32, 32), (64, 16, 32, 40),
+                                          (100, 8, 20, 32), (112, 16, 32, 32), (128, 16, 32, 32)])
+def test_cert_band_counts(tmp_path, orc, nb, base, H, W):
+    """Band counts from 4 to 128 (a wave's quarter of the channels from 1 to
+    32, partly empty 8-channel loads, the guarded conversion below 112
+    bands), each bit for bit against the checker."""
+    b = synth.make_blob(seed=60 + nb, base=base, n_bands=nb)
+    x = synth.make_input(61 + nb, 2, nb, H, W)
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
 def test_cert_vs_exact_order_batch(tmp_path):
     b = synth.make_blob(seed=47)
     x = synth.make_input(48, 96, 120, 32, 32)
