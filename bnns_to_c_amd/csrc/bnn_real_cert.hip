@@ -68,6 +68,12 @@ template <int CTRL, bool ZERO>
 __device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t src) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, 0xF, 0xF, ZERO);
 }
+// a DPP move whose lanes all take a source lane or 0 (bound_ctrl), so no
+// old value has to be placed in the destination first
+template <int CTRL>
+__device__ __forceinline__ uint32_t dmov(uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)src, CTRL, 0xF, 0xF, true);
+}
 constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121, kRor15 = 0x12F;
 
 // Operands of the pixel to the left (kx = 0) and right (kx = 2): lane p of a
@@ -76,15 +82,15 @@ constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121, kRor15 = 0x12F;
 __device__ __forceinline__ void shift_left(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    o[0][i] = dpp<kShr1, true>(0u, a[0][i]);
-    o[1][i] = dpp<kShr1, false>(dpp<kRor1, false>(0u, a[0][i]), a[1][i]);
+    o[0][i] = dmov<kShr1>(a[0][i]);
+    o[1][i] = dpp<kShr1, false>(dmov<kRor1>(a[0][i]), a[1][i]);
   }
 }
 __device__ __forceinline__ void shift_right(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    o[0][i] = dpp<kShl1, false>(dpp<kRor15, false>(0u, a[1][i]), a[0][i]);
-    o[1][i] = dpp<kShl1, true>(0u, a[1][i]);
+    o[0][i] = dpp<kShl1, false>(dmov<kRor15>(a[1][i]), a[0][i]);
+    o[1][i] = dmov<kShl1>(a[1][i]);
   }
 }
 
@@ -133,10 +139,10 @@ __device__ __forceinline__ float rows_sum(float x) {
 // per-pixel value (segment s in v[s]) plus its left and right neighbours
 __device__ __forceinline__ void window3(const float (&v)[2], float (&o)[2]) {
   const uint32_t a0 = bits_of(v[0]), a1 = bits_of(v[1]);
-  const float l0 = f32_of(dpp<kShr1, true>(0u, a0));
-  const float l1 = f32_of(dpp<kShr1, false>(dpp<kRor1, false>(0u, a0), a1));
-  const float r0 = f32_of(dpp<kShl1, false>(dpp<kRor15, false>(0u, a1), a0));
-  const float r1 = f32_of(dpp<kShl1, true>(0u, a1));
+  const float l0 = f32_of(dmov<kShr1>(a0));
+  const float l1 = f32_of(dpp<kShr1, false>(dmov<kRor1>(a0), a1));
+  const float r0 = f32_of(dpp<kShl1, false>(dmov<kRor15>(a1), a0));
+  const float r1 = f32_of(dmov<kShl1>(a1));
   o[0] = __fadd_rn(__fadd_rn(l0, v[0]), r0);
   o[1] = __fadd_rn(__fadd_rn(l1, v[1]), r1);
 }
