@@ -422,6 +422,7 @@ struct BnnDevice {
   // the certified first conv's tables (v1, all signs +-1, cin <= 128, cin % 4 == 0), and cert_mode()
   uint16_t* rcwb = nullptr;
   uint32_t* rcws = nullptr;
+  float *rct1 = nullptr, *rct2 = nullptr, *rcb0 = nullptr, *rcdc = nullptr;  // its fold summary
   bool cert = false;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   bool mid = false;  // the fused middle applies (mid_fits at load, and mid_mode())
@@ -578,6 +579,17 @@ int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
   v = padv(a.B); if ((rc = dev_upload(D, &D->rB, v.data(), v.size()))) return rc;
   v = padv(a.slope); if ((rc = dev_upload(D, &D->rslope, v.data(), v.size()))) return rc;
   v = padv(a.rsign); if ((rc = dev_upload(D, &D->rrsign, v.data(), v.size()))) return rc;
+  if (D->rcwb) {
+    // the certified kernel's summary of each channel's fold
+    const size_t np = (size_t)(c.Cout + 31) / 32 * 32;
+    std::vector<float> t1(np, INFINITY), t2(np, INFINITY), b0(np, -1.0f), dc(np, 0.0f);
+    for (int co = 0; co < c.Cout; ++co)
+      real_fold_switches(c.alpha[co], a.A[co], a.B[co], a.slope[co], a.rsign[co], &t1[co], &t2[co], &b0[co], &dc[co]);
+    if ((rc = dev_upload(D, &D->rct1, t1.data(), np))) return rc;
+    if ((rc = dev_upload(D, &D->rct2, t2.data(), np))) return rc;
+    if ((rc = dev_upload(D, &D->rcb0, b0.data(), np))) return rc;
+    if ((rc = dev_upload(D, &D->rcdc, dc.data(), np))) return rc;
+  }
   return BNN_OK;
 }
 
@@ -668,7 +680,7 @@ int build_device(Model* m, const StemPart* st = nullptr) {
     if ((rc = upload_bconv(D, &D->d2[i], m->dec_conv2[i], 0, &m->dec_act2[i], nullptr))) return rc;
   }
   D->mid = mid_mode() && mid_fits(D);
-  D->cert = cert_mode() && D->rcwb && D->rcws;
+  D->cert = cert_mode() && D->rcwb && D->rcws && D->rct1;
   if (D->mid) {
     const auto L = mid_layers(D);
     const Conv* cv[kMidLayers] = {&m->enc_conv1[2], &m->enc_conv2[2], &m->enc_conv1[3], &m->enc_conv2[3],
@@ -821,6 +833,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       ra.f32 = nullptr;
       ra.cwb = D->rcwb;
       ra.cws = D->rcws;
+      ra.ct1 = D->rct1; ra.ct2 = D->rct2; ra.cb0 = D->rcb0; ra.cdc = D->rcdc;
       HIP_TRY(launch_real_cert(ra, st));
       if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
     } else {

@@ -13,6 +13,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cmath>
+#include <cstring>
 #include <vector>
 
 namespace bnn {
@@ -109,6 +112,8 @@ struct RealArgs {
   // sign masks, real_cert_tables(); null leaves that kernel unused
   const uint16_t* cwb;
   const uint32_t* cws;
+  // its fold summary per channel (real_fold_switches), padded like alpha
+  const float *ct1, *ct2, *cb0, *cdc;
   const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;
@@ -209,6 +214,93 @@ inline void real_cert_tables(const int8_t* wsign, int cout, int cin, uint16_t* b
     for (int t = 0; t < 9; ++t)
       for (int ci = 0; ci < cin && ci < 128; ++ci)
         if (wsign[((size_t)co * cin + ci) * 9 + t] > 0) s[((size_t)co * 9 + t) * 4 + ci / 32] |= 1u << (ci % 32);
+}
+// The real fold's bit as a function of the tap sum v, in the reference's
+// float steps (csrc/bnn_fold.c:62-77, A * o + B fused): o = al * v,
+// z = fma(A, o, B), h = z < 0 ? sl * z : z, bit = h + rs > 0.
+inline bool real_fold_bit_host(float v, float al, float A, float B, float sl, float rs) {
+  const float o = al * v;
+  const float z = std::fma(A, o, B);
+  const float h = z < 0.0f ? sl * z : z;
+  return h + rs > 0.0f;
+}
+// Finite floats in order as integers (-0 and +0 both 0) and back.
+inline int32_t real_ford(float f) {
+  uint32_t b;
+  std::memcpy(&b, &f, 4);
+  return (b & 0x80000000u) ? -(int32_t)(b & 0x7FFFFFFFu) : (int32_t)b;
+}
+inline float real_fval(int32_t o) {
+  const uint32_t b = o >= 0 ? (uint32_t)o : (0x80000000u | (uint32_t)(-o));
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+// The points where the fold's bit changes along the floats of [-dc, dc]:
+// there the bit of v is b0 ^ (v >= t1) ^ (v >= t2) (t = +inf: no change).
+// dc is a power of two small enough that o, z, h and h + rs stay finite for
+// |v| <= dc, so no step meets an infinity or a NaN.  Then z is monotone in
+// v (RN products and fma are monotone), the PReLU branch splits the range
+// into at most two runs, on the z >= 0 run the bit is non-decreasing in z,
+// on the z < 0 run non-increasing for a negative slope and non-decreasing
+// otherwise: each run holds at most one change and a slope >= 0 at most one
+// in all.  Each change is found by bisection on the ordered floats, and the
+// result is checked at the run ends and around every change.  Parameters
+// that are not finite, or a failed check, give b0 = -1: every output of the
+// channel is left to the reference-order recompute.
+inline void real_fold_switches(float al, float A, float B, float sl, float rs, float* t1, float* t2, float* b0,
+                               float* dc) {
+  *t1 = *t2 = INFINITY;
+  *b0 = -1.0f;
+  *dc = 0.0f;
+  const float big = 4.2535295e37f;  // 2^125 = FLT_MAX / 8, rounded down
+  for (float x : {al, A, B, sl, rs})
+    if (!std::isfinite(x)) return;
+  const double m = std::max({1.0, std::fabs((double)al), std::fabs((double)A * al), std::fabs((double)sl * A * al)});
+  if (std::fabs(B) > big || std::fabs((double)sl * B) > big || std::fabs(rs) > big) return;
+  const float d = std::ldexp(1.0f, (int)std::floor(std::log2(big / m)));
+  const int32_t kLo = real_ford(-d), kHi = real_ford(d);
+  auto F = [&](int32_t o) { return real_fold_bit_host(real_fval(o), al, A, B, sl, rs); };
+  auto Zn = [&](int32_t o) { return std::fma(A, al * real_fval(o), B) < 0.0f; };
+  // first o in (a, b] where pred(o) == pred(b), given pred(a) != pred(b)
+  auto bisect = [](int32_t a, int32_t b, auto pred) {
+    const bool pb = pred(b);
+    while ((int64_t)b - a > 1) {
+      const int32_t mid = (int32_t)(((int64_t)a + b) >> 1);
+      if (pred(mid) == pb) b = mid;
+      else a = mid;
+    }
+    return b;
+  };
+  int32_t r1 = kHi, r2 = kHi;  // run 0 = [kLo, r1], run 1 = [r2, kHi]
+  bool two = false;
+  if (Zn(kLo) != Zn(kHi)) {
+    r2 = bisect(kLo, kHi, Zn);
+    r1 = r2 - 1;
+    two = true;
+  }
+  std::vector<int32_t> sw;
+  if (F(kLo) != F(r1)) sw.push_back(bisect(kLo, r1, F));
+  if (two) {
+    if (F(r1) != F(r2)) sw.push_back(r2);
+    if (F(r2) != F(kHi)) sw.push_back(bisect(r2, kHi, F));
+  }
+  if (sw.size() > 2) return;
+  const bool base = F(kLo);
+  auto model = [&](int32_t o) {
+    bool bit = base;
+    for (int32_t t : sw) bit ^= o >= t;
+    return bit;
+  };
+  std::vector<int32_t> probe = {kLo, kHi, r1, r2, 0, -1, 1};
+  for (int32_t t : sw)
+    for (int32_t k = -2; k <= 2; ++k) probe.push_back(std::min(kHi, std::max(kLo, t + k)));
+  for (int32_t o : probe)
+    if (model(o) != F(o)) return;
+  *t1 = sw.size() > 0 ? real_fval(sw[0]) : INFINITY;
+  *t2 = sw.size() > 1 ? real_fval(sw[1]) : INFINITY;
+  *b0 = base ? 1.0f : 0.0f;
+  *dc = d;
 }
 // whether launch_real_cert takes a layer of this shape (rows wider than 32
 // run as tiles of 24 output columns)

@@ -6,11 +6,13 @@
 // scales by alpha and folds (csrc/bnn_fold.c:62-77); only the fold's bit
 // leaves the layer.  This kernel computes an approximation v' of the tap sum
 // v together with a bound E >= |v' - v| that holds for every input, and
-// evaluates the fold at v' - E and v' + E.  alpha * v, A * o + B, the PReLU
-// branch and the final add are each monotone on either side of z = 0, so
-// when both ends land on the same side with the same bit, that bit is the
-// reference's.  Any other output is recomputed in the reference's order from
-// the input rows the block still holds in LDS.
+// asks whether the fold's bit can change between v' - E and v' + E.  The
+// host summarises each channel's fold as at most two change points along
+// the floats of a range where no step overflows (real_fold_switches: alpha
+// * v, A * o + B, the PReLU branch and the final add are each monotone on
+// either side of z = 0); an interval in that range holding no change point
+// has one bit, the reference's.  Any other output is recomputed in the
+// reference's order from the input rows the block still holds in LDS.
 //
 // v': per input row and wave (32 input channels), x is scaled by 2^(10 - e),
 // e the exponent of the largest |x| there, and split into two integer digits
@@ -248,11 +250,12 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   const int co = 16 * grp + fc;
   const bool chan = co < a.cout;
   const float f_al = a.alpha[co], f_A = a.A[co], f_B = a.B[co], f_sl = a.slope[co], f_rs = a.rsign[co];
-  // with a slope >= 0 the PReLU branch is non-decreasing in z (both pieces
-  // are, and meet at 0), so the bit is monotone in v and equal bits at
-  // v - E and v + E decide it; a negative or NaN slope also needs both ends
-  // on one side of z = 0
-  const bool mono = f_sl >= 0.0f;
+  // the fold's bit along [-dc, dc] as at most two change points
+  // (real_fold_switches): bit(v) = b0 ^ (v >= t1) ^ (v >= t2) there, so an
+  // interval inside [-dc, dc] holding no change point has one bit; b0 < 0
+  // marks a channel whose every output is recomputed
+  const float f_t1 = a.ct1[co], f_t2 = a.ct2[co], f_dc = a.cdc[co];
+  const bool f_thr = a.cb0[co] >= 0.0f, f_b0 = a.cb0[co] > 0.5f;
   // 2^-24 (1 + 2^-9) times the weighted window sum, rounding up (the 2^-9
   // also covers the round-to-nearest steps of A, Q and E below)
   const float cA = 0x1p-24f * (1.0f + 0x1p-9f);
@@ -406,11 +409,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         // E, then room for rounding v -+ E to nearest
         const float E = __fadd_rn(__fmaf_rn(cA, Aw[k], __fmul_rn(Qs, 1.0f + 0x1p-9f)), 0x1p-110f);
         const float Ev = __fmaf_rn(fabsf(v[k]), 0x1p-22f, __fmul_rn(E, 1.0f + 0x1p-20f));
-        float zl_, zh_;
-        const bool bl = fold_bit(__fsub_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zl_);
-        const bool bh = fold_bit(__fadd_rn(v[k], Ev), f_al, f_A, f_B, f_sl, f_rs, zh_);
-        const bool ok = bl == bh && (mono || (zl_ < 0.0f) == (zh_ < 0.0f)) && !__builtin_isnan(zl_) && !__builtin_isnan(zh_);
-        bit[k] = bl && chan;
+        const float lo = __fsub_rn(v[k], Ev), hi = __fadd_rn(v[k], Ev);
+        const bool c1 = lo >= f_t1, c2 = lo >= f_t2;
+        const bool ok = f_thr && (hi >= f_t1) == c1 && (hi >= f_t2) == c2 && lo >= -f_dc && hi <= f_dc;
+        bit[k] = (f_b0 ^ c1 ^ c2) && chan;
         unc[k] = !ok && chan && fpx0 + k >= vlo && fpx0 + k < vhi;
       }
       uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
@@ -502,7 +504,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
 
 hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
-  if (!a.cwb || !a.cws || !a.out || a.f32 || a.hout) return hipErrorInvalidValue;
+  if (!a.cwb || !a.cws || !a.ct1 || !a.ct2 || !a.cb0 || !a.cdc || !a.out || a.f32 || a.hout) return hipErrorInvalidValue;
   const int rowlen = a.pcols > 0 ? a.sW : a.W;
   if (!real_cert_fits(a.cin, a.W, rowlen) || (uintptr_t)a.x % 16) return hipErrorInvalidValue;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
