@@ -22,7 +22,7 @@
 // matrix core's result is exact whatever its internal order.  The digit sums
 // are recombined (2048 Zh + Zl) and scaled back by 2^(e - 21) in fp32.
 //
-// E = 2^-24 (1 + 2^-8) A + (1 + 2^-8) Q + 2^-110, rounded up, with
+// E = 2^-24 (1 + 2^-8) A + (1 + 2^-8) Q + 2^-109, rounded up, with
 //  * A = sum over the output's 3 x 3 x cin window of (cin - ci + 16) |x|,
 //    ci the input channel;
 //  * Q = half a grid step 2^(e-21) per term: 48 * 2^(e-21) per (input row,
@@ -256,9 +256,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   // marks a channel whose every output is recomputed
   const float f_t1 = a.ct1[co], f_t2 = a.ct2[co], f_dc = a.cdc[co];
   const bool f_thr = a.cb0[co] >= 0.0f, f_b0 = a.cb0[co] > 0.5f;
-  // 2^-24 (1 + 2^-9) times the weighted window sum, rounding up (the 2^-9
-  // also covers the round-to-nearest steps of A, Q and E below)
-  const float cA = 0x1p-24f * (1.0f + 0x1p-9f);
+  // 2^-24 (1 + 2^-9 + 2^-19) times the weighted window sum: the 2^-9 covers
+  // the round-to-nearest steps of A and Q, the 2^-19 those of E and the room
+  // for rounding v -+ E to nearest (with the |v| 2^-22 term below)
+  const float cA = 0x1p-24f * (1.0f + 0x1p-9f + 0x1p-19f);
   const int cwo = (a.cout + 31) >> 5;
   const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
 
@@ -403,12 +404,14 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
       }
       const float4 qq = *reinterpret_cast<const float4*>(qw);
       const float Qs = __fadd_rn(__fadd_rn(qq.x, qq.y), __fadd_rn(qq.z, qq.w));
+      // the row's quantisation part of E with its margins, and 2^-109 for
+      // underflow
+      const float Qc = __fadd_rn(__fmul_rn(Qs, 1.0f + 0x1p-9f + 0x1p-19f), 0x1p-109f);
       bool bit[2], unc[2];
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        // E, then room for rounding v -+ E to nearest
-        const float E = __fadd_rn(__fmaf_rn(cA, Aw[k], __fmul_rn(Qs, 1.0f + 0x1p-9f)), 0x1p-110f);
-        const float Ev = __fmaf_rn(fabsf(v[k]), 0x1p-22f, __fmul_rn(E, 1.0f + 0x1p-20f));
+        // E with room for rounding v -+ E to nearest
+        const float Ev = __fmaf_rn(fabsf(v[k]), 0x1p-22f, __fmaf_rn(cA, Aw[k], Qc));
         const float lo = __fsub_rn(v[k], Ev), hi = __fadd_rn(v[k], Ev);
         const bool c1 = lo >= f_t1, c2 = lo >= f_t2;
         const bool ok = f_thr && (hi >= f_t1) == c1 && (hi >= f_t2) == c2 && lo >= -f_dc && hi <= f_dc;
