@@ -51,6 +51,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "bnn_device.h"
 #include "bnn_kernels.h"
 
@@ -515,12 +517,17 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   const int nld = (a.cin + 7) / 8;
   const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4;
   const bool guard = a.cin / 4 < 28;
-  static bool attr[2] = {false, false};
-  if (!attr[guard]) {
+  // the kernel asks for more than 64 KiB of LDS: allow it once per variant
+  // and device (bit d of the variant's mask for device d)
+  static std::atomic<uint64_t> attr[2];
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr[guard].load(std::memory_order_acquire) & bit)) {
     hipError_t e = guard ? hipFuncSetAttribute((const void*)k_real_cert<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)
                          : hipFuncSetAttribute((const void*)k_real_cert<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
-    attr[guard] = true;
+    attr[guard].fetch_or(bit, std::memory_order_acq_rel);
   }
   const long ntile = a.W <= 32 ? 1 : (a.W + 23) / 24;
   if ((long)a.N * ntile >= 0x7FFFFFFF) return hipErrorInvalidValue;
