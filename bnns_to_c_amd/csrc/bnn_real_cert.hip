@@ -111,11 +111,14 @@ __device__ __forceinline__ bool fold_bit(float v, float al, float A, float B, fl
 }
 
 // the LDS byte offset of (channel ci, column x) in a row buffer: 16-byte
-// column groups of channels with bit 1 set are swapped in halves (group
-// g -> g ^ 4), which puts the four lane rows of an operand read in four
-// different 16-bank quarters
+// column groups of channels whose bits 0 and 1 differ are swapped in halves
+// (group g -> g ^ 4).  An operand read takes four consecutive channels, one
+// per 16-lane row: with 64 banks the four land in four different 16-bank
+// quarters, and with 32 the two channels of each half-wave in different
+// 16-bank halves.
+__device__ __forceinline__ uint32_t row_swz(int ci) { return (uint32_t)((ci ^ (ci >> 1)) & 1); }
 __device__ __forceinline__ uint32_t row_off(int ci, int x) {
-  return (uint32_t)ci * 128u + ((uint32_t)((x >> 2) ^ (((ci >> 1) & 1) << 2)) << 4) + (uint32_t)(x & 3) * 4u;
+  return (uint32_t)ci * 128u + ((uint32_t)((x >> 2) ^ (row_swz(ci) << 2)) << 4) + (uint32_t)(x & 3) * 4u;
 }
 __device__ __forceinline__ void block_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -206,7 +209,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   for (int m = 0; m < 4; ++m) {
     const int k = wv + 4 * m;
     const int ci = 8 * k + (lane >> 3);
-    const int g4 = (lane & 7) ^ (((ci >> 1) & 1) << 2);
+    const int g4 = (lane & 7) ^ (int)(row_swz(ci) << 2);
     const int cg = wx0 + 4 * g4;  // image column of the 16-byte group
     const bool ok = k < nld && ci < cin && cg >= 0 && cg < ig.xlim;
     doff[m] = ok ? (uint32_t)(ig.base + (size_t)ci * ig.cstride + cg) * 4u : kCertFar;
@@ -435,8 +438,8 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         const int iy = r + ky - 1, ix = upx + kx - 1;
         if (lane < 9 && iy >= 0 && iy < H && wx0 + ix >= 0 && wx0 + ix < W) {
           // lane t sums tap t: its four sign-mask words, then the channels
-          // in batches of 32 read ahead of their adds (channels 4 m, 4 m + 1
-          // at column offset c0, 4 m + 2, 4 m + 3 at the swapped one, as
+          // in batches of 32 read ahead of their adds (channels 4 m, 4 m + 3
+          // at column offset c0, 4 m + 1, 4 m + 2 at the swapped one, as
           // row_off lays them out).  A last partial batch reads up to 28
           // channels past cin, inside the block's LDS (a row buffer holds
           // at least cin channels and 11 KiB of partials follow the ring),
@@ -444,17 +447,17 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
           // unchanged.
           const uint4 m4 = *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4]);
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
-          const float* c0 = rowp + (row_off(0, ix) >> 2);
-          const float* c1 = rowp + (row_off(2, ix) >> 2) - 64;
+          const float* c0 = rowp + (row_off(0, ix) >> 2);       // channels 4 m, 4 m + 3
+          const float* c1 = rowp + (row_off(1, ix) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
           for (int cb = 0; cb < cin; cb += 32) {
             float xb[32];
 #pragma unroll
             for (int j = 0; j < 32; j += 4) {
               const int c4 = cb + j;
               xb[j] = c0[c4 * 32];
-              xb[j + 1] = c0[c4 * 32 + 32];
+              xb[j + 1] = c1[c4 * 32 + 32];
               xb[j + 2] = c1[c4 * 32 + 64];
-              xb[j + 3] = c1[c4 * 32 + 96];
+              xb[j + 3] = c0[c4 * 32 + 96];
             }
             // -x for a clear mask bit: bit j of the inverted word moved to
             // the sign position
