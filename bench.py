@@ -580,7 +580,7 @@ def main() -> int:
     real_flops = 2 * real_work
     achieved = real_flops / (real["ms"] / 1e3)
     # which first-conv kernel ran: the certified one unless BNN_CERT=0 (its
-    # shape condition, cin <= 128 and W <= 32 in multiples of 4, holds here)
+    # shape condition, 4 <= cin <= 128 and W in multiples of 4, holds here)
     cert = os.environ.get("BNN_CERT") != "0"
     real_bytes = N * 120 * H * W * 4 + N * H * W * 4  # input floats once, output words once
     if cert:
