@@ -52,6 +52,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "bnn_device.h"
 #include "bnn_kernels.h"
@@ -80,22 +81,21 @@ __device__ __forceinline__ uint32_t dmov(uint32_t src) {
 }
 constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121, kRor15 = 0x12F;
 
-// Operands of the pixel to the left (kx = 0) and right (kx = 2): lane p of a
-// 16-lane row holds pixel 16 s + p of segment s.  Pixel -1 and pixel 32 are
-// outside every row of width <= 32 and read 0.
-__device__ __forceinline__ void shift_left(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
+// Pixel layout of the operands: lane p of a 16-lane row holds pixel 2p of
+// the even segment (s = 0) and pixel 2p + 1 of the odd segment (s = 1).
+// The left neighbour (kx = 0) of pixel 2p is the odd segment one lane down
+// (lane 0: pixel -1, read as 0), of pixel 2p + 1 the even segment's own
+// lane; the right neighbour (kx = 2) of pixel 2p is the odd segment's own
+// lane, of 2p + 1 the even segment one lane up (lane 15: pixel 32, read as
+// 0).  So each direction moves one segment by one lane, and the moved-in
+// zeros are exactly the zero padding of a 32-column window.
+__device__ __forceinline__ void lane_down(const cert_u32x4& a, cert_u32x4& o) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[0][i] = dmov<kShr1>(a[0][i]);
-    o[1][i] = dpp<kShr1, false>(dmov<kRor1>(a[0][i]), a[1][i]);
-  }
+  for (int i = 0; i < 4; ++i) o[i] = dmov<kShr1>(a[i]);
 }
-__device__ __forceinline__ void shift_right(const cert_u32x4 (&a)[2], cert_u32x4 (&o)[2]) {
+__device__ __forceinline__ void lane_up(const cert_u32x4& a, cert_u32x4& o) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[0][i] = dpp<kShl1, false>(dmov<kRor15>(a[1][i]), a[0][i]);
-    o[1][i] = dmov<kShl1>(a[1][i]);
-  }
+  for (int i = 0; i < 4; ++i) o[i] = dmov<kShl1>(a[i]);
 }
 
 __device__ __forceinline__ float f32_of(uint32_t b) { return __builtin_bit_cast(float, b); }
@@ -143,20 +143,19 @@ __device__ __forceinline__ float rows_sum(float x) {
   const auto r32 = __builtin_amdgcn_permlane32_swap(bits_of(y), bits_of(y), false, false);
   return __fadd_rn(f32_of(r32[0]), f32_of(r32[1]));
 }
-// per-pixel value (segment s in v[s]) plus its left and right neighbours
+// per-pixel value (pixel 2p + s in v[s]) plus its left and right neighbours
 __device__ __forceinline__ void window3(const float (&v)[2], float (&o)[2]) {
-  const uint32_t a0 = bits_of(v[0]), a1 = bits_of(v[1]);
-  const float l0 = f32_of(dmov<kShr1>(a0));
-  const float l1 = f32_of(dpp<kShr1, false>(dmov<kRor1>(a0), a1));
-  const float r0 = f32_of(dpp<kShl1, false>(dmov<kRor15>(a1), a0));
-  const float r1 = f32_of(dmov<kShl1>(a1));
-  o[0] = __fadd_rn(__fadd_rn(l0, v[0]), r0);
-  o[1] = __fadd_rn(__fadd_rn(l1, v[1]), r1);
+  const float l = f32_of(dmov<kShr1>(bits_of(v[1])));  // pixel 2p - 1
+  const float r = f32_of(dmov<kShl1>(bits_of(v[0])));  // pixel 2p + 2
+  const float c = __fadd_rn(v[0], v[1]);
+  o[0] = __fadd_rn(c, l);
+  o[1] = __fadd_rn(c, r);
 }
-// a wave's partial of one output row: (pixel, channel) at
-// ((px / 4) * 16 + c) * 4 + px % 4, so a lane's four MFMA result rows are
-// one 16-byte store
-__device__ __forceinline__ int part_idx(int px, int c) { return ((px >> 2) * 16 + c) * 4 + (px & 3); }
+// a wave's partial of one output row: MFMA result register i of lane
+// (channel c, row group g) of segment s, pixel 8 g + 2 i + s, at
+// ((s * 4 + g) * 16 + c) * 4 + i, so a lane's four result rows are one
+// 16-byte store
+__device__ __forceinline__ int part_idx(int s, int g, int c) { return ((s * 4 + g) * 16 + c) * 4; }
 
 // Wave w converts input channels cpw * w .. cpw * w + cpw - 1 (cpw = cin / 4):
 // element j of lane (p, gq) is channel cpw * w + 4 j + gq, column 16 s + p;
@@ -236,10 +235,9 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
     }
   };
 
-  // conversion reads and the lane's valid elements
-  uint32_t rdoff[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) rdoff[s] = row_off(cpw * wv + gq, 16 * s + p);
+  // conversion reads (pixels 2p and 2p + 1 of element j's channel, one
+  // 8-byte read) and the lane's valid elements
+  const uint32_t rdoff = row_off(cpw * wv + gq, 2 * p);
   uint32_t jvalid = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) jvalid |= (4 * j + gq < cpw ? 1u : 0u) << j;
@@ -267,16 +265,26 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   const float cA = 0x1p-24f * (1.0f + 0x1p-9f + 0x1p-19f);
   const int cwo = (a.cout + 31) >> 5;
   const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
+  // the partials of pixels fpx0 (even segment) and fpx0 + 1 (odd, 256 floats
+  // on) in a wave's partial: segment row group wv, register fq
+  const int i0 = part_idx(0, wv, fc) + fq;
 
   issue(0);
 
-  cert_f32x4 op[2], oc[2], on[2];
+  // rolling state, indexed by row mod 3: acc[r % 3] the partial of output
+  // row r, ab[y % 3] / qr[y % 3] the window sums and Q of input row y.  The
+  // row loop is unrolled by three so that every index is a constant.
+  cert_f32x4 acc[3][2];
+  float ab[3][2], qr[3];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) op[s] = oc[s] = on[s] = (cert_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-  float ab1[2] = {0.0f, 0.0f}, ab2[2] = {0.0f, 0.0f};  // window sums of rows yi - 1, yi - 2
-  float q1 = 0.0f, q2 = 0.0f;
+  for (int k = 0; k < 3; ++k) {
+    acc[k][0] = acc[k][1] = (cert_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    ab[k][0] = ab[k][1] = 0.0f;
+    qr[k] = 0.0f;
+  }
 
   for (int yi = 0; yi <= H; ++yi) {
+    constexpr int c0 = 0, cn = 1, cp = 2;  // yi % 3, (yi + 1) % 3, (yi - 1) % 3 after rotation
     const bool has = yi < H;
     // row yi landed, this wave's LDS traffic done, then every wave's
     wait_vm_lgkm<0>();
@@ -288,19 +296,19 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
       const float* row = cert_lds + (size_t)(yi % kCertRing) * rb / 4;
       float xv[2][8];
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = row[(rdoff[s] + (uint32_t)j * 512u) / 4];
-          xv[s][j] = (GUARD || j == 7) ? ((jvalid >> j) & 1u ? v : 0.0f) : v;
-        }
+      for (int j = 0; j < 8; ++j) {
+        const float2 v = *reinterpret_cast<const float2*>(&row[(rdoff + (uint32_t)j * 512u) / 4]);
+        const bool ok = (GUARD || j == 7) ? ((jvalid >> j) & 1u) != 0 : true;
+        xv[0][j] = ok ? v.x : 0.0f;
+        xv[1][j] = ok ? v.y : 0.0f;
+      }
       // the wave's largest |x|: within each 16-lane row by rotation, then the
       // four rows through scalar registers (|x| bits order as unsigned
       // integers; a NaN input reaches v' as NaN and is recomputed)
       float m = 0.0f, as[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        m = fmaxf(m, fmaxf(fabsf(xv[0][j]), fabsf(xv[1][j])));
+        m = fmaxf(fmaxf(m, fabsf(xv[0][j])), fabsf(xv[1][j]));
         as[0] = __fmaf_rn(fabsf(xv[0][j]), wsum[j], as[0]);
         as[1] = __fmaf_rn(fabsf(xv[1][j]), wsum[j], as[1]);
       }
@@ -345,65 +353,73 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
           zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[s]), Bw[ky * 3 + 1], z4, 0, 0, 0);
         }
       {
-        cert_u32x4 sh[2], sl[2];
-        shift_left(hi, sh);
-        shift_left(lo, sl);
+        // kx = 0: even pixels take the odd segment one lane down, odd pixels
+        // the even segment
+        cert_u32x4 dh, dl;
+        lane_down(hi[1], dh);
+        lane_down(lo[1], dl);
 #pragma unroll
-        for (int ky = 0; ky < 3; ++ky)
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sh[s]), Bw[ky * 3], zh[ky][s], 0, 0, 0);
-            zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sl[s]), Bw[ky * 3], zl[ky][s], 0, 0, 0);
-          }
+        for (int ky = 0; ky < 3; ++ky) {
+          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dh), Bw[ky * 3], zh[ky][0], 0, 0, 0);
+          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dl), Bw[ky * 3], zl[ky][0], 0, 0, 0);
+          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[0]), Bw[ky * 3], zh[ky][1], 0, 0, 0);
+          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[0]), Bw[ky * 3], zl[ky][1], 0, 0, 0);
+        }
       }
       {
-        cert_u32x4 sh[2], sl[2];
-        shift_right(hi, sh);
-        shift_right(lo, sl);
+        // kx = 2: even pixels take the odd segment, odd pixels the even
+        // segment one lane up
+        cert_u32x4 uh, ul;
+        lane_up(hi[0], uh);
+        lane_up(lo[0], ul);
 #pragma unroll
-        for (int ky = 0; ky < 3; ++ky)
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sh[s]), Bw[ky * 3 + 2], zh[ky][s], 0, 0, 0);
-            zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(sl[s]), Bw[ky * 3 + 2], zl[ky][s], 0, 0, 0);
-          }
+        for (int ky = 0; ky < 3; ++ky) {
+          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[1]), Bw[ky * 3 + 2], zh[ky][0], 0, 0, 0);
+          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[1]), Bw[ky * 3 + 2], zl[ky][0], 0, 0, 0);
+          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(uh), Bw[ky * 3 + 2], zh[ky][1], 0, 0, 0);
+          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ul), Bw[ky * 3 + 2], zl[ky][1], 0, 0, 0);
+        }
       }
       // input row yi feeds output rows yi + 1 (ky 0), yi (ky 1), yi - 1 (ky 2)
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          on[s][r] = __fmul_rn(__fmaf_rn(zh[0][s][r], 2048.0f, zl[0][s][r]), sb);
-          oc[s][r] = __fmaf_rn(__fmaf_rn(zh[1][s][r], 2048.0f, zl[1][s][r]), sb, oc[s][r]);
-          op[s][r] = __fmaf_rn(__fmaf_rn(zh[2][s][r], 2048.0f, zl[2][s][r]), sb, op[s][r]);
+          acc[cn][s][r] = __fmul_rn(__fmaf_rn(zh[0][s][r], 2048.0f, zl[0][s][r]), sb);
+          acc[c0][s][r] = __fmaf_rn(__fmaf_rn(zh[1][s][r], 2048.0f, zl[1][s][r]), sb, acc[c0][s][r]);
+          acc[cp][s][r] = __fmaf_rn(__fmaf_rn(zh[2][s][r], 2048.0f, zl[2][s][r]), sb, acc[cp][s][r]);
         }
     }
+    ab[c0][0] = abn[0];
+    ab[c0][1] = abn[1];
+    qr[c0] = qn;
 
     if (yi >= 1) {
-      // output row r = yi - 1 is complete in op: each wave leaves its partial,
-      // its window sum of |x| and its quantisation bound in LDS
+      // output row r = yi - 1 is complete in acc[cp]: each wave leaves its
+      // partial, its window sum of |x| (rows yi - 2, yi - 1, yi) and its
+      // quantisation bound in LDS
       const int r = yi - 1;
       float* mine = opart + wv * 512;
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        *reinterpret_cast<float4*>(&mine[part_idx(16 * s + 4 * gq, p)]) = make_float4(op[s][0], op[s][1], op[s][2], op[s][3]);
-      if (gq == 0) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) absw[wv * 32 + 16 * s + p] = __fadd_rn(__fadd_rn(ab2[s], ab1[s]), abn[s]);
-      }
-      if (lane == 0) qw[wv] = __fadd_rn(__fadd_rn(q2, q1), qn);
+        *reinterpret_cast<float4*>(&mine[part_idx(s, gq, p)]) =
+            make_float4(acc[cp][s][0], acc[cp][s][1], acc[cp][s][2], acc[cp][s][3]);
+      if (gq == 0)
+        *reinterpret_cast<float2*>(&absw[wv * 32 + 2 * p]) =
+            make_float2(__fadd_rn(__fadd_rn(ab[cn][0], ab[cp][0]), ab[c0][0]),
+                        __fadd_rn(__fadd_rn(ab[cn][1], ab[cp][1]), ab[c0][1]));
+      if (lane == 0) qw[wv] = __fadd_rn(__fadd_rn(qr[cn], qr[cp]), qr[c0]);
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
       block_barrier();
 
       // finalize: the four partials in wave order
       float v[2] = {0.0f, 0.0f}, Aw[2] = {0.0f, 0.0f};
-      const int i0 = part_idx(fpx0, fc);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float2 t = *reinterpret_cast<const float2*>(&opart[w * 512 + i0]);
+        const float t0 = opart[w * 512 + i0], t1 = opart[w * 512 + i0 + 256];
         const float2 u = *reinterpret_cast<const float2*>(&absw[w * 32 + fpx0]);
-        v[0] = __fadd_rn(v[0], t.x);
-        v[1] = __fadd_rn(v[1], t.y);
+        v[0] = __fadd_rn(v[0], t0);
+        v[1] = __fadd_rn(v[1], t1);
         Aw[0] = __fadd_rn(Aw[0], u.x);
         Aw[1] = __fadd_rn(Aw[1], u.y);
       }
@@ -447,17 +463,17 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
           // unchanged.
           const uint4 m4 = *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4]);
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
-          const float* c0 = rowp + (row_off(0, ix) >> 2);       // channels 4 m, 4 m + 3
-          const float* c1 = rowp + (row_off(1, ix) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
+          const float* ch0 = rowp + (row_off(0, ix) >> 2);       // channels 4 m, 4 m + 3
+          const float* ch1 = rowp + (row_off(1, ix) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
           for (int cb = 0; cb < cin; cb += 32) {
             float xb[32];
 #pragma unroll
             for (int j = 0; j < 32; j += 4) {
               const int c4 = cb + j;
-              xb[j] = c0[c4 * 32];
-              xb[j + 1] = c1[c4 * 32 + 32];
-              xb[j + 2] = c1[c4 * 32 + 64];
-              xb[j + 3] = c0[c4 * 32 + 96];
+              xb[j] = ch0[c4 * 32];
+              xb[j + 1] = ch1[c4 * 32 + 32];
+              xb[j + 2] = ch1[c4 * 32 + 64];
+              xb[j + 3] = ch0[c4 * 32 + 96];
             }
             // -x for a clear mask bit: bit j of the inverted word moved to
             // the sign position
@@ -469,21 +485,21 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
               const uint32_t live = (1u << (cin - cb)) - 1u;
 #pragma unroll
               for (int j = 0; j < 32; ++j) {
-                const float v = f32_of(bits_of(xb[j]) ^ ((nw << (31 - j)) & 0x80000000u));
-                st = __fadd_rn(st, ((live >> j) & 1u) ? v : 0.0f);
+                const float xs = f32_of(bits_of(xb[j]) ^ ((nw << (31 - j)) & 0x80000000u));
+                st = __fadd_rn(st, ((live >> j) & 1u) ? xs : 0.0f);
               }
             }
           }
         }
-        float acc = 0.0f;
+        float tot = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 9; ++t) acc = __fadd_rn(acc, f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(st), t)));
+        for (int t = 0; t < 9; ++t) tot = __fadd_rn(tot, f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(st), t)));
         // the channel's fold parameters from lane li, which holds them
         auto from_li = [&](float f) __attribute__((always_inline)) {
           return f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(f), li));
         };
         float zz;
-        const bool ub = fold_bit(acc, from_li(f_al), from_li(f_A), from_li(f_B), from_li(f_sl), from_li(f_rs), zz);
+        const bool ub = fold_bit(tot, from_li(f_al), from_li(f_A), from_li(f_B), from_li(f_sl), from_li(f_rs), zz);
         bm[which] = ub ? (bm[which] | (1ull << li)) : (bm[which] & ~(1ull << li));
       }
 
@@ -496,15 +512,16 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
       }
     }
+    // next step: output rows yi + 1 and yi, input rows yi - 1 and yi
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      op[s] = oc[s];
-      oc[s] = on[s];
-      ab2[s] = ab1[s];
-      ab1[s] = abn[s];
+      acc[cp][s] = acc[c0][s];
+      acc[c0][s] = acc[cn][s];
+      ab[cn][s] = ab[cp][s];
+      ab[cp][s] = ab[c0][s];
     }
-    q2 = q1;
-    q1 = qn;
+    qr[cn] = qr[cp];
+    qr[cp] = qr[c0];
   }
 }
 
