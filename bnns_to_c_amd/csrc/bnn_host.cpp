@@ -424,6 +424,10 @@ struct BnnDevice {
   uint32_t* rcws = nullptr;
   float *rct1 = nullptr, *rct2 = nullptr, *rcb0 = nullptr, *rcdc = nullptr;  // its fold summary
   bool cert = false;
+  // outputs the certified conv recomputed (device) and certified in all
+  // (host), since the last bnn_cert_stats
+  unsigned long long* rcnt = nullptr;
+  unsigned long long cert_outputs = 0;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   bool mid = false;  // the fused middle applies (mid_fits at load, and mid_mode())
   float *hw = nullptr, *hb = nullptr;
@@ -589,6 +593,8 @@ int upload_real(BnnDevice* D, const Conv& c, const Act& a) {
     if ((rc = dev_upload(D, &D->rct2, t2.data(), np))) return rc;
     if ((rc = dev_upload(D, &D->rcb0, b0.data(), np))) return rc;
     if ((rc = dev_upload(D, &D->rcdc, dc.data(), np))) return rc;
+    const unsigned long long zero = 0;
+    if ((rc = dev_upload(D, &D->rcnt, &zero, 1))) return rc;
   }
   return BNN_OK;
 }
@@ -834,7 +840,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
       ra.cwb = D->rcwb;
       ra.cws = D->rcws;
       ra.ct1 = D->rct1; ra.ct2 = D->rct2; ra.cb0 = D->rcb0; ra.cdc = D->rcdc;
+      ra.ucnt = D->rcnt;
       HIP_TRY(launch_real_cert(ra, st));
+      D->cert_outputs += (unsigned long long)cnt * D->rcout * H * W;
       if ((rc = mark("enc1.conv1", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin * 9))) return rc;
     } else {
       HIP_TRY(launch_real(ra, st));
@@ -1652,6 +1660,22 @@ void prof_report(FILE* o) {
   }
   fprintf(o, "# total per-op: %.4f ms\n", tot * 1e3);
 }
+int bnn_cert_stats(const Model* m, unsigned long long* undecided, unsigned long long* outputs) {
+  if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
+  BnnDevice* D = m->dev;
+  unsigned long long u = 0;
+  if (D->rcnt) {
+    HIP_TRY(hipSetDevice(D->device));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(&u, D->rcnt, sizeof u, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemset(D->rcnt, 0, sizeof u));
+  }
+  if (undecided) *undecided = u;
+  if (outputs) *outputs = D->cert_outputs;
+  D->cert_outputs = 0;
+  return BNN_OK;
+}
+
 void bnn_prof_enable(int on) { g_prof_on = on != 0; }
 int bnn_prof_count(void) { return (int)g_prof.size(); }
 int bnn_prof_get(int i, char* label, int label_len, char* optype, int optype_len, double* ms, double* work) {

@@ -114,6 +114,9 @@ struct RealArgs {
   const uint32_t* cws;
   // its fold summary per channel (real_fold_switches), padded like alpha
   const float *ct1, *ct2, *cb0, *cdc;
+  // where it adds the number of outputs it recomputed in the reference's
+  // order (may be null)
+  unsigned long long* ucnt;
   const float* alpha;   // per-channel arrays padded to a multiple of 32
   const float* A;
   const float* B;

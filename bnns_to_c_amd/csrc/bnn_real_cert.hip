@@ -143,6 +143,18 @@ __device__ __forceinline__ float rows_sum(float x) {
   const auto r32 = __builtin_amdgcn_permlane32_swap(bits_of(y), bits_of(y), false, false);
   return __fadd_rn(f32_of(r32[0]), f32_of(r32[1]));
 }
+// the largest of the lanes' non-negative floats, as bits (which order as
+// unsigned integers): within each 16-lane row by rotation, then the four
+// rows through scalar registers
+__device__ __forceinline__ uint32_t wave_max_bits(float m) {
+  uint32_t mb = bits_of(m);
+  mb = max(mb, dpp<0x128, false>(mb, mb));  // row_ror:8
+  mb = max(mb, dpp<0x124, false>(mb, mb));  // row_ror:4
+  mb = max(mb, dpp<0x122, false>(mb, mb));  // row_ror:2
+  mb = max(mb, dpp<kRor1, false>(mb, mb));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)mb, 0), (uint32_t)__builtin_amdgcn_readlane((int)mb, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)mb, 32), (uint32_t)__builtin_amdgcn_readlane((int)mb, 48)));
+}
 // per-pixel value (pixel 2p + s in v[s]) plus its left and right neighbours
 __device__ __forceinline__ void window3(const float (&v)[2], float (&o)[2]) {
   const float l = f32_of(dmov<kShr1>(bits_of(v[1])));  // pixel 2p - 1
@@ -283,6 +295,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
     qr[k] = 0.0f;
   }
 
+  uint32_t nund = 0;  // outputs this wave recomputed
   for (int yi = 0; yi <= H; ++yi) {
     constexpr int c0 = 0, cn = 1, cp = 2;  // yi % 3, (yi + 1) % 3, (yi - 1) % 3 after rotation
     const bool has = yi < H;
@@ -302,9 +315,8 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         xv[0][j] = ok ? v.x : 0.0f;
         xv[1][j] = ok ? v.y : 0.0f;
       }
-      // the wave's largest |x|: within each 16-lane row by rotation, then the
-      // four rows through scalar registers (|x| bits order as unsigned
-      // integers; a NaN input reaches v' as NaN and is recomputed)
+      // the wave's largest |x| (max ignores a NaN, which reaches v' and A as
+      // NaN)
       float m = 0.0f, as[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -312,13 +324,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
         as[0] = __fmaf_rn(fabsf(xv[0][j]), wsum[j], as[0]);
         as[1] = __fmaf_rn(fabsf(xv[1][j]), wsum[j], as[1]);
       }
-      uint32_t mb = bits_of(m);
-      mb = max(mb, dpp<0x128, false>(mb, mb));  // row_ror:8
-      mb = max(mb, dpp<0x124, false>(mb, mb));  // row_ror:4
-      mb = max(mb, dpp<0x122, false>(mb, mb));  // row_ror:2
-      mb = max(mb, dpp<kRor1, false>(mb, mb));
-      const uint32_t mw = max(max((uint32_t)__builtin_amdgcn_readlane((int)mb, 0), (uint32_t)__builtin_amdgcn_readlane((int)mb, 16)),
-                              max((uint32_t)__builtin_amdgcn_readlane((int)mb, 32), (uint32_t)__builtin_amdgcn_readlane((int)mb, 48)));
+      const uint32_t mw = wave_max_bits(m);
       const bool finite = mw < 0x7F800000u;
       const int e = finite ? max((int)(mw >> 23) - 127, -100) : 127;
       const float sc = f32_of((uint32_t)(127 + 10 - e) << 23);
@@ -441,6 +447,19 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
       }
       uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
       uint64_t um[2] = {__ballot(unc[0]), __ballot(unc[1])};
+      if (um[0] | um[1]) {
+        // A is NaN exactly when the window holds a NaN (its terms are |x|
+        // times positive weights; such an output is never certified): the
+        // reference's sum is then NaN and the fold's bit 0 for any
+        // parameters (NaN > 0 is false), so it needs no recompute
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const uint64_t nm = __ballot(Aw[k] != Aw[k]);
+          um[k] &= ~nm;
+          bm[k] &= ~nm;
+        }
+        nund += (uint32_t)(__builtin_popcountll(um[0]) + __builtin_popcountll(um[1]));
+      }
 
       // uncertain outputs: the reference's order, lane t < 9 summing tap t
       // over the channels from the LDS rows r - 1 .. r + 1
@@ -523,6 +542,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
     qr[cn] = qr[cp];
     qr[cp] = qr[c0];
   }
+  if (a.ucnt && nund && lane == 0) atomicAdd(a.ucnt, (unsigned long long)nund);
 }
 
 }  // namespace

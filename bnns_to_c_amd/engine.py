@@ -74,6 +74,7 @@ def lib() -> C.CDLL:
     L.bnn_forward_batch.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32]
     L.bnn_forward_device.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
     L.bnn_forward_device_noalloc.argtypes = [_vp, _vp, _ci, _ci, _ci, _vp, _vp]
+    L.bnn_cert_stats.argtypes = [_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)]
     L.bnn_forward_debug.argtypes = [_vp, _f32, _ci, _ci, _ci, _f32, STAGE_CB, _vp]
     L.bnn_forward_patched.argtypes = [_vp, _f32, _ci, _ci, _f32, _ci]
     L.bnn_forward_patched_device.argtypes = [_vp, _vp, _ci, _ci, _vp, _ci, _vp]
@@ -218,6 +219,14 @@ class Engine:
         inter-layer tensors live in the library's fixed per-GPU scratch array."""
         _check(lib().bnn_forward_device_noalloc(self.h, _vp(d_in), N, H, W, _vp(d_out),
                                                 _vp(stream or None)))
+
+    def cert_stats(self) -> tuple:
+        """(undecided, outputs) of the certified first conv since the last
+        call (bnn_cert_stats): the outputs it recomputed in the reference's
+        order, and all it made.  Waits for the model's GPU."""
+        u, o = C.c_ulonglong(0), C.c_ulonglong(0)
+        _check(lib().bnn_cert_stats(self.h, C.byref(u), C.byref(o)))
+        return int(u.value), int(o.value)
 
     def forward_patched(self, cube: np.ndarray, P: int = 32) -> np.ndarray:
         """Scene [n_bands, H, W] -> logit map [n_classes, H, W] by independent

@@ -139,6 +139,14 @@ typedef void (*bnn_stage_cb)(void *ctx, const char *name, int dtype, int n, int 
 int bnn_forward_debug(const Model *m, const float *input, int N, int H, int W,
                       float *logits, bnn_stage_cb cb, void *ctx);
 
+/* No counterpart in the reference.  The certified first conv's record since
+ * the previous call (or the load): the outputs it decided from its bounded
+ * approximation plus the ones it recomputed in the reference's order
+ * (*outputs), and the recomputed ones (*undecided).  Waits for all work on
+ * the model's GPU, then resets both counts.  Both are 0 for a model whose
+ * first conv runs in the reference's order (BNN_CERT=0, general signs). */
+int bnn_cert_stats(const Model *m, unsigned long long *undecided, unsigned long long *outputs);
+
 /* Per-op GPU timing of the device forward (hipEvents around every kernel). */
 void bnn_prof_enable(int on);
 int bnn_prof_count(void);

@@ -166,3 +166,43 @@ def test_cert_scene(tmp_path, orc):
     want = scene.stitch(model.forward_batch(scene.cut(cube, 32)), 70, 100)
     assert _bits_equal(got, want)
     eng.close()
+
+
+def test_cert_nan_windows_decided(tmp_path, orc):
+    """An output whose 3x3 window holds a NaN has the reference's tap sum NaN
+    and fold bit 0 for any parameters, so it is decided without a
+    reference-order recompute: a patch of NaNs recomputes nothing, and a
+    patch with NaN blocks only what its finite outputs need."""
+    b = synth.make_blob(seed=53)
+    x = synth.make_input(54, 3, 120, 32, 32)
+    x[0] = np.nan                      # every window
+    x[1, :, 4:12, 6:20] = np.nan       # a block in every band
+    x[2, 17, :, 9] = np.nan            # a column of one band
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    eng.cert_stats()
+    _check(eng, model, x)
+    eng.cert_stats()
+    eng.forward_batch(x[:1])
+    und, outs = eng.cert_stats()
+    assert (und, outs) == (0, 16 * 32 * 32)
+    eng.close()
+
+
+def test_cert_stats_counts(tmp_path):
+    """bnn_cert_stats: outputs certified and recomputed since the last call,
+    then both reset; the exact-order kernel reports none."""
+    b = synth.make_blob(seed=55)
+    x = synth.make_input(56, 64, 120, 32, 32)
+    eng = _engine(tmp_path, b)
+    eng.cert_stats()
+    eng.forward_batch(x)
+    und, outs = eng.cert_stats()
+    assert outs == 64 * 16 * 32 * 32
+    assert 0 < und < outs // 1000
+    assert eng.cert_stats() == (0, 0)
+    eng.close()
+    ex = _engine(tmp_path, b, "e.blob", cert=False)
+    ex.forward_batch(x)
+    assert ex.cert_stats() == (0, 0)
+    ex.close()
