@@ -830,7 +830,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     if (D->stem) {
       HIP_TRY(launch_stem(ra, st));
       if ((rc = mark("stem.conv", "conv_real", (double)N * D->rcout * H * W, (double)D->rcin))) return rc;
-    } else if (D->cert && real_cert_fits(D->rcin, W, sc ? sc->sW : W)) {
+    } else if (D->cert && real_cert_fits(D->rcin, W, sc ? sc->sW : W) && (uintptr_t)ra.x % 16 == 0) {
+      // (the certified kernel stages 16-byte groups; an input that is not
+      // 16-byte aligned takes the exact-order kernel below)
       if (dump) {
         RealArgs rf = ra;
         rf.out = nullptr;
@@ -1349,15 +1351,23 @@ int bnn_forward_device_noalloc(const Model* m, const float* d_input, int N, int 
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
   if (!D->scratch) return set_err(BNN_EHIP, "allocation-free forward unavailable: %s", D->scratch_err.c_str());
+  // sub-batches of at most patches_per_launch, as run_device splits them
+  const int per = patches_per_launch(m, H, W);
   Workspace w;
-  const size_t need = plan_ws(m, D, w, N, H, W, nullptr);
+  const size_t need = plan_ws(m, D, w, std::min(N, per), H, W, nullptr);
   if (need > (size_t)BNN_NOALLOC_SCRATCH_BYTES)
     return set_err(BNN_EARG, "N=%d H=%d W=%d needs %zu bytes of scratch; the allocation-free forward holds %zu",
                    N, H, W, need, (size_t)BNN_NOALLOC_SCRATCH_BYTES);
-  plan_ws(m, D, w, N, H, W, D->scratch);
-  // one part on the caller's stream: no side streams, events or profiling
-  return enqueue_forward(m, D, w, d_input, N, H, W, d_logits, (hipStream_t)stream, nullptr, nullptr, nullptr,
-                         nullptr, 1);
+  for (int n0 = 0; n0 < N; n0 += per) {
+    const int n = std::min(per, N - n0);
+    plan_ws(m, D, w, n, H, W, D->scratch);
+    // one part on the caller's stream: no side streams, events or profiling
+    if ((rc = enqueue_forward(m, D, w, d_input + (size_t)n0 * m->n_bands * H * W, n, H, W,
+                              d_logits + (size_t)n0 * m->n_classes * H * W, (hipStream_t)stream, nullptr, nullptr,
+                              nullptr, nullptr, 1)))
+      return rc;
+  }
+  return BNN_OK;
 }
 
 int bnn_forward_patched(const Model* m, const float* input, int H, int W, float* logits, int P) {

@@ -40,3 +40,65 @@ def test_noalloc_matches_device_forward(tmp_path):
         eng.forward_device_noalloc(x.data_ptr(), 4000, 32, 32, got.data_ptr(), s.cuda_stream)
     assert ei.value.code == E.BNN_EARG and "scratch" in str(ei.value)
     eng.close()
+
+
+def test_noalloc_past_launch_limit(tmp_path):
+    """A call whose input passes the per-launch limit (2 GiB) runs as
+    sub-batches over the same scratch, like bnn_forward_device: 425 bands at
+    32x32 is 1.74 MB per patch, so 1,300 patches are two launches."""
+    import torch
+
+    b = synth.make_blob(seed=3, base=16, n_bands=425)
+    p = tmp_path / "m.blob"
+    p.write_bytes(B.to_bytes(b))
+    eng = E.Engine(str(p))
+    N, H, W = 1300, 32, 32
+    print(f"noalloc case N={N} bands=425", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((N, 425, H, W), device="cuda", generator=g)
+    assert x.numel() * 4 > 2**31
+    s = torch.cuda.Stream()
+    want = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+    got = torch.full((N, b.n_classes, H, W), float("nan"), dtype=torch.float32, device="cuda")
+    eng.forward_device(x.data_ptr(), N, H, W, want.data_ptr(), s.cuda_stream)
+    eng.forward_device_noalloc(x.data_ptr(), N, H, W, got.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    del x
+    eng.close()
+
+
+def test_noalloc_graph_capture(tmp_path):
+    """The allocation-free forward captured in a HIP graph (after one eager
+    call, which does the per-device set-up) and replayed on new inputs, with
+    eager work between the replays: every replay bit-identical to
+    bnn_forward_device on the same input."""
+    import torch
+
+    b = synth.make_blob(seed=1, base=16)
+    p = tmp_path / "m.blob"
+    p.write_bytes(B.to_bytes(b))
+    eng = E.Engine(str(p))
+    N, H, W = 64, 32, 32
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn((N, 120, H, W), device="cuda", generator=gen)
+    y = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+    want = torch.empty_like(y)
+    s = torch.cuda.Stream()
+    eng.forward_device_noalloc(x.data_ptr(), N, H, W, y.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        eng.forward_device_noalloc(x.data_ptr(), N, H, W, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    for r in range(4):
+        print(f"graph replay {r}", flush=True)
+        x.copy_(torch.randn((N, 120, H, W), device="cuda", generator=gen))
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eng.forward_device(x.data_ptr(), N, H, W, want.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32)), r
+    del graph
+    eng.close()
