@@ -248,6 +248,78 @@ def cpu_baseline_react(blob_path: str, budget_s: float):
                       f"OMP_NUM_THREADS={cores}"}
 
 
+def conv_time(engine, torch, fn, reps: int = 5):
+    """Median first-conv time (ms) and median step time (ms) over reps
+    profiled calls of fn, after an untimed settle."""
+    import numpy as np
+    settle(fn, torch, 0.02)
+    torch.cuda.synchronize()
+    steps = []
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        steps.append((time.perf_counter() - t0) * 1e3)
+    engine.prof_enable(False)
+    ms = [m for lab, op, m, w in engine.prof_records() if op == "conv_real"]
+    return float(np.median(ms)), float(np.median(steps))
+
+
+def cert_adversarial(torch, np, engine, blob, synth, td, sp, N, H, W):
+    """The certified first conv on inputs built to leave outputs to its
+    reference-order recompute (csrc/bnn_conv_realin.c:98-111), each against
+    the same batch of N(0,1) patches:
+      ties  every band +-1 (integer tap sums) and each channel's fold placed
+            exactly on one integer sum, so csrc/bnn_fold.c:62-77 sits on
+            z = 0 for about one output in a hundred;
+      nan   a quarter of the patches all NaN, the others with a NaN block in
+            every band (NaN windows are decided without a recompute)."""
+    res = {}
+
+    def run(tag, b, x):
+        path = os.path.join(td, f"adv_{tag}.blob")
+        blob.write(b, path)
+        e = engine.Engine(path)
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.empty((N, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+        fn = lambda: e.forward_device(dx.data_ptr(), N, H, W, dy.data_ptr(), sp)
+        conv_ms, step_ms = conv_time(engine, torch, fn)
+        e.cert_stats()
+        fn()
+        und, outs = e.cert_stats()
+        e.close()
+        res[tag] = {"first_conv_us": round(conv_ms * 1e3, 1), "forward_ms": round(step_ms, 3),
+                    "recomputed_outputs": und, "outputs": outs}
+        log(f"certified conv, {tag} input: {conv_ms * 1e3:.1f} us, {und} of {outs} outputs recomputed")
+
+    b = synth.make_blob(seed=0, base=16)
+    run("normal", b, synth.make_input(1, N, 120, H, W))
+    xn = synth.make_input(1, N, 120, H, W)
+    xn[: N // 4] = np.nan
+    xn[N // 4:, :, 8:16, 10:22] = np.nan
+    run("nan", b, xn)
+    # ties: the fold's B from one of patch 0's own conv outputs per channel
+    bt = synth.make_blob(seed=41)
+    xt = np.random.default_rng(42).choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, H, W))
+    p0 = os.path.join(td, "adv_ties0.blob")
+    blob.write(bt, p0)
+    e0 = engine.Engine(p0)
+    _, st = e0.forward_debug(xt[:1])
+    e0.close()
+    conv = st["enc1.conv1"][0]
+    act = bt.enc_act1[0]
+    A = act.A.astype(np.float32)
+    Bv, rs = act.B.copy(), act.rsign.copy()
+    for c in range(conv.shape[0]):
+        Bv[c] = np.float32(-(A[c] * conv[c, 5 + c, 3 + c]))
+        rs[c] = np.float32(0.0) if c % 2 == 0 else np.float32(1e-30)
+    act.B, act.rsign = Bv.astype(np.float32), rs.astype(np.float32)
+    run("ties", bt, xt)
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,7 +503,24 @@ def main() -> int:
         log(f"scene {SH}x{SW}x{b.n_bands} ({npatch} patches): device {scene_dev_ms:.3f} ms "
             f"({npatch / scene_dev_ms * 1e3:,.0f} patches/s), host pointers {scene_host_ms:.2f} ms "
             f"({cube.nbytes / scene_host_ms / 1e6:.1f} GB/s of input)")
+        # per-kernel times of the device scene call (one launch of 660 patches
+        # per kernel: the batch is not split across streams here)
+        engine.prof_reset()
+        engine.prof_enable(True)
+        for _ in range(reps):
+            eng.forward_patched_device(d_cube.data_ptr(), SH, SW, d_map.data_ptr(), PS, sp)
+        torch.cuda.synchronize()
+        engine.prof_enable(False)
+        agg3 = {}
+        for lab, op, ms, work in engine.prof_records():
+            agg3.setdefault(lab, [op, []])[1].append(ms)
+        scene_kern = [{"label": lab, "op": op, "us": round(float(np.median(v)) * 1e3, 2)}
+                      for lab, (op, v) in agg3.items()]
+        for k3 in scene_kern:
+            log(f"  scene {k3['label']:10s} {k3['op']:12s} {k3['us']:9.1f} us")
         del d_cube, d_map
+
+        adversarial = cert_adversarial(torch, np, engine, blob, synth, td, sp, N, H, W)
 
         # the v2 spectral-stem model (csrc/bnn_model_stem.c): 16-channel stem
         # (the reference exporter's default), base 16, same batch and input
@@ -562,13 +651,24 @@ def main() -> int:
         a = agg.setdefault(lab, [op, [], 0, work])
         a[1].append(ms)
         a[2] += 1
+    # which first-conv kernel ran: the certified one unless BNN_CERT=0 (its
+    # shape condition, 4 <= cin <= 128 and W in multiples of 4, holds here)
+    cert = os.environ.get("BNN_CERT") != "0"
+    real_bytes = N * 120 * H * W * 4 + N * H * W * 4  # input floats once, output words once
     kernels = []
     for lab, (op, mss, cnt, work) in agg.items():
         mean = float(np.median(mss))  # median over the profiled forwards
         if op == "conv_real":
             rate = 2 * work / (mean / 1e3)
-            kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "tflops": round(rate / 1e12, 3),
-                            "frac": round(rate / PEAK_FP32_FLOPS, 4)})
+            if cert:
+                # bound by HBM: frac is the fraction of the 8 TB/s peak
+                kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "bound": "hbm",
+                                "gb_s": round(real_bytes / (mean / 1e3) / 1e9, 1),
+                                "frac": round(real_bytes / (mean / 1e3) / PEAK_HBM, 4),
+                                "fp32_equivalent_tflops": round(rate / 1e12, 3)})
+            else:
+                kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "bound": "mfma",
+                                "tflops": round(rate / 1e12, 3), "frac": round(rate / PEAK_FP32_FLOPS, 4)})
         else:
             rate = 2 * work / (mean / 1e3)
             kernels.append({"label": lab, "op": op, "ms": round(mean, 5), "tbinops": round(rate / 1e12, 2),
@@ -579,12 +679,13 @@ def main() -> int:
     real_work = agg[real["label"]][3]
     real_flops = 2 * real_work
     achieved = real_flops / (real["ms"] / 1e3)
-    # which first-conv kernel ran: the certified one unless BNN_CERT=0 (its
-    # shape condition, 4 <= cin <= 128 and W in multiples of 4, holds here)
-    cert = os.environ.get("BNN_CERT") != "0"
-    real_bytes = N * 120 * H * W * 4 + N * H * W * 4  # input floats once, output words once
     if cert:
         rate_b = real_bytes / (real["ms"] / 1e3)
+        # outputs the bound left open and the kernel recomputed in the
+        # reference's order, in one headline forward
+        eng.cert_stats()
+        step()
+        und, outs = eng.cert_stats()
         roofline = {"bound": "hbm",
                     "kernel": "enc1.conv1 certified first conv + real fold (fp16 matrix-core integer-digit sums, "
                               "rigorous error bound, reference-order recompute of undecided outputs)",
@@ -596,7 +697,8 @@ def main() -> int:
                                    "out)",
                     "fp32_equivalent": {"tflops": round(achieved / 1e12, 3),
                                         "of_fp32_matrix_peak": round(achieved / PEAK_FP32_FLOPS, 4),
-                                        "note": f"{real_flops:.4g} FLOP of the FP32 conv per launch / the same time"}}
+                                        "note": f"{real_flops:.4g} FLOP of the FP32 conv per launch / the same time"},
+                    "recomputed_outputs": und, "outputs": outs}
     else:
         roofline = {"bound": "mfma", "kernel": "enc1.conv1 real-input conv + real fold (order-exact FP32, K=1 MFMA)",
                     "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
@@ -733,7 +835,13 @@ def main() -> int:
                                 "past the scene), benchmark config 3",
                       "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),
                       "host_ms": round(scene_host_ms, 3),
-                      "host_note": "host cube in, host map out: strips through pinned buffers over PCIe"},
+                      "host_note": "host cube in, host map out: strips through pinned buffers over PCIe",
+                      "kernels": scene_kern},
+            "cert_adversarial": {"config": f"the headline batch ({N} patches 32x32x120): the certified first conv "
+                                           "on N(0,1) patches, on patches with NaNs, and on +-1 bands with each "
+                                           "channel's fold placed on an integer tap sum (about 1% of outputs on "
+                                           "the fold's switch point)",
+                                 **adversarial},
             "v2_stem": {"config": "v2 spectral-stem model, 16-channel 1x1 stem, base 16, 32x32x120, batch 1024",
                         "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),
                         "stem_kernel_us": round(stem_ms * 1e3, 2), "stem_bytes": stem_bytes,
