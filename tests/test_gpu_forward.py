@@ -149,6 +149,32 @@ def test_batch_1024(tmp_path, orc):
     eng.close()
 
 
+def test_batch_1024_every_patch(tmp_path, orc):
+    """The headline batch (1024 patches of 32x32x120, the bench blob and
+    input): every patch's enc1.act1 bits (the certified first conv) and its
+    logits bit for bit against the checker, from the debug forward and from
+    the plain forward (the headline path: two parts on two streams)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    b = synth.make_blob(seed=0)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(1, 1024)
+    logits, st = eng.forward_debug(x)
+    plain = eng.forward_batch(x)
+    assert _same(plain, logits)
+    act1 = st["enc1.act1"]
+    model = orc.parse(B.to_bytes(b))
+
+    def patch_ok(n):
+        want, ref = model.forward(x[n], stages=True)
+        return np.array_equal(act1[n], ref["enc1.act1"]) and _same(logits[n], want)
+
+    with ThreadPoolExecutor(8) as ex:
+        bad = [n for n, ok in enumerate(ex.map(patch_ok, range(1024))) if not ok]
+    assert not bad, bad[:8]
+    eng.close()
+
+
 def test_device_api_and_dropin(tmp_path):
     import torch
     b = synth.make_blob(seed=2)
@@ -258,6 +284,29 @@ def test_cfg4_large_tile_vs_checker(tmp_path, orc, monkeypatch):
     assert _same(batch[0], want)
     for n in (1, 2):
         assert _same(batch[n], eng.forward_batch(x[n:n + 1])[0]), n
+    eng.close()
+
+
+def test_cfg4_full_batch(tmp_path, orc, monkeypatch):
+    """Benchmark config 4 at its real batch: 64 patches of 256x256x120, base
+    32 (the certified first conv in tiles of 24 columns with both 16-channel
+    groups, the matrix-core binary convs).  Every patch of the batch equals
+    its own single-patch run, and two patches equal the checker."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    monkeypatch.delenv("BNN_BCONV_MFMA", raising=False)
+    b = synth.make_blob(seed=0, base=32)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(105, 64, 120, 256, 256)
+    batch = eng.forward_batch(x)
+    for n in range(64):
+        assert _same(batch[n], eng.forward_batch(x[n:n + 1])[0]), n
+    model = orc.parse(B.to_bytes(b))
+    idx = (0, 63)
+    with ThreadPoolExecutor(2) as ex:
+        want = list(ex.map(lambda n: model.forward(x[n]), idx))
+    for n, w in zip(idx, want):
+        assert _same(batch[n], w), n
     eng.close()
 
 
