@@ -404,6 +404,7 @@ bool use_mfma(const DevBconv& L, int epi, int H, int W) {
 struct Workspace {
   int N = 0, H = 0, W = 0;
   uint8_t* base = nullptr;
+  size_t cap = 0;  // bytes at base
   uint32_t *a1 = nullptr, *skip[4] = {}, *down[4] = {}, *h[4] = {}, *b1 = nullptr, *b2 = nullptr;
   uint32_t *d1[4] = {}, *d2[4] = {};
 };
@@ -737,11 +738,23 @@ size_t plan_ws(const Model* m, const BnnDevice* D, Workspace& w, int N, int H, i
 
 int ensure_ws(const Model* m, BnnDevice* D, Workspace& w, int N, int H, int W) {
   if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
+  // another shape that fits the allocation is laid out in it anew (work
+  // already enqueued on the same stream finishes first; the tiles of one
+  // whole image run on one stream)
+  const size_t need = plan_ws(m, D, w, N, H, W, nullptr);
+  if (w.base && need <= w.cap) {
+    uint8_t* base = w.base;
+    const size_t cap = w.cap;
+    plan_ws(m, D, w, N, H, W, base);
+    w.cap = cap;
+    return BNN_OK;
+  }
   // a forward may still be in flight on a caller's stream
-  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; }
+  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; w.cap = 0; }
   uint8_t* base = nullptr;
-  HIP_TRY(hipMalloc((void**)&base, plan_ws(m, D, w, N, H, W, nullptr)));
+  HIP_TRY(hipMalloc((void**)&base, need));
   plan_ws(m, D, w, N, H, W, base);
+  w.cap = need;
   return BNN_OK;
 }
 
@@ -1057,8 +1070,101 @@ int check_shape(const Model* m, int N, int H, int W) {
   if (N < 0) return set_err(BNN_EARG, "negative batch");
   if (H < 16 || W < 16)
     return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
-  if (patches_per_launch(m, H, W) < 1)
-    return set_err(BNN_EARG, "one %dx%d patch of %d bands exceeds a launch (2 GiB)", H, W, m->n_bands);
+  return BNN_OK;
+}
+
+int run_device_launch(const Model* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+                      Dumps* dmp);
+int grow(float** p, size_t* cap, size_t bytes);
+
+// ------------------------------------------------------------ whole images in tiles
+// An image whose input passes the per-launch limit (or, for tests, the tile
+// budget BNN_TILE_BYTES) runs as tiles: full-width row strips, or square
+// tiles when a strip of 2 * kTileHalo + 16 rows is already too large.  Core
+// edges sit on multiples of 16 px, so every 2x2 pool pairs the same rows and
+// columns as in the whole image and every inner concat is exact (the
+// reference's up_cat offsets, csrc/bnn_model.c:130-148, only arise at the
+// image's own bottom and right edges, which a tile ending there shares).
+// Each tile runs as an image of its own over its core plus kTileHalo px of
+// the image on every side (clipped at the image border); its logits are the
+// whole image's on the core.  The zero padding a tile sees at an inner edge
+// reaches at most 94 px inward: one row per 3x3 conv at its level, halved
+// (rounded up) by each pool, doubled by each upsample -- 2 px after enc1,
+// 3, 4, 4 rows after enc2-4, 4 at the bottleneck, then 10, 22, 46 and 94
+// after dec4-dec1 (level 3, 2, 1, 0 rows: 8 + 2, 20 + 2, 44 + 2, 92 + 2).
+constexpr int kTileHalo = 128;
+
+size_t tile_budget() {
+  const char* e = getenv("BNN_TILE_BYTES");
+  const size_t def = (size_t)1 << 30;
+  if (!e || !*e) return def;
+  const long long v = atoll(e);
+  return v >= (1 << 20) ? (size_t)v : def;
+}
+
+bool needs_tiles(const Model* m, int H, int W) {
+  const size_t img = (size_t)m->n_bands * H * W * 4;
+  return patches_per_launch(m, H, W) < 1 || img > tile_budget();
+}
+
+// core tile sizes (multiples of 16, or the image's own extent)
+int plan_tiles(const Model* m, int H, int W, int* th, int* tw) {
+  const size_t px = (size_t)m->n_bands * 4, bud = std::min(tile_budget(), (size_t)0x7FFFFFF0ull);
+  const size_t rows = bud / (px * W);
+  if (rows >= (size_t)2 * kTileHalo + 16) {
+    *tw = W;
+    *th = (int)std::min<size_t>((rows - 2 * kTileHalo) / 16 * 16, (size_t)H);
+    return BNN_OK;
+  }
+  size_t side = 16;
+  while ((side + 16) * (side + 16) * px <= bud) side += 16;
+  if (side < (size_t)2 * kTileHalo + 16)
+    return set_err(BNN_EARG, "%d bands: a tile of %d px (16 + 2 x %d halo) exceeds the tile budget", m->n_bands,
+                   16 + 2 * kTileHalo, kTileHalo);
+  *th = *tw = (int)(side - 2 * kTileHalo);
+  return BNN_OK;
+}
+
+// The tiles of N whole images (input [N][bands][H][W] -> logits
+// [N][classes][H][W], host or device pointers) through the staging buffers,
+// in order on stream s.
+int run_tiles(const Model* m, const float* in, bool in_host, int N, int H, int W, float* out, bool out_host,
+              hipStream_t s) {
+  int rc, th, tw;
+  if ((rc = plan_tiles(m, H, W, &th, &tw))) return rc;
+  BnnDevice* D = m->dev;
+  const int nb = m->n_bands, nc = m->n_classes;
+  const int fh = std::min(H, th + 2 * kTileHalo), fw = std::min(W, tw + 2 * kTileHalo);
+  if ((rc = grow(&D->stage_in, &D->stage_in_cap, (size_t)nb * fh * fw * 4))) return rc;
+  if ((rc = grow(&D->stage_out, &D->stage_out_cap, (size_t)nc * fh * fw * 4))) return rc;
+  const hipMemcpyKind kin = in_host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+  const hipMemcpyKind kout = out_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  for (int n = 0; n < N; ++n) {
+    const float* img = in + (size_t)n * nb * H * W;
+    float* lg = out + (size_t)n * nc * H * W;
+    for (int r0 = 0; r0 < H; r0 += th)
+      for (int c0 = 0; c0 < W; c0 += tw) {
+        const int r1 = std::min(H, r0 + th), c1 = std::min(W, c0 + tw);
+        const int a0 = std::max(0, r0 - kTileHalo), a1 = std::min(H, r1 + kTileHalo);
+        const int b0 = std::max(0, c0 - kTileHalo), b1 = std::min(W, c1 + kTileHalo);
+        const int h = a1 - a0, w = b1 - b0;
+        if (h < 16 || w < 16) return set_err(BNN_EARG, "tile %dx%d at (%d, %d): below 16 px", h, w, a0, b0);
+        if (w == W) {
+          HIP_TRY(hipMemcpy2DAsync(D->stage_in, (size_t)h * W * 4, img + (size_t)a0 * W, (size_t)H * W * 4,
+                                   (size_t)h * W * 4, nb, kin, s));
+        } else {
+          for (int c = 0; c < nb; ++c)
+            HIP_TRY(hipMemcpy2DAsync(D->stage_in + (size_t)c * h * w, (size_t)w * 4,
+                                     img + (size_t)c * H * W + (size_t)a0 * W + b0, (size_t)W * 4, (size_t)w * 4, h,
+                                     kin, s));
+        }
+        if ((rc = run_device_launch(m, D->stage_in, 1, h, w, D->stage_out, s, nullptr))) return rc;
+        for (int c = 0; c < nc; ++c)
+          HIP_TRY(hipMemcpy2DAsync(lg + (size_t)c * H * W + (size_t)r0 * W + c0, (size_t)W * 4,
+                                   D->stage_out + (size_t)c * h * w + (size_t)(r0 - a0) * w + (c0 - b0),
+                                   (size_t)w * 4, (size_t)(c1 - c0) * 4, r1 - r0, kout, s));
+      }
+  }
   return BNN_OK;
 }
 
@@ -1072,6 +1178,10 @@ int run_device(const Model* m, const float* d_in, int N, int H, int W, float* d_
                Dumps* dmp) {
   int rc;
   if ((rc = check_shape(m, N, H, W))) return rc;
+  if (needs_tiles(m, H, W)) {
+    if (dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes images of at most 2 GiB");
+    return run_tiles(m, d_in, false, N, H, W, d_logits, false, s);
+  }
   const int per = patches_per_launch(m, H, W);
   if (N > per && dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes at most %d patches of %dx%d", per, H, W);
   for (int n0 = 0; n0 < N; n0 += per) {
@@ -1263,6 +1373,12 @@ int run_host(const Model* m, const float* input, int N, int H, int W, float* log
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
   BnnDevice* D = m->dev;
+  if (needs_tiles(m, H, W)) {
+    if (dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes images of at most 2 GiB");
+    if ((rc = run_tiles(m, input, true, N, H, W, logits, true, D->stream))) return rc;
+    HIP_TRY(hipStreamSynchronize(D->stream));
+    return BNN_OK;
+  }
   const int per = patches_per_launch(m, H, W);
   if (N > per && dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes at most %d patches of %dx%d", per, H, W);
   const int nc = std::min(N, per);
@@ -1353,6 +1469,9 @@ int bnn_forward_device_noalloc(const Model* m, const float* d_input, int N, int 
   if (!D->scratch) return set_err(BNN_EHIP, "allocation-free forward unavailable: %s", D->scratch_err.c_str());
   // sub-batches of at most patches_per_launch, as run_device splits them
   const int per = patches_per_launch(m, H, W);
+  if (per < 1)
+    return set_err(BNN_EARG, "one %dx%d image of %d bands exceeds a launch (2 GiB): it runs in tiles through "
+                   "staging buffers, which the allocation-free forward does not allocate", H, W, m->n_bands);
   Workspace w;
   const size_t need = plan_ws(m, D, w, std::min(N, per), H, W, nullptr);
   if (need > (size_t)BNN_NOALLOC_SCRATCH_BYTES)

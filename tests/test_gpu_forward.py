@@ -382,3 +382,57 @@ def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, fused):
     want = eng.forward_batch(x)
     eng.close()
     assert _same(got, want)
+
+
+def _tile_budget(monkeypatch, nbytes):
+    if nbytes is None:
+        monkeypatch.delenv("BNN_TILE_BYTES", raising=False)
+    else:
+        monkeypatch.setenv("BNN_TILE_BYTES", str(nbytes))
+
+
+@pytest.mark.parametrize("H,W,budget", [(640, 200, 48 << 20), (400, 600, 40 << 20), (333, 277, 50 << 20)])
+def test_whole_image_tiles(tmp_path, orc, monkeypatch, H, W, budget):
+    """A whole image run in tiles (full-width strips, or square tiles when a
+    strip of 272 rows passes the budget; core edges on multiples of 16 px,
+    128 px of halo) gives the logits of the untiled run bit for bit, and the
+    checker's; the budget is lowered here so that small images tile."""
+    b = synth.make_blob(seed=6)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(107, 1, 120, H, W)
+    _tile_budget(monkeypatch, None)
+    whole = eng.forward_batch(x)
+    _tile_budget(monkeypatch, budget)
+    tiled = eng.forward_batch(x)
+    _tile_budget(monkeypatch, None)
+    assert _same(tiled, whole)
+    want = orc.parse(B.to_bytes(b)).forward(x[0])
+    assert _same(tiled[0], want)
+    eng.close()
+
+
+def test_whole_image_past_2gib(tmp_path, orc, monkeypatch):
+    """A single 120-band image of 2304 x 2048 (2.26 GB of input, past the
+    2 GiB a launch addresses) through bnn_forward's host path and through
+    the device path: tiled, and equal to the checker's whole-image forward."""
+    import torch
+
+    _tile_budget(monkeypatch, None)
+    b = synth.make_blob(seed=8)
+    eng, _ = _engine(tmp_path, b)
+    H, W = 2304, 2048
+    x = np.random.default_rng(109).standard_normal((1, 120, H, W), dtype=np.float32)
+    assert x.nbytes > 2**31
+    print("whole image 2304x2048x120: host path", flush=True)
+    got = eng.forward(x[0])
+    print("device path", flush=True)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty((1, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+    eng.forward_device(dx.data_ptr(), 1, H, W, dy.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert _same(dy.cpu().numpy()[0], got)
+    del dx, dy
+    print("checker", flush=True)
+    want = orc.parse(B.to_bytes(b)).forward(x[0])
+    assert _same(got, want)
+    eng.close()
