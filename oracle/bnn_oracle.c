@@ -321,8 +321,7 @@ static void conv_real_general(const float *x, const int8_t *wsign, const float *
     const int Ho = out_size(H, kh, pad, stride), Wo = out_size(W, kw, pad, stride);
     float *xt = malloc((size_t)H * W * cin * sizeof(float) + 4);
     float *wt = malloc((size_t)kh * kw * cin * cout * sizeof(float) + 4);
-    float *acc = malloc((size_t)cout * 2 * sizeof(float) + 8), *s = acc + cout;
-    if (!xt || !wt || !acc) { fprintf(stderr, "oracle: out of memory\n"); exit(1); }
+    if (!xt || !wt) { fprintf(stderr, "oracle: out of memory\n"); exit(1); }
     for (int ci = 0; ci < cin; ++ci)
         for (int p = 0; p < H * W; ++p) xt[(size_t)p * cin + ci] = x[(size_t)ci * H * W + p];
     for (int co = 0; co < cout; ++co)
@@ -330,6 +329,12 @@ static void conv_real_general(const float *x, const int8_t *wsign, const float *
             for (int tap = 0; tap < kh * kw; ++tap)
                 wt[((size_t)tap * cin + ci) * cout + co] =
                     (float)wsign[((size_t)co * cin + ci) * kh * kw + tap];
+    /* output rows in parallel: each output is still one thread's chain */
+    #pragma omp parallel
+    {
+    float *acc = malloc((size_t)cout * 2 * sizeof(float) + 8), *s = acc + cout;
+    if (!acc) { fprintf(stderr, "oracle: out of memory\n"); exit(1); }
+    #pragma omp for schedule(static)
     for (int oy = 0; oy < Ho; ++oy) {
         const int y0 = oy * stride - pad;
         const int ky0 = y0 < 0 ? -y0 : 0, ky1 = y0 + kh > H ? H - y0 : kh;
@@ -353,7 +358,9 @@ static void conv_real_general(const float *x, const int8_t *wsign, const float *
                 out[((size_t)co * Ho + oy) * Wo + ox] = alpha[co] * acc[co];
         }
     }
-    free(xt); free(wt); free(acc);
+    free(acc);
+    }
+    free(xt); free(wt);
 }
 
 /* csrc/bnn_conv_realin.c:140-155: 1x1/pad 0/stride 1 as Cin rank-1 updates
