@@ -243,6 +243,7 @@ struct DevBlock {
 struct RWorkspace {
   int N = 0, H = 0, W = 0;
   uint8_t* base = nullptr;
+  size_t cap = 0;  // bytes at base
   float *h1[9] = {}, *res[9] = {}, *h2[9] = {}, *skip[4] = {}, *down[4] = {};
   uint32_t *a2[9] = {}, *skipb[4] = {}, *downb[4] = {}, *upb[9] = {};
 };
@@ -423,7 +424,6 @@ int level_of(int k) { return k < 4 ? k : k == 4 ? 4 : 8 - k; }
 
 int ensure_ws(const ModelR* m, BnnReactDevice* D, RWorkspace& w, int N, int H, int W) {
   if (w.base && w.N >= N && w.H == H && w.W == W) return BNN_OK;
-  if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; }
   int hs[5], wsz[5];
   level_dims(H, W, hs, wsz);
   std::vector<std::pair<void**, size_t>> plan;  // bytes
@@ -449,7 +449,14 @@ int ensure_ws(const ModelR* m, BnnReactDevice* D, RWorkspace& w, int N, int H, i
   }
   size_t total = 0;
   for (auto& e : plan) total += (e.second + 255) & ~(size_t)255;
-  HIP_TRY(hipMalloc((void**)&w.base, total));
+  // another shape that fits the allocation is laid out in it anew (work
+  // already enqueued on the same stream finishes first; the tiles of one
+  // whole image run on one stream); otherwise a larger one replaces it
+  if (!w.base || total > w.cap) {
+    if (w.base) { HIP_TRY(hipDeviceSynchronize()); (void)hipFree(w.base); w.base = nullptr; w.cap = 0; }
+    HIP_TRY(hipMalloc((void**)&w.base, total));
+    w.cap = total;
+  }
   size_t off = 0;
   for (auto& e : plan) {
     *e.first = w.base + off;
@@ -718,7 +725,8 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
 // A launch addresses its input with 32-bit byte offsets, so one launch
 // takes less than 2 GiB of it: a batch runs in sub-batches of that size
 // (patches_per_launch), a cube of 2 GiB or more in strips of whole patch
-// rows (run_patched_strips).  One image of 2 GiB or more is refused.
+// rows (run_patched_strips), one image of 2 GiB or more in tiles
+// (run_tiles).
 constexpr size_t kLaunchBytes = 0x7FFFFFF0ull;
 int patches_per_launch(const ModelR* m, int H, int W) {
   return (int)std::min<size_t>(1 << 30, (kLaunchBytes - 1) / ((size_t)m->n_bands * H * W * 4));
@@ -728,8 +736,91 @@ int check_shape(const ModelR* m, int N, int H, int W) {
   if (!m || !m->dev) return set_err(BNN_EARG, "model not loaded");
   if (N < 0) return set_err(BNN_EARG, "negative batch");
   if (H < 16 || W < 16) return set_err(BNN_EARG, "H=%d W=%d: the four 2x2 pools need H, W >= 16", H, W);
-  if (patches_per_launch(m, H, W) < 1)
-    return set_err(BNN_EARG, "one %dx%dx%d image exceeds a launch (2 GiB of input)", m->n_bands, H, W);
+  return BNN_OK;
+}
+
+int run_device_launch(const ModelR* m, const float* d_in, int N, int H, int W, float* d_logits, hipStream_t s,
+                      Dumps* dmp, const Scene* sc);
+int grow(float** p, size_t* cap, size_t bytes);
+
+// An image whose input passes the per-launch limit (or, for tests, the tile
+// budget BNN_TILE_BYTES) runs in tiles exactly as the v1 forward's whole
+// images do (bnn_host.cpp, kTileHalo): full-width row strips, or square
+// tiles, with core edges on multiples of 16 px and 128 px of the image
+// around each core.  The v3 chain has the same contamination depth from a
+// tile's inner edge: two 3x3 binary convs per block at each level (its 1x1
+// projections and epilogues stay on their pixel), 2x2 pools and nearest
+// upsamples between levels, so 94 px.
+constexpr int kTileHalo = 128;
+
+size_t tile_budget() {
+  const char* e = getenv("BNN_TILE_BYTES");
+  const size_t def = (size_t)1 << 30;
+  if (!e || !*e) return def;
+  const long long v = atoll(e);
+  return v >= (1 << 20) ? (size_t)v : def;
+}
+
+bool needs_tiles(const ModelR* m, int H, int W) {
+  return patches_per_launch(m, H, W) < 1 || (size_t)m->n_bands * H * W * 4 > tile_budget();
+}
+
+int plan_tiles(const ModelR* m, int H, int W, int* th, int* tw) {
+  const size_t px = (size_t)m->n_bands * 4, bud = std::min(tile_budget(), kLaunchBytes - 1);
+  const size_t rows = bud / (px * W);
+  if (rows >= (size_t)2 * kTileHalo + 16) {
+    *tw = W;
+    *th = (int)std::min<size_t>((rows - 2 * kTileHalo) / 16 * 16, (size_t)H);
+    return BNN_OK;
+  }
+  size_t side = 16;
+  while ((side + 16) * (side + 16) * px <= bud) side += 16;
+  if (side < (size_t)2 * kTileHalo + 16)
+    return set_err(BNN_EARG, "%d bands: a tile of %d px (16 + 2 x %d halo) exceeds the tile budget", m->n_bands,
+                   16 + 2 * kTileHalo, kTileHalo);
+  *th = *tw = (int)(side - 2 * kTileHalo);
+  return BNN_OK;
+}
+
+// The tiles of N whole images (host or device pointers) through the strip
+// staging buffers (a streamed file's cube sits in stage_in), in order on s.
+int run_tiles(const ModelR* m, const float* in, bool in_host, int N, int H, int W, float* out, bool out_host,
+              hipStream_t s) {
+  int rc, th, tw;
+  if ((rc = plan_tiles(m, H, W, &th, &tw))) return rc;
+  BnnReactDevice* D = m->dev;
+  const int nb = m->n_bands, nc = m->n_classes;
+  const int fh = std::min(H, th + 2 * kTileHalo), fw = std::min(W, tw + 2 * kTileHalo);
+  if ((rc = grow(&D->strip_in, &D->strip_in_cap, (size_t)nb * fh * fw * 4))) return rc;
+  if ((rc = grow(&D->strip_out, &D->strip_out_cap, (size_t)nc * fh * fw * 4))) return rc;
+  const hipMemcpyKind kin = in_host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+  const hipMemcpyKind kout = out_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  for (int n = 0; n < N; ++n) {
+    const float* img = in + (size_t)n * nb * H * W;
+    float* lg = out + (size_t)n * nc * H * W;
+    for (int r0 = 0; r0 < H; r0 += th)
+      for (int c0 = 0; c0 < W; c0 += tw) {
+        const int r1 = std::min(H, r0 + th), c1 = std::min(W, c0 + tw);
+        const int a0 = std::max(0, r0 - kTileHalo), a1 = std::min(H, r1 + kTileHalo);
+        const int b0 = std::max(0, c0 - kTileHalo), b1 = std::min(W, c1 + kTileHalo);
+        const int h = a1 - a0, w = b1 - b0;
+        if (h < 16 || w < 16) return set_err(BNN_EARG, "tile %dx%d at (%d, %d): below 16 px", h, w, a0, b0);
+        if (w == W) {
+          HIP_TRY(hipMemcpy2DAsync(D->strip_in, (size_t)h * W * 4, img + (size_t)a0 * W, (size_t)H * W * 4,
+                                   (size_t)h * W * 4, nb, kin, s));
+        } else {
+          for (int c = 0; c < nb; ++c)
+            HIP_TRY(hipMemcpy2DAsync(D->strip_in + (size_t)c * h * w, (size_t)w * 4,
+                                     img + (size_t)c * H * W + (size_t)a0 * W + b0, (size_t)W * 4, (size_t)w * 4, h,
+                                     kin, s));
+        }
+        if ((rc = run_device_launch(m, D->strip_in, 1, h, w, D->strip_out, s, nullptr, nullptr))) return rc;
+        for (int c = 0; c < nc; ++c)
+          HIP_TRY(hipMemcpy2DAsync(lg + (size_t)c * H * W + (size_t)r0 * W + c0, (size_t)W * 4,
+                                   D->strip_out + (size_t)c * h * w + (size_t)(r0 - a0) * w + (c0 - b0),
+                                   (size_t)w * 4, (size_t)(c1 - c0) * 4, r1 - r0, kout, s));
+      }
+  }
   return BNN_OK;
 }
 
@@ -762,6 +853,10 @@ int run_device(const ModelR* m, const float* d_in, int N, int H, int W, float* d
   int rc;
   if ((rc = check_shape(m, N, H, W))) return rc;
   if (N == 0) return BNN_OK;
+  if (!sc && needs_tiles(m, H, W)) {
+    if (dmp && dmp->on) return set_err(BNN_EARG, "a debug forward takes images of at most 2 GiB");
+    return run_tiles(m, d_in, false, N, H, W, d_logits, false, s);
+  }
   const int per = patches_per_launch(m, H, W);
   if ((dmp && dmp->on) || sc || N <= per) return run_device_launch(m, d_in, N, H, W, d_logits, s, dmp, sc);
   for (int n0 = 0; n0 < N; n0 += per) {
@@ -789,6 +884,12 @@ int run_host(const ModelR* m, const float* input, int N, int H, int W, float* lo
   if (N == 0) return BNN_OK;
   BnnReactDevice* D = m->dev;
   const bool dump = dmp && dmp->on;
+  if (needs_tiles(m, H, W)) {
+    if (dump) return set_err(BNN_EARG, "a debug forward takes images of at most 2 GiB");
+    if ((rc = run_tiles(m, input, true, N, H, W, logits, true, D->stream))) return rc;
+    HIP_TRY(hipStreamSynchronize(D->stream));
+    return BNN_OK;
+  }
   const int per = dump ? N : std::min(N, patches_per_launch(m, H, W));
   const size_t pin = (size_t)m->n_bands * H * W, pout = (size_t)m->n_classes * H * W;
   if ((rc = grow(&D->stage_in, &D->stage_in_cap, per * pin * 4))) return rc;

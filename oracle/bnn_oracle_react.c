@@ -193,6 +193,8 @@ int orr_parse(const uint8_t *buf, size_t len, orr_model **out, char *err, int er
  * acc = fma(W, x, acc) from +0 (csrc/bnn_realin_blk.h:59-70; the scalar
  * pixel tail of :76-81 and react_proj_1x1 run the same chain) */
 void orr_proj(const float *x, const float *Wm, float *out, int cin, int HW, int cout) {
+    /* outputs in parallel; each is one thread's chain */
+    #pragma omp parallel for collapse(2) schedule(static)
     for (int co = 0; co < cout; ++co)
         for (long p = 0; p < HW; ++p) {
             float acc = 0.0f;
@@ -208,6 +210,8 @@ void orr_proj(const float *x, const float *Wm, float *out, int cin, int HW, int 
  * image is skipped; finally alpha * acc. */
 void orr_conv3(const float *x, const int8_t *wsign, const float *alpha, float *out,
                int cin, int H, int W, int cout) {
+    /* outputs in parallel; each is one thread's chain */
+    #pragma omp parallel for collapse(2) schedule(static)
     for (int co = 0; co < cout; ++co)
         for (int oy = 0; oy < H; ++oy)
             for (int ox = 0; ox < W; ++ox) {

@@ -391,7 +391,7 @@ def _tile_budget(monkeypatch, nbytes):
         monkeypatch.setenv("BNN_TILE_BYTES", str(nbytes))
 
 
-@pytest.mark.parametrize("H,W,budget", [(640, 200, 48 << 20), (400, 600, 40 << 20), (333, 277, 50 << 20)])
+@pytest.mark.parametrize("H,W,budget", [(640, 200, 48 << 20), (400, 600, 70 << 20), (333, 277, 50 << 20)])
 def test_whole_image_tiles(tmp_path, orc, monkeypatch, H, W, budget):
     """A whole image run in tiles (full-width strips, or square tiles when a
     strip of 272 rows passes the budget; core edges on multiples of 16 px,

@@ -425,3 +425,56 @@ def test_react_default_stream_is_ordered(tmp_path):
         eng.forward_patched_device(d_cube.data_ptr(), 272, 270, d_map.data_ptr(), 16, None)
         assert _same(d_map.cpu().numpy(), want_map)
     eng.close()
+
+
+@pytest.mark.parametrize("H,W,budget", [(640, 200, 48 << 20), (333, 277, 50 << 20), (400, 600, 70 << 20)])
+def test_react_whole_image_tiles(tmp_path, rorc, monkeypatch, H, W, budget):
+    """A v3 whole image in tiles (row strips, or square tiles; core edges on
+    16 px, 128 px of halo), forced here by a small tile budget: the logits of
+    the untiled run bit for bit, and the checker's."""
+    b = synth.make_blob_react(seed=43, base=8)
+    eng, _ = _engine(tmp_path, b)
+    x = synth.make_input(44, 1, 120, H, W)
+    monkeypatch.delenv("BNN_TILE_BYTES", raising=False)
+    whole = eng.forward_batch(x)
+    monkeypatch.setenv("BNN_TILE_BYTES", str(budget))
+    tiled = eng.forward_batch(x)
+    monkeypatch.delenv("BNN_TILE_BYTES", raising=False)
+    assert _same(tiled, whole)
+    assert _same(tiled[0], rorc.parse(R.to_bytes(b)).forward(x[0]))
+    eng.close()
+
+
+def test_react_whole_image_past_2gib(tmp_path, rorc, monkeypatch):
+    """A single 120-band v3 image of 2304 x 2048 (2.26 GB, past the 2 GiB a
+    launch addresses): bnn_forward_react (host), the device entry point and
+    the reference's file reader path (bnn_infer_react on an input file,
+    bnn_forward_react_file) all run it in tiles and equal the checker."""
+    import torch
+
+    monkeypatch.delenv("BNN_TILE_BYTES", raising=False)
+    b = synth.make_blob_react(seed=45, base=8)
+    eng, path = _engine(tmp_path, b)
+    H, W = 2304, 2048
+    x = np.random.default_rng(46).standard_normal((120, H, W), dtype=np.float32)
+    assert x.nbytes > 2**31
+    print("v3 whole image: host path", flush=True)
+    got = eng.forward(x)
+    print("device path", flush=True)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty((1, b.n_classes, H, W), dtype=torch.float32, device="cuda")
+    eng.forward_device(dx.data_ptr(), 1, H, W, dy.data_ptr())
+    torch.cuda.synchronize()
+    assert _same(dy.cpu().numpy()[0], got)
+    del dx, dy
+    print("file path (CLI)", flush=True)
+    xin, out = tmp_path / "big.in", tmp_path / "big.out"
+    x.tofile(xin)
+    r = subprocess.run([E.CLI_REACT_PATH, path, str(xin), str(out), str(H), str(W), "1"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert _same(np.fromfile(out, np.float32).reshape(-1, H, W), got)
+    os.unlink(xin)
+    print("checker", flush=True)
+    assert _same(got, rorc.parse(R.to_bytes(b)).forward(x))
+    eng.close()
