@@ -175,7 +175,7 @@ __device__ __forceinline__ int part_idx(int s, int g, int c) { return ((s * 4 + 
 // occur for j < 7 (cpw < 28); otherwise only element 7 can be one.
 template <bool GUARD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
+void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int p = lane & 15, gq = lane >> 4;
@@ -184,7 +184,19 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   // wider rows: tiles of 24 output columns, each block's 32-column window
   // starting 4 columns before its tile (columns outside the image read 0)
   const int ntile = W <= 32 ? 1 : (W + 23) / 24;
-  const int n = blockIdx.x / ntile, tile = blockIdx.x - n * ntile, grp = blockIdx.y;
+  // XCD-aware order: blocks go to the XCDs in turn (block b to XCD b % 8),
+  // and XCD x takes the x-th eighth of the work items (patch, tile, group)
+  // in order, so a tile's channel groups, which read the same input window
+  // and write the two halves of the same output words, run on one XCD side
+  // by side, next to the neighbouring tiles whose windows overlap theirs:
+  // their reads and writes meet in that XCD's L2
+  // (one block per patch keeps the plain order)
+  const int ng = (a.cout + 15) >> 4;
+  const bool xorder = ng > 1 || ntile > 1;
+  const uint32_t item = xorder ? (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  if (item >= nitems) return;
+  const int grp = (int)(item % (uint32_t)ng), tt = (int)(item / (uint32_t)ng);
+  const int n = tt / ntile, tile = tt - n * ntile;
   const int wx0 = W <= 32 ? 0 : 24 * tile - 4;  // image column of window column 0
   const int vlo = W <= 32 ? 0 : 4, vhi = W <= 32 ? W : min(28, W - wx0);  // output window columns
   const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
@@ -276,7 +288,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld) {
   // for rounding v -+ E to nearest (with the |v| 2^-22 term below)
   const float cA = 0x1p-24f * (1.0f + 0x1p-9f + 0x1p-19f);
   const int cwo = (a.cout + 31) >> 5;
-  const bool whole_word = (grp & 1) == 0 && grp == (int)gridDim.y - 1;
+  const bool whole_word = (grp & 1) == 0 && grp == ng - 1;
   // the partials of pixels fpx0 (even segment) and fpx0 + 1 (odd, 256 floats
   // on) in a wave's partial: segment row group wv, register fq
   const int i0 = part_idx(0, wv, fc) + fq;
@@ -570,10 +582,13 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
     attr[guard].fetch_or(bit, std::memory_order_acq_rel);
   }
   const long ntile = a.W <= 32 ? 1 : (a.W + 23) / 24;
-  if ((long)a.N * ntile >= 0x7FFFFFFF) return hipErrorInvalidValue;
-  dim3 grid((unsigned)((long)a.N * ntile), (unsigned)((a.cout + 15) / 16));
-  if (guard) hipLaunchKernelGGL((k_real_cert<true>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
-  else hipLaunchKernelGGL((k_real_cert<false>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld);
+  const long nitems = (long)a.N * ntile * ((a.cout + 15) / 16);
+  if (nitems >= 0x7FFFFFF0) return hipErrorInvalidValue;
+  // a multiple of 8 blocks (one per XCD in turn); the padding ones exit
+  const bool xorder = ntile > 1 || a.cout > 16;
+  const dim3 grid((unsigned)(xorder ? (nitems + 7) / 8 * 8 : nitems));
+  if (guard) hipLaunchKernelGGL((k_real_cert<true>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
+  else hipLaunchKernelGGL((k_real_cert<false>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
   return hipGetLastError();
 }
 
