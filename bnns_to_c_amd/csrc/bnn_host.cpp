@@ -388,6 +388,15 @@ bool mid_mode() {
   return !(e && !strcmp(e, "0"));
 }
 
+// With the fused middle, the level-1 layers around it (enc2.c1, enc2.c2,
+// dec2.c1, dec2.c2) run inside the same kernel when level 1 is 16 x 16 and
+// they have at most 32 output channels (mid_ext_fits); BNN_MIDX=0 keeps
+// them as per-layer kernels.
+bool midx_mode() {
+  const char* e = getenv("BNN_MIDX");
+  return !(e && !strcmp(e, "0"));
+}
+
 // The certified first conv (launch_real_cert) makes the v1 enc1.conv1 bits
 // whenever its shape fits (real_cert_fits); BNN_CERT=0 keeps the exact-order
 // matrix-core kernel for them.  The debug forward's float conv output always
@@ -431,6 +440,7 @@ struct BnnDevice {
   unsigned long long cert_outputs = 0;
   DevBconv e1[4], e2[4], b1, b2, d1[4], d2[4];
   bool mid = false;  // the fused middle applies (mid_fits at load, and mid_mode())
+  bool midx = false; // and takes the level-1 layers too (mid_ext_fits, midx_mode())
   float *hw = nullptr, *hb = nullptr;
   int ncls = 0;
   Workspace ws;
@@ -542,6 +552,20 @@ bool mid_fits(BnnDevice* D) {
     if (L[l]->cout > cap[l]) return false;
   return D->d1[0].cw0 == words(D->e2[3].cout) && D->d1[0].cw1 == words(D->b2.cout) &&
          D->d1[1].cw0 == words(D->e2[2].cout) && D->d1[1].cw1 == words(D->d2[0].cout);
+}
+
+// Whether the fused middle can also take the level-1 layers: one group of
+// 32 output channels each, paired taps only over a one-word first segment,
+// and dec2.c1's concat split as the enc2 skip, then dec3.c2's words.
+bool mid_ext_fits(BnnDevice* D) {
+  const DevBconv* X[kMidXLayers] = {&D->e1[1], &D->e2[1], &D->d1[2], &D->d2[2]};
+  for (int l = 0; l < kMidXLayers; ++l) {
+    if (X[l]->cout > 32 || (X[l]->pair && X[l]->cw0 != 1)) return false;
+    if ((X[l]->cw1 != 0) != (l == 2)) return false;
+  }
+  return D->e1[1].cw0 == words(D->e2[0].cout) && D->e2[1].cw0 == words(D->e1[1].cout) &&
+         D->d1[2].cw0 == words(D->e2[1].cout) && D->d1[2].cw1 == words(D->d2[1].cout) &&
+         D->d2[2].cw0 == words(D->d1[2].cout);
 }
 
 // real conv weights.  v2 stem: lane masks of the 1x1 matrix-core kernel
@@ -687,6 +711,7 @@ int build_device(Model* m, const StemPart* st = nullptr) {
     if ((rc = upload_bconv(D, &D->d2[i], m->dec_conv2[i], 0, &m->dec_act2[i], nullptr))) return rc;
   }
   D->mid = mid_mode() && mid_fits(D);
+  D->midx = D->mid && midx_mode() && mid_ext_fits(D);
   D->cert = cert_mode() && D->rcwb && D->rcws && D->rct1;
   if (D->mid) {
     const auto L = mid_layers(D);
@@ -915,8 +940,38 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   // pooled bits, output dec3.c2's bits; the debug forward takes every
   // intermediate tensor and P as the per-layer kernels would
   const bool use_mid = D->mid && hs[2] == 8 && wsz[2] == 8;
+  // and enc2.c1 .. dec2.c2 around it (level 1 is 16 x 16): input enc1's
+  // pooled bits, output dec2.c2's bits.  Its blocks run fourteen layers
+  // each; in a split batch only the last part takes it: the earlier parts'
+  // binary layers run beside the next part's first conv, which leaves each
+  // CU room for one such block at a time, and the per-layer kernels fill
+  // that room better (measured at batch 1024: fused in both parts 0.287 ms,
+  // in neither 0.278, in the last 0.268)
+  const bool ext_ok = use_mid && D->midx && hs[1] == 16 && wsz[1] == 16;
+  bool use_ext = ext_ok;
   auto mid = [&]() -> int {
     const auto L = mid_layers(D);
+    MidArgs a{};
+    double work = 0;
+    const DevBconv* XL[kMidXLayers] = {&D->e1[1], &D->e2[1], &D->d1[2], &D->d2[2]};
+    auto xlayer = [&](int l) {
+      MidXLayer& xl = a.X[l];
+      const DevBconv& B = *XL[l];
+      xl.w = B.wt;
+      xl.lo = B.f1.lo; xl.wid = B.f1.wid;
+      xl.lo2 = B.f2.lo; xl.wid2 = B.f2.wid;
+      xl.cin = B.cin; xl.cout = B.cout; xl.cw0 = B.cw0; xl.cw1 = B.cw1; xl.pair = B.pair;
+      if (dump) {
+        xl.P = dmp->P[pi++];
+        if (l == 1) xl.P2 = dmp->P2[1];
+      }
+      work += (double)N * B.cout * 16 * 16 * B.cin * 9;
+    };
+    if (use_ext) {
+      a.ext = 1;
+      xlayer(0);
+      xlayer(1);
+    }
     uint32_t* T[kMidTensors] = {w.down[1], w.h[2], w.skip[2], w.down[2], w.h[3], w.skip[3], w.down[3],
                                 w.b1,      w.b2,   w.d1[0],   w.d2[0],   w.d1[1], w.d2[1]};
     static const int lvl[kMidTensors] = {2, 2, 2, 3, 3, 3, 4, 4, 4, 3, 3, 2, 2};
@@ -924,8 +979,6 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
                                  words(L[2]->cout),    words(L[3]->cout), words(L[3]->cout), words(L[4]->cout),
                                  words(L[5]->cout),    words(L[6]->cout), words(L[7]->cout), words(L[8]->cout),
                                  words(L[9]->cout)};
-    MidArgs a{};
-    double work = 0;
     for (int l = 0; l < kMidLayers; ++l) {
       MidLayer& ml = a.L[l];
       ml.w = L[l]->mw;
@@ -947,10 +1000,24 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     }
     static const int d[kMidLayers] = {8, 8, 4, 4, 2, 2, 4, 4, 8, 8};
     for (int l = 0; l < kMidLayers; ++l) work += (double)N * L[l]->cout * d[l] * d[l] * L[l]->cin * 9;
+    if (use_ext) {
+      xlayer(2);
+      xlayer(3);
+      // 0 enc1 pooled (in), 1 enc2.c1, 2 enc2 skip, 3 dec2.c1, 4 dec2.c2 (out)
+      const uint32_t* XT[kMidXTensors] = {w.down[0], w.h[1], w.skip[1], w.d1[2], w.d2[2]};
+      const int xcw[kMidXTensors] = {words(D->e2[0].cout), words(D->e1[1].cout), words(D->e2[1].cout),
+                                     words(D->d1[2].cout), words(D->d2[2].cout)};
+      for (int i = 0; i < kMidXTensors; ++i) {
+        a.xt[i] = const_cast<uint32_t*>(at(XT[i], 1, xcw[i]));
+        a.xcw[i] = xcw[i];
+        a.xoff[i] = off;
+        off += 256 * xcw[i];
+      }
+    }
     a.N = cnt;
     a.ldsw = off;
     HIP_TRY(launch_mid(a, dump, st));
-    return mark("enc3-dec3", "bconv_mid", work, 1.0);
+    return mark(use_ext ? "enc2-dec2" : "enc3-dec3", "bconv_mid", work, 1.0);
   };
 
   static const char* enc_c1[4] = {"enc1.c1", "enc2.c1", "enc3.c1", "enc4.c1"};
@@ -960,7 +1027,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   auto part = [&]() -> int {
   if ((rc = first_conv())) return rc;
   const uint32_t* x = w.a1;
-  for (int i = 0; i < (use_mid ? 2 : 4); ++i) {
+  for (int i = 0; i < (use_ext ? 1 : use_mid ? 2 : 4); ++i) {
     const uint32_t* hin = x;
     if (i || D->stem) {
       if ((rc = bconv(D->e1[i], EPI_FOLD, x, nullptr, i, 0, w.h[i], nullptr, nullptr, enc_c1[i]))) return rc;
@@ -972,9 +1039,9 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   int xl = 4, i0 = 0;
   if (use_mid) {
     if ((rc = mid())) return rc;
-    x = w.d2[1];
-    xl = 2;
-    i0 = 2;
+    x = use_ext ? w.d2[2] : w.d2[1];
+    xl = use_ext ? 1 : 2;
+    i0 = use_ext ? 3 : 2;
   } else {
     if ((rc = bconv(D->b1, EPI_FOLD, x, nullptr, 4, 0, w.b1, nullptr, nullptr, "bott.c1"))) return rc;
     if ((rc = bconv(D->b2, EPI_FOLD, w.b1, nullptr, 4, 0, w.b2, nullptr, nullptr, "bott.c2"))) return rc;
@@ -1048,6 +1115,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     nb = (int)((long)rows * k / parts) * unit;
     cnt = (k + 1 == parts ? N : (int)((long)rows * (k + 1) / parts) * unit) - nb;
     st = k ? D->side[k - 1] : s;
+    use_ext = ext_ok && k + 1 == parts;
     if ((rc = part())) return rc;
   }
   for (int k = 1; k < parts; ++k) {

@@ -523,15 +523,39 @@ struct MidLayer {
   int32_t* P;   // [N][cout][d][d] (debug forward)
   int32_t* P2;  // pooled P (debug forward, pool layers)
 };
+// The level-1 layers around the middle (ext = 1, patches whose level 1 is
+// 16 x 16 and whose level-1 layers have at most 32 output channels):
+// enc2.c1, enc2.c2 (+pool, into tensor 0), dec2.c1 (concat of the enc2 skip
+// and tensor 12), dec2.c2, pixels on lanes.  Weights in k_bconv's table
+// ([word][cout rounded to 32][9], the first segment's taps paired when
+// pair), rules padded to 64 with width 0.
+constexpr int kMidXLayers = 4, kMidXTensors = 5;
+struct MidXLayer {
+  const uint32_t* w;
+  const int32_t* lo;
+  const uint32_t* wid;
+  const int32_t* lo2;
+  const uint32_t* wid2;
+  int cin, cout, cw0, cw1, pair;
+  int32_t* P;   // [N][cout][16][16] (debug forward)
+  int32_t* P2;  // pooled P (debug forward, enc2.c2)
+};
 // Tensors, [N][d][d][cw] words each: 0 enc2 pooled bits (input), 1 enc3.c1,
 // 2 enc3 skip, 3 enc3 down, 4 enc4.c1, 5 enc4 skip, 6 enc4 down, 7 bott.c1,
 // 8 bott.c2, 9 dec4.c1, 10 dec4.c2, 11 dec3.c1, 12 dec3.c2 (output).  off: a
 // tensor's word offset in the block's LDS (one patch), ldsw the total.
+// With ext, tensor 0 is made in the kernel and the level-1 tensors are
+// 0 enc1 pooled bits (input), 1 enc2.c1, 2 enc2 skip, 3 dec2.c1, 4 dec2.c2
+// (output), 16 x 16 each.
 struct MidArgs {
   MidLayer L[kMidLayers];
   uint32_t* t[kMidTensors];
   int off[kMidTensors], dim[kMidTensors], cw[kMidTensors];
   int N, ldsw;
+  int ext;
+  MidXLayer X[kMidXLayers];
+  uint32_t* xt[kMidXTensors];
+  int xoff[kMidXTensors], xcw[kMidXTensors];
 };
 hipError_t launch_mid(const MidArgs& a, bool dump, hipStream_t s);
 

@@ -43,6 +43,7 @@ def _same(a, b):
     (13, 48, False, 2, 32, 32),   # head over 48 channels: dec1.conv2 then the separate head kernel
     (14, 64, True, 1, 30, 34),    # head over 64 channels, odd sizes
     (15, 8, True, 2, 33, 35),     # fused middle at base 8 (enc3 of 32 channels), level 2 of 8 x 8
+    (16, 8, True, 2, 32, 33),     # fused middle with the level-1 layers at base 8 (paired taps)
 ])
 def test_stages_vs_checker(tmp_path, orc, seed, base, cov, N, H, W):
     b = synth.make_blob(seed=seed, base=base, coverage=cov)
@@ -361,27 +362,42 @@ def _ops(eng, x):
     return {lab: op for lab, op, _ms, _w in E.prof_records()}
 
 
-@pytest.mark.parametrize("base,H,W,fused", [(16, 32, 32, True), (8, 35, 32, True), (16, 28, 32, False),
-                                            (32, 32, 32, False)])
-def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, fused):
+@pytest.mark.parametrize("base,H,W,fused,ext", [(16, 32, 32, True, True), (8, 35, 32, True, False),
+                                                (8, 32, 33, True, True), (16, 28, 32, False, False),
+                                                (32, 32, 32, False, False)])
+def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, fused, ext):
     """enc3.c1 .. dec3.c2 run as one kernel when level 2 is 8 x 8 and the
-    widths fit (base <= 16); BNN_MID=0 keeps the per-layer kernels, with
-    the same logits bit for bit."""
+    widths fit (base <= 16), and with enc2.c1, enc2.c2, dec2.c1 and dec2.c2
+    around them when level 1 is 16 x 16; BNN_MIDX=0 keeps the level-1 layers
+    as per-layer kernels and BNN_MID=0 every layer, with the same logits bit
+    for bit."""
     b = synth.make_blob(seed=40 + base, base=base)
     x = synth.make_input(41, 37, 120, H, W)
     monkeypatch.delenv("BNN_MID", raising=False)
+    monkeypatch.delenv("BNN_MIDX", raising=False)
     eng, _ = _engine(tmp_path, b)
     ops = _ops(eng, x)
-    assert ("enc3-dec3" in ops) == fused, ops
+    assert ("enc2-dec2" in ops) == ext, ops
+    assert ("enc3-dec3" in ops) == (fused and not ext), ops
+    assert ("enc2.c1" in ops) == (not ext), ops
     assert ("bott.c1" in ops) == (not fused), ops
     got = eng.forward_batch(x)
     eng.close()
+    monkeypatch.setenv("BNN_MIDX", "0")
+    eng, _ = _engine(tmp_path, b, "x0.blob")
+    ops = _ops(eng, x)
+    assert "enc2-dec2" not in ops and ("enc3-dec3" in ops) == fused, ops
+    want_x = eng.forward_batch(x)
+    eng.close()
+    monkeypatch.delenv("BNN_MIDX", raising=False)
     monkeypatch.setenv("BNN_MID", "0")
     eng, _ = _engine(tmp_path, b, "m0.blob")
-    assert "enc3-dec3" not in _ops(eng, x)
+    ops = _ops(eng, x)
+    assert "enc3-dec3" not in ops and "enc2-dec2" not in ops, ops
     want = eng.forward_batch(x)
     eng.close()
     assert _same(got, want)
+    assert _same(want_x, want)
 
 
 def _tile_budget(monkeypatch, nbytes):
