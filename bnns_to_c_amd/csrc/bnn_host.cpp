@@ -366,6 +366,8 @@ int mfma_conv_mode() {
 // slower)
 constexpr int kSplitMin = 128;
 constexpr int kSplitMax = 2;
+// the fused middle takes the level-1 layers from this many patches a launch
+constexpr int kMidExtMin = 256;
 
 // ------------------------------------------------------------ device model
 struct DevBconv {
@@ -942,13 +944,16 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   const bool use_mid = D->mid && hs[2] == 8 && wsz[2] == 8;
   // and enc2.c1 .. dec2.c2 around it (level 1 is 16 x 16): input enc1's
   // pooled bits, output dec2.c2's bits.  Its blocks run fourteen layers
-  // each; in a split batch only the last part takes it: the earlier parts'
-  // binary layers run beside the next part's first conv, which leaves each
-  // CU room for one such block at a time, and the per-layer kernels fill
-  // that room better (measured at batch 1024: fused in both parts 0.287 ms,
-  // in neither 0.278, in the last 0.268)
+  // each, one after the other, so it pays only with at least one block per
+  // CU (kMidExtMin patches; below that the per-layer kernels, which spread
+  // each layer over many more blocks, finish first: 0.123 against 0.132 ms
+  // at batch 128).  In a split batch only the last part takes it: the
+  // earlier parts' binary layers run beside the next part's first conv,
+  // which leaves each CU room for one such block at a time, and the
+  // per-layer kernels fill that room better (measured at batch 1024: fused
+  // in both parts 0.287 ms, in neither 0.278, in the last 0.268).
   const bool ext_ok = use_mid && D->midx && hs[1] == 16 && wsz[1] == 16;
-  bool use_ext = ext_ok;
+  bool use_ext = ext_ok && N >= kMidExtMin;
   auto mid = [&]() -> int {
     const auto L = mid_layers(D);
     MidArgs a{};
@@ -1115,7 +1120,7 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     nb = (int)((long)rows * k / parts) * unit;
     cnt = (k + 1 == parts ? N : (int)((long)rows * (k + 1) / parts) * unit) - nb;
     st = k ? D->side[k - 1] : s;
-    use_ext = ext_ok && k + 1 == parts;
+    use_ext = ext_ok && k + 1 == parts && cnt >= kMidExtMin;
     if ((rc = part())) return rc;
   }
   for (int k = 1; k < parts; ++k) {

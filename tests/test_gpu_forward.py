@@ -362,38 +362,43 @@ def _ops(eng, x):
     return {lab: op for lab, op, _ms, _w in E.prof_records()}
 
 
-@pytest.mark.parametrize("base,H,W,fused,ext", [(16, 32, 32, True, True), (8, 35, 32, True, False),
-                                                (8, 32, 33, True, True), (16, 28, 32, False, False),
-                                                (32, 32, 32, False, False)])
-def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, fused, ext):
+_MID_LABEL = {"ext": "enc2-dec2", "mid": "enc3-dec3"}
+
+
+@pytest.mark.parametrize("base,H,W,N,mode", [(16, 32, 32, 256, "ext"), (8, 32, 32, 256, "ext"),
+                                             (16, 32, 32, 37, "mid"), (8, 35, 32, 256, "mid"),
+                                             (8, 32, 33, 256, "ext"), (16, 28, 32, 37, "none"),
+                                             (32, 32, 32, 37, "none")])
+def test_fused_middle_rule_and_logits(tmp_path, monkeypatch, base, H, W, N, mode):
     """enc3.c1 .. dec3.c2 run as one kernel when level 2 is 8 x 8 and the
-    widths fit (base <= 16), and with enc2.c1, enc2.c2, dec2.c1 and dec2.c2
-    around them when level 1 is 16 x 16; BNN_MIDX=0 keeps the level-1 layers
-    as per-layer kernels and BNN_MID=0 every layer, with the same logits bit
-    for bit."""
+    widths fit (base <= 16); with enc2.c1, enc2.c2, dec2.c1 and dec2.c2
+    around them when level 1 is 16 x 16 and a part of the batch has at
+    least 256 patches.  BNN_MIDX=0 keeps the level-1 layers as per-layer
+    kernels and BNN_MID=0 every layer, with the same logits bit for bit."""
     b = synth.make_blob(seed=40 + base, base=base)
-    x = synth.make_input(41, 37, 120, H, W)
+    x = synth.make_input(41, N, 120, H, W)
     monkeypatch.delenv("BNN_MID", raising=False)
     monkeypatch.delenv("BNN_MIDX", raising=False)
     eng, _ = _engine(tmp_path, b)
     ops = _ops(eng, x)
-    assert ("enc2-dec2" in ops) == ext, ops
-    assert ("enc3-dec3" in ops) == (fused and not ext), ops
-    assert ("enc2.c1" in ops) == (not ext), ops
-    assert ("bott.c1" in ops) == (not fused), ops
+    for m, lab in _MID_LABEL.items():
+        assert (lab in ops) == (m == mode), ops
+    assert ("enc2.c1" in ops) == (mode != "ext"), ops
+    assert ("bott.c1" in ops) == (mode == "none"), ops
     got = eng.forward_batch(x)
     eng.close()
     monkeypatch.setenv("BNN_MIDX", "0")
     eng, _ = _engine(tmp_path, b, "x0.blob")
     ops = _ops(eng, x)
-    assert "enc2-dec2" not in ops and ("enc3-dec3" in ops) == fused, ops
+    assert "enc2-dec2" not in ops, ops
+    assert ("enc3-dec3" in ops) == (mode != "none"), ops
     want_x = eng.forward_batch(x)
     eng.close()
     monkeypatch.delenv("BNN_MIDX", raising=False)
     monkeypatch.setenv("BNN_MID", "0")
     eng, _ = _engine(tmp_path, b, "m0.blob")
     ops = _ops(eng, x)
-    assert "enc3-dec3" not in ops and "enc2-dec2" not in ops, ops
+    assert not any(lab in ops for lab in _MID_LABEL.values()), ops
     want = eng.forward_batch(x)
     eng.close()
     assert _same(got, want)
