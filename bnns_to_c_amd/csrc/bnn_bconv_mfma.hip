@@ -190,21 +190,33 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 #pragma unroll
     for (int g = 0; g < 4; ++g) acc[m][g] = i32x4v{0, 0, 0, 0};
 
-  // this block's items: blockIdx.x, + gridDim.x, ...; the chunks of all of
-  // them form one pipeline
-  uint32_t it = blockIdx.x;
+  // This block's items, XCD-aware: blocks go to the XCDs in turn (block b
+  // to XCD b % 8, the grid a multiple of 8), XCD x takes the tiles
+  // x, x + 8, x + 16, ... and its blocks walk that list's items (tile, then
+  // channel group fastest) in turn, so a tile's channel groups, which read
+  // the same staged rows and write different words of the same pixels, run
+  // side by side on one XCD and their stores merge in its L2.  Local item
+  // li of XCD x is tile (li / ncot) * 8 + x, group li % ncot; the chunks of
+  // all of a block's items form one pipeline.
+  const uint32_t xcd = blockIdx.x & 7u, nslot = gridDim.x >> 3;
+  auto item_of = [&](uint32_t li) -> uint32_t {
+    const uint32_t tile = (li / (uint32_t)ncot) * 8u + xcd;
+    return tile < T.ntiles ? tile * (uint32_t)ncot + li % (uint32_t)ncot : 0xFFFFFFFFu;
+  };
+  uint32_t li = blockIdx.x >> 3;
+  uint32_t it = item_of(li);
   if (it >= nitems) return;
-  const uint32_t step = gridDim.x;
   stage_load(it, 0);
   stage_store(0);
-  // the chunk after (it, c) is (it, c + 1), or (it + step, 0)
-  uint32_t lit = it;  // item and chunk of the staged-ahead words in sw
+  // the chunk after (it, c) is (it, c + 1), or (the block's next item, 0)
+  uint32_t lli = li, lit = it;  // item and chunk of the staged-ahead words in sw
   int lc = 0;
   bool lok = true;
   auto advance = [&]() {
     if (++lc == T.nch) {
       lc = 0;
-      lit += step;
+      lli += nslot;
+      lit = item_of(lli);
       lok = lit < nitems;
     }
   };
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 #pragma unroll 1
     for (int c = 0; c < T.nch; ++c) {
       const bool last = c + 1 == T.nch;
-      const uint32_t nbase = last ? a_base(it + step) : abase;  // past the last item: unused
+      const uint32_t nbase = last ? a_base(item_of(li + nslot)) : abase;  // past the last item: unused
       const uint32_t bo = (uint32_t)buf * bufb;
 #pragma unroll
       for (int t = 0; t < 9; ++t) {
@@ -322,7 +334,8 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
         }
       }
     }
-    it += step;
+    li += nslot;
+    it = item_of(li);
     if (it >= nitems) break;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
@@ -413,7 +426,9 @@ hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& mc, int epi, bo
   const size_t per_cu = std::min<size_t>(3, (160 * 1024) / lds);
   const size_t items = ntiles * (size_t)(a.cout / 64);
   if (items >= 0xFFFFFFFFull) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)std::min<size_t>(items, per_cu * cus));
+  // (a multiple of 8 blocks for the XCD-aware item order; blocks without
+  // an item exit)
+  const dim3 grid((unsigned)((std::min<size_t>(items, per_cu * cus) + 7) / 8 * 8));
   if (epi == EPI_POOL) {
     if (dump) hipLaunchKernelGGL((k_bconv_mfma<EPI_POOL, true>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
     else hipLaunchKernelGGL((k_bconv_mfma<EPI_POOL, false>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
