@@ -306,7 +306,7 @@ inline void real_fold_switches(float al, float A, float B, float sl, float rs, f
   *dc = d;
 }
 // whether launch_real_cert takes a layer of this shape (rows wider than 32
-// run as tiles of 24 output columns)
+// run as tiles of 32 columns with a one-column halo either side)
 inline bool real_cert_fits(int cin, int W, int rowlen) {
   return cin >= 4 && cin <= 128 && cin % 4 == 0 && W >= 4 && W % 4 == 0 && rowlen % 4 == 0;
 }

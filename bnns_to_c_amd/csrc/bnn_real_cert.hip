@@ -37,8 +37,8 @@
 //    "+ 16" covers these and the tap adds, 2^-8 the (1 + 2^-16) factors and
 //    the roundings of A itself, 2^-110 underflow.
 //
-// Work split: one block of four waves per (patch, 16-channel group); wave w
-// converts a quarter of the input channels.  Rows stream through a ring of
+// Work split: one block of four waves per (patch, 16-channel group, tile
+// of 32 columns); wave w converts a quarter of the input channels.  Rows stream through a ring of
 // four LDS row buffers by 16-byte LDS DMA, one row ahead.  Each step
 // converts one input row into digits (the shifted operands of the kx = 0 and
 // kx = 2 taps come from DPP row shifts, the 16-lane rows being the operand's
@@ -48,6 +48,13 @@
 // its Q to LDS (plain stores; float atomics on LDS are several times slower
 // here), and after a barrier each wave adds the four in wave order for a
 // quarter of the row, folds, certifies and writes the bits.
+//
+// Rows wider than 32 (HALO): each block takes 32 output columns, its window
+// the same 32 columns (128-byte aligned rows of each channel), and the two
+// columns either side of it (halo) arrive beside each row, one float per
+// channel and side; they are converted like the window's values, and the
+// lanes at the window's ends take them, instead of the zero padding, as
+// their kx = 0 / kx = 2 operands and window sums.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -79,7 +86,9 @@ template <int CTRL>
 __device__ __forceinline__ uint32_t dmov(uint32_t src) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)src, CTRL, 0xF, 0xF, true);
 }
-constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121, kRor15 = 0x12F;
+constexpr int kShl1 = 0x101, kShr1 = 0x111, kRor1 = 0x121;
+// halo of one ring slot: [channel 128][side 2] floats
+constexpr uint32_t kHaloSlot = 128 * 2 * 4;
 
 // Pixel layout of the operands: lane p of a 16-lane row holds pixel 2p of
 // the even segment (s = 0) and pixel 2p + 1 of the odd segment (s = 1).
@@ -96,6 +105,16 @@ __device__ __forceinline__ void lane_down(const cert_u32x4& a, cert_u32x4& o) {
 __device__ __forceinline__ void lane_up(const cert_u32x4& a, cert_u32x4& o) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = dmov<kShl1>(a[i]);
+}
+// the same with a halo: the lane whose neighbour lies outside the window
+// (lane 0 moving down, lane 15 moving up, in each 16-lane row) keeps h
+__device__ __forceinline__ void lane_down_h(const cert_u32x4& a, const cert_u32x4& h, cert_u32x4& o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = dpp<kShr1, false>(h[i], a[i]);
+}
+__device__ __forceinline__ void lane_up_h(const cert_u32x4& a, const cert_u32x4& h, cert_u32x4& o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = dpp<kShl1, false>(h[i], a[i]);
 }
 
 __device__ __forceinline__ float f32_of(uint32_t b) { return __builtin_bit_cast(float, b); }
@@ -156,9 +175,11 @@ __device__ __forceinline__ uint32_t wave_max_bits(float m) {
              max((uint32_t)__builtin_amdgcn_readlane((int)mb, 32), (uint32_t)__builtin_amdgcn_readlane((int)mb, 48)));
 }
 // per-pixel value (pixel 2p + s in v[s]) plus its left and right neighbours
-__device__ __forceinline__ void window3(const float (&v)[2], float (&o)[2]) {
-  const float l = f32_of(dmov<kShr1>(bits_of(v[1])));  // pixel 2p - 1
-  const float r = f32_of(dmov<kShl1>(bits_of(v[0])));  // pixel 2p + 2
+// (HALO: lane 0's left and lane 15's right neighbour is h, the halo's)
+template <bool HALO>
+__device__ __forceinline__ void window3(const float (&v)[2], float h, float (&o)[2]) {
+  const float l = f32_of(HALO ? dpp<kShr1, false>(bits_of(h), bits_of(v[1])) : dmov<kShr1>(bits_of(v[1])));  // pixel 2p - 1
+  const float r = f32_of(HALO ? dpp<kShl1, false>(bits_of(h), bits_of(v[0])) : dmov<kShl1>(bits_of(v[0])));  // pixel 2p + 2
   const float c = __fadd_rn(v[0], v[1]);
   o[0] = __fadd_rn(c, l);
   o[1] = __fadd_rn(c, r);
@@ -173,7 +194,7 @@ __device__ __forceinline__ int part_idx(int s, int g, int c) { return ((s * 4 + 
 // element j of lane (p, gq) is channel cpw * w + 4 j + gq, column 16 s + p;
 // elements past the wave's channels read as 0.  GUARD: such elements may
 // occur for j < 7 (cpw < 28); otherwise only element 7 can be one.
-template <bool GUARD>
+template <bool GUARD, bool HALO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -181,15 +202,16 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   const int p = lane & 15, gq = lane >> 4;
   const int H = a.H, W = a.W, cin = a.cin, cpw = cin >> 2;
   // rows up to 32 wide: one block per patch, window column = image column;
-  // wider rows: tiles of 24 output columns, each block's 32-column window
-  // starting 4 columns before its tile (columns outside the image read 0)
-  const int ntile = W <= 32 ? 1 : (W + 23) / 24;
+  // wider rows (HALO): tiles of 32 columns, the window the tile itself
+  // (columns outside the image read 0)
+  const int ntile = HALO ? (W + 31) / 32 : 1;
   // XCD-aware order: blocks go to the XCDs in turn (block b to XCD b % 8),
   // and XCD x takes the x-th eighth of the work items (patch, tile, group)
   // in order, so a tile's channel groups, which read the same input window
   // and write the two halves of the same output words, run on one XCD side
-  // by side, next to the neighbouring tiles whose windows overlap theirs:
-  // their reads and writes meet in that XCD's L2
+  // by side, next to the neighbouring tiles whose rows share cache lines
+  // with theirs (the halo columns): their reads and writes meet in that
+  // XCD's L2
   // (one block per patch keeps the plain order)
   const int ng = (a.cout + 15) >> 4;
   const bool xorder = ng > 1 || ntile > 1;
@@ -197,13 +219,16 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   if (item >= nitems) return;
   const int grp = (int)(item % (uint32_t)ng), tt = (int)(item / (uint32_t)ng);
   const int n = tt / ntile, tile = tt - n * ntile;
-  const int wx0 = W <= 32 ? 0 : 24 * tile - 4;  // image column of window column 0
-  const int vlo = W <= 32 ? 0 : 4, vhi = W <= 32 ? W : min(28, W - wx0);  // output window columns
+  const int wx0 = HALO ? 32 * tile : 0;  // image column of window column 0
+  const int vhi = HALO ? min(32, W - wx0) : W;  // output window columns 0 .. vhi - 1
   const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
   float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [wave][512]
   float* absw = opart + 4 * 512;                         // [wave][32]
   float* qw = absw + 4 * 32;                             // [wave]
   uint32_t* wsl = reinterpret_cast<uint32_t*>(qw + 4);   // [channel][tap][4] sign masks
+  // HALO: [ring slot][channel 128][side 2], at byte hal_off
+  const uint32_t hal_off = (uint32_t)kCertRing * rb + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4u;
+  const float* hal = cert_lds + hal_off / 4;
   typedef __attribute__((address_space(3))) float* lds_f32;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_f32)cert_lds;
 
@@ -237,6 +262,13 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     const bool ok = k < nld && ci < cin && cg >= 0 && cg < ig.xlim;
     doff[m] = ok ? (uint32_t)(ig.base + (size_t)ci * ig.cstride + cg) * 4u : kCertFar;
   }
+  // HALO: wave w's one load per row brings channels 32 w .. 32 w + 31, lane
+  // L channel 32 w + L / 2 at window column -1 (L even) or 32 (L odd)
+  uint32_t hoff = kCertFar;
+  if (HALO) {
+    const int ci = 32 * wv + (lane >> 1), col = (lane & 1) ? wx0 + 32 : wx0 - 1;
+    if (ci < cin && col >= 0 && col < ig.xlim) hoff = (uint32_t)(ig.base + (size_t)ci * ig.cstride + col) * 4u;
+  }
   const uint64_t xaddr = (uint64_t)(uintptr_t)a.x;
   auto uni = [](uint32_t v) __attribute__((always_inline)) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
   typedef uint32_t dma_u32x4 __attribute__((ext_vector_type(4)));
@@ -255,6 +287,15 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                    :
                    : "s"(m0v), "v"(vo), "s"(rd)
+                   : "memory");
+    }
+    if (HALO && 32 * wv < cin) {
+      const uint32_t m0h = uni(lds0 + hal_off + (uint32_t)(y % kCertRing) * kHaloSlot + (uint32_t)wv * 256u);
+      const uint32_t vo = (inrow && hoff != kCertFar) ? hoff + ro : kCertFar;
+      const dma_u32x4 rd = xsrc;
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                   :
+                   : "s"(m0h), "v"(vo), "s"(rd)
                    : "memory");
     }
   };
@@ -327,14 +368,30 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         xv[0][j] = ok ? v.x : 0.0f;
         xv[1][j] = ok ? v.y : 0.0f;
       }
+      // HALO: lane 0's left and lane 15's right halo value of element j's
+      // channel (0 in the other lanes)
+      float hx[8];
+      if constexpr (HALO) {
+        const float* hrow = hal + (size_t)(yi % kCertRing) * (kHaloSlot / 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float2 v = *reinterpret_cast<const float2*>(&hrow[2 * (cpw * wv + 4 * j + gq)]);
+          const bool ok = ((GUARD || j == 7) ? ((jvalid >> j) & 1u) != 0 : true) && (p == 0 || p == 15);
+          hx[j] = ok ? (p == 0 ? v.x : v.y) : 0.0f;
+        }
+      }
       // the wave's largest |x| (max ignores a NaN, which reaches v' and A as
       // NaN)
-      float m = 0.0f, as[2] = {0.0f, 0.0f};
+      float m = 0.0f, as[2] = {0.0f, 0.0f}, ash = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         m = fmaxf(fmaxf(m, fabsf(xv[0][j])), fabsf(xv[1][j]));
         as[0] = __fmaf_rn(fabsf(xv[0][j]), wsum[j], as[0]);
         as[1] = __fmaf_rn(fabsf(xv[1][j]), wsum[j], as[1]);
+        if constexpr (HALO) {
+          m = fmaxf(m, fabsf(hx[j]));
+          ash = __fmaf_rn(fabsf(hx[j]), wsum[j], ash);
+        }
       }
       const uint32_t mw = wave_max_bits(m);
       const bool finite = mw < 0x7F800000u;
@@ -345,21 +402,35 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       // sum |x| over the wave's channels per pixel, then over the three taps
       // of a row
       float ap[2] = {rows_sum(as[0]), rows_sum(as[1])};
-      window3(ap, abn);
+      window3<HALO>(ap, HALO ? rows_sum(ash) : 0.0f, abn);
 
-      // digits, packed two per register
-      cert_u32x4 hi[2], lo[2];
+      // digits, packed two per register (HALO: the halo's in hh, hl)
+      // (x, y: the high digits' pair, then the low digits')
+      auto digits = [&](float x0, float x1) __attribute__((always_inline)) {
+        const float u0 = __fmul_rn(x0, sc), u1 = __fmul_rn(x1, sc);
+        const float d10 = __builtin_rintf(u0), d11 = __builtin_rintf(u1);
+        const float d00 = __builtin_rintf(__fmul_rn(__fsub_rn(u0, d10), 2048.0f));
+        const float d01 = __builtin_rintf(__fmul_rn(__fsub_rn(u1, d11), 2048.0f));
+        return make_uint2(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d10, d11)),
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d00, d01)));
+      };
+      cert_u32x4 hi[2], lo[2], hh, hl;
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float u0 = __fmul_rn(xv[s][2 * i], sc), u1 = __fmul_rn(xv[s][2 * i + 1], sc);
-          const float d10 = __builtin_rintf(u0), d11 = __builtin_rintf(u1);
-          const float d00 = __builtin_rintf(__fmul_rn(__fsub_rn(u0, d10), 2048.0f));
-          const float d01 = __builtin_rintf(__fmul_rn(__fsub_rn(u1, d11), 2048.0f));
-          hi[s][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d10, d11));
-          lo[s][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d00, d01));
+          const uint2 d = digits(xv[s][2 * i], xv[s][2 * i + 1]);
+          hi[s][i] = d.x;
+          lo[s][i] = d.y;
         }
+      if constexpr (HALO) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint2 d = digits(hx[2 * i], hx[2 * i + 1]);
+          hh[i] = d.x;
+          hl[i] = d.y;
+        }
+      }
       // digit sums per ky (taps ky * 3 + kx), kx = 1 first
       cert_f32x4 zh[3][2], zl[3][2];
       const cert_f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -374,8 +445,13 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         // kx = 0: even pixels take the odd segment one lane down, odd pixels
         // the even segment
         cert_u32x4 dh, dl;
-        lane_down(hi[1], dh);
-        lane_down(lo[1], dl);
+        if constexpr (HALO) {
+          lane_down_h(hi[1], hh, dh);
+          lane_down_h(lo[1], hl, dl);
+        } else {
+          lane_down(hi[1], dh);
+          lane_down(lo[1], dl);
+        }
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
           zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dh), Bw[ky * 3], zh[ky][0], 0, 0, 0);
@@ -388,8 +464,13 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         // kx = 2: even pixels take the odd segment, odd pixels the even
         // segment one lane up
         cert_u32x4 uh, ul;
-        lane_up(hi[0], uh);
-        lane_up(lo[0], ul);
+        if constexpr (HALO) {
+          lane_up_h(hi[0], hh, uh);
+          lane_up_h(lo[0], hl, ul);
+        } else {
+          lane_up(hi[0], uh);
+          lane_up(lo[0], ul);
+        }
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
           zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[1]), Bw[ky * 3 + 2], zh[ky][0], 0, 0, 0);
@@ -455,7 +536,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         const bool c1 = lo >= f_t1, c2 = lo >= f_t2;
         const bool ok = f_thr && (hi >= f_t1) == c1 && (hi >= f_t2) == c2 && lo >= -f_dc && hi <= f_dc;
         bit[k] = (f_b0 ^ c1 ^ c2) && chan;
-        unc[k] = !ok && chan && fpx0 + k >= vlo && fpx0 + k < vhi;
+        unc[k] = !ok && chan && fpx0 + k < vhi;
       }
       uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
       uint64_t um[2] = {__ballot(unc[0]), __ballot(unc[1])};
@@ -491,11 +572,15 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
           // channels past cin, inside the block's LDS (a row buffer holds
           // at least cin channels and 11 KiB of partials follow the ring),
           // and adds +0 for them, which leaves a sum that started at +0
-          // unchanged.
+          // unchanged.  HALO: a column outside the window (-1 or 32) reads
+          // the row's halo, [channel][side], instead.
           const uint4 m4 = *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4]);
+          const bool hcol = HALO && (ix < 0 || ix > 31);
+          const int ixr = hcol ? 0 : ix;
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
-          const float* ch0 = rowp + (row_off(0, ix) >> 2);       // channels 4 m, 4 m + 3
-          const float* ch1 = rowp + (row_off(1, ix) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
+          const float* ch0 = rowp + (row_off(0, ixr) >> 2);       // channels 4 m, 4 m + 3
+          const float* ch1 = rowp + (row_off(1, ixr) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
+          const float* hp = hal + (size_t)(iy % kCertRing) * (kHaloSlot / 4) + (ix < 0 ? 0 : 1);
           for (int cb = 0; cb < cin; cb += 32) {
             float xb[32];
 #pragma unroll
@@ -505,6 +590,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
               xb[j + 1] = ch1[c4 * 32 + 32];
               xb[j + 2] = ch1[c4 * 32 + 64];
               xb[j + 3] = ch0[c4 * 32 + 96];
+            }
+            if (hcol) {
+#pragma unroll
+              for (int j = 0; j < 32; ++j) xb[j] = hp[2 * (cb + j)];
             }
             // -x for a clear mask bit: bit j of the inverted word moved to
             // the sign position
@@ -535,7 +624,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       }
 
       // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k
-      if (fc < 2 && fpx0 + fc >= vlo && fpx0 + fc < vhi) {
+      if (fc < 2 && fpx0 + fc < vhi) {
         const uint32_t word = (uint32_t)((fc ? bm[1] : bm[0]) >> (16 * fq)) & 0xFFFFu;
         const int HW = H * W;
         uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)r * W + wx0 + fpx0 + fc) * cwo) + grp * 2;
@@ -567,28 +656,36 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= kCertFar) return hipErrorInvalidValue;
   const int nld = (a.cin + 7) / 8;
-  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4;
-  const bool guard = a.cin / 4 < 28;
+  const bool guard = a.cin / 4 < 28, halo = a.W > 32;
+  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4 + (halo ? kCertRing * kHaloSlot : 0);
+  const void* fn = guard ? (halo ? (const void*)k_real_cert<true, true> : (const void*)k_real_cert<true, false>)
+                         : (halo ? (const void*)k_real_cert<false, true> : (const void*)k_real_cert<false, false>);
+  const int var = (guard ? 1 : 0) + (halo ? 2 : 0);
   // the kernel asks for more than 64 KiB of LDS: allow it once per variant
   // and device (bit d of the variant's mask for device d)
-  static std::atomic<uint64_t> attr[2];
+  static std::atomic<uint64_t> attr[4];
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
-  if (!(attr[guard].load(std::memory_order_acquire) & bit)) {
-    hipError_t e = guard ? hipFuncSetAttribute((const void*)k_real_cert<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)
-                         : hipFuncSetAttribute((const void*)k_real_cert<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr[guard].fetch_or(bit, std::memory_order_acq_rel);
+  if (!(attr[var].load(std::memory_order_acquire) & bit)) {
+    if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); e != hipSuccess)
+      return e;
+    attr[var].fetch_or(bit, std::memory_order_acq_rel);
   }
-  const long ntile = a.W <= 32 ? 1 : (a.W + 23) / 24;
+  const long ntile = halo ? (a.W + 31) / 32 : 1;
   const long nitems = (long)a.N * ntile * ((a.cout + 15) / 16);
   if (nitems >= 0x7FFFFFF0) return hipErrorInvalidValue;
   // a multiple of 8 blocks (one per XCD in turn); the padding ones exit
   const bool xorder = ntile > 1 || a.cout > 16;
   const dim3 grid((unsigned)(xorder ? (nitems + 7) / 8 * 8 : nitems));
-  if (guard) hipLaunchKernelGGL((k_real_cert<true>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
-  else hipLaunchKernelGGL((k_real_cert<false>), grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
+  const uint32_t xb = (uint32_t)xbytes, ni = (uint32_t)nitems;
+  if (guard) {
+    if (halo) hipLaunchKernelGGL((k_real_cert<true, true>), grid, dim3(256), lds, s, a, xb, nld, ni);
+    else hipLaunchKernelGGL((k_real_cert<true, false>), grid, dim3(256), lds, s, a, xb, nld, ni);
+  } else {
+    if (halo) hipLaunchKernelGGL((k_real_cert<false, true>), grid, dim3(256), lds, s, a, xb, nld, ni);
+    else hipLaunchKernelGGL((k_real_cert<false, false>), grid, dim3(256), lds, s, a, xb, nld, ni);
+  }
   return hipGetLastError();
 }
 

@@ -7,7 +7,9 @@ bound cannot decide many outputs and the reference-order recompute must:
   exactly on one integer sum: about one output in a hundred sits on z = 0;
 * bands scaled by 2^-20 .. 2^20, zero rows, and an infinity and a NaN;
 * the scene path (edge patches partly outside the cube);
-* rows wider than 32 (tiles of 24 output columns with a 4-column margin).
+* rows wider than 32 (tiles of 32 columns whose edge outputs read the
+  neighbouring columns from a one-column halo either side), with undecided
+  and non-finite outputs at the tile edges.
 
 The debug forward reports the act1 bits of the certified kernel (its float
 conv output comes from the exact-order kernel); the plain forward's logits
@@ -59,7 +61,7 @@ def _check(eng, model, x):
         assert _bits_equal(plain[n], want), ("plain logits", n)
 
 
-@pytest.mark.parametrize("H,W", [(32, 32), (24, 76)])
+@pytest.mark.parametrize("H,W", [(32, 32), (24, 76), (24, 96)])
 def test_cert_threshold_ties(tmp_path, orc, H, W):
     b = synth.make_blob(seed=41)
     rng = np.random.default_rng(42)
@@ -104,6 +106,25 @@ def test_cert_wide_range_and_nonfinite(tmp_path, orc):
     eng.close()
 
 
+def test_cert_wide_edges_nonfinite(tmp_path, orc):
+    """Rows of 72 (tiles 0-31, 32-63, 64-71): an infinity, a NaN, a zero
+    column and large values in the columns either side of each tile edge,
+    which the edge outputs read through the halo."""
+    b = synth.make_blob(seed=47)
+    rng = np.random.default_rng(48)
+    x = rng.standard_normal((3, 120, 20, 72), dtype=np.float32)
+    x[0, 5, 4, 31] = np.inf
+    x[0, 9, 11, 32] = -np.inf
+    x[1, 77, 9, 63] = np.nan
+    x[1, 3, 15, 64] = np.nan
+    x[2, :, :, 32] = 0.0
+    x[2, :, 6, 30:34] *= np.float32(1e6)
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
 @pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16),
                                        (16, 16, 72), (8, 20, 100), (32, 16, 256), (16, 36, 36)])
 def test_cert_shapes(tmp_path, orc, base, H, W):
@@ -142,7 +163,7 @@ def test_cert_vs_exact_order_batch(tmp_path):
 
 
 def test_cert_wide_vs_exact_order(tmp_path):
-    """Rows wider than 32 run as tiles of 24 output columns: the large-tile
+    """Rows wider than 32 run as tiles of 32 columns with a halo: the large-tile
     configuration's shape (256 x 256, base 32: two 16-channel groups) against
     the order-exact kernel."""
     b = synth.make_blob(seed=51, base=32)

@@ -290,7 +290,7 @@ def test_cfg4_large_tile_vs_checker(tmp_path, orc, monkeypatch):
 
 def test_cfg4_full_batch(tmp_path, orc, monkeypatch):
     """Benchmark config 4 at its real batch: 64 patches of 256x256x120, base
-    32 (the certified first conv in tiles of 24 columns with both 16-channel
+    32 (the certified first conv in tiles of 32 columns with both 16-channel
     groups, the matrix-core binary convs).  Every patch of the batch equals
     its own single-patch run, and two patches equal the checker."""
     from concurrent.futures import ThreadPoolExecutor
