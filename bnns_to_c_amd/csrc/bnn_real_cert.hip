@@ -194,7 +194,13 @@ __device__ __forceinline__ int part_idx(int s, int g, int c) { return ((s * 4 + 
 // element j of lane (p, gq) is channel cpw * w + 4 j + gq, column 16 s + p;
 // elements past the wave's channels read as 0.  GUARD: such elements may
 // occur for j < 7 (cpw < 28); otherwise only element 7 can be one.
-template <bool GUARD, bool HALO>
+//
+// G = 2 (17 to 32 output channels): one block makes both 16-channel groups
+// of its tile from one conversion of the input (two sets of matrix ops, two
+// partial sets in LDS, one whole output word per pixel); its recompute
+// reads the sign masks and the halo columns from global memory, which
+// leaves LDS room for two blocks per CU.
+template <bool GUARD, bool HALO, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -213,8 +219,8 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   // with theirs (the halo columns): their reads and writes meet in that
   // XCD's L2
   // (one block per patch keeps the plain order)
-  const int ng = (a.cout + 15) >> 4;
-  const bool xorder = ng > 1 || ntile > 1;
+  const int ng = (a.cout + 16 * G - 1) / (16 * G);  // blocks per tile
+  const bool xorder = ng > 1 || ntile > 1 || G > 1;
   const uint32_t item = xorder ? (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   if (item >= nitems) return;
   const int grp = (int)(item % (uint32_t)ng), tt = (int)(item / (uint32_t)ng);
@@ -222,30 +228,37 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   const int wx0 = HALO ? 32 * tile : 0;  // image column of window column 0
   const int vhi = HALO ? min(32, W - wx0) : W;  // output window columns 0 .. vhi - 1
   const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
-  float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [wave][512]
-  float* absw = opart + 4 * 512;                         // [wave][32]
+  float* opart = cert_lds + (size_t)kCertRing * rb / 4;  // [group][wave][512]
+  float* absw = opart + G * 4 * 512;                     // [wave][32]
   float* qw = absw + 4 * 32;                             // [wave]
-  uint32_t* wsl = reinterpret_cast<uint32_t*>(qw + 4);   // [channel][tap][4] sign masks
-  // HALO: [ring slot][channel 128][side 2], at byte hal_off
-  const uint32_t hal_off = (uint32_t)kCertRing * rb + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4u;
+  uint32_t* wsl = reinterpret_cast<uint32_t*>(qw + 4);   // G = 1: [channel][tap][4] sign masks
+  // HALO: [slot][channel 128][side 2], at byte hal_off, one slot per ring
+  // row (G = 1) or two (G = 2: the conversion's and the next row's)
+  constexpr int kHS = G == 1 ? kCertRing : 2;
+  const uint32_t hal_off = (uint32_t)kCertRing * rb + (G * 4 * 512 + 4 * 32 + 4 + (G == 1 ? 16 * 36 : 0)) * 4u;
   const float* hal = cert_lds + hal_off / 4;
+  // G = 2: the 32 channels' fold parameters, [parameter 9][channel 32]
+  // (alpha, A, B, slope, rsign, t1, t2, dc, b0), after the halo slots
+  float* fpar = cert_lds + hal_off / 4 + (HALO ? kHS * kHaloSlot / 4 : 0);
   typedef __attribute__((address_space(3))) float* lds_f32;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_f32)cert_lds;
 
-  // this wave's operand table: B[t] for tap t
-  cert_f16x8 Bw[9];
-  {
-    const uint4* src = reinterpret_cast<const uint4*>(a.cwb) + ((size_t)(grp * 4 + wv) * 9) * 64 + lane;
+  // this wave's operand tables: Bw[g][t] for group g, tap t
+  cert_f16x8 Bw[G][9];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.cwb) + ((size_t)((grp * G + g) * 4 + wv) * 9) * 64 + lane;
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const uint4 v = src[t * 64];
-      Bw[t] = as_h8((cert_u32x4){v.x, v.y, v.z, v.w});
+      Bw[g][t] = as_h8((cert_u32x4){v.x, v.y, v.z, v.w});
     }
   }
 
-  // the group's sign masks (16 channels x 9 taps x 4 words) for the
+  // G = 1: the group's sign masks (16 channels x 9 taps x 4 words) for the
   // reference-order recompute; the first row barrier orders them
-  for (int i = tid; i < 16 * 36; i += 256) wsl[i] = a.cws[(size_t)grp * 16 * 36 + i];
+  if constexpr (G == 1)
+    for (int i = tid; i < 16 * 36; i += 256) wsl[i] = a.cws[(size_t)grp * 16 * 36 + i];
 
   // DMA: wave w issues the row's 1 KiB loads k = w, w + 4, ... < nld; lane L
   // of load k fetches 16 bytes: channel 8 k + L / 8, column group (L % 8)
@@ -290,7 +303,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
                    : "memory");
     }
     if (HALO && 32 * wv < cin) {
-      const uint32_t m0h = uni(lds0 + hal_off + (uint32_t)(y % kCertRing) * kHaloSlot + (uint32_t)wv * 256u);
+      const uint32_t m0h = uni(lds0 + hal_off + (uint32_t)(y % kHS) * kHaloSlot + (uint32_t)wv * 256u);
       const uint32_t vo = (inrow && hoff != kCertFar) ? hoff + ro : kCertFar;
       const dma_u32x4 rd = xsrc;
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
@@ -312,24 +325,51 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) wsum[j] = (float)(cin + 16 - (cpw * wv + 4 * j + gq));
 
-  // finalize: lane -> output channel fc, pixels fpx0 and fpx0 + 1
-  const int fc = lane & 15, fq = lane >> 4;
-  const int fpx0 = 8 * wv + 2 * fq;
-  const int co = 16 * grp + fc;
-  const bool chan = co < a.cout;
-  const float f_al = a.alpha[co], f_A = a.A[co], f_B = a.B[co], f_sl = a.slope[co], f_rs = a.rsign[co];
-  // the fold's bit along [-dc, dc] as at most two change points
+  // finalize: lane -> output channel fc of each group, pixels fpx0 and
+  // fpx0 + 1.  The fold's bit along [-dc, dc] as at most two change points
   // (real_fold_switches): bit(v) = b0 ^ (v >= t1) ^ (v >= t2) there, so an
   // interval inside [-dc, dc] holding no change point has one bit; b0 < 0
-  // marks a channel whose every output is recomputed
-  const float f_t1 = a.ct1[co], f_t2 = a.ct2[co], f_dc = a.cdc[co];
-  const bool f_thr = a.cb0[co] >= 0.0f, f_b0 = a.cb0[co] > 0.5f;
+  // marks a channel whose every output is recomputed.  G = 1 holds the
+  // lane's channel's parameters in registers, G = 2 reads them from LDS
+  // when it folds (fpar, staged here; the first row barrier orders it).
+  const int fc = lane & 15, fq = lane >> 4;
+  const int fpx0 = 8 * wv + 2 * fq;
+  float r_al = 0.0f, r_A = 0.0f, r_B = 0.0f, r_sl = 0.0f, r_rs = 0.0f, r_t1 = 0.0f, r_t2 = 0.0f, r_dc = 0.0f,
+        r_b0 = 0.0f;
+  if constexpr (G == 1) {
+    const int co = 16 * grp + fc;
+    r_al = a.alpha[co]; r_A = a.A[co]; r_B = a.B[co]; r_sl = a.slope[co]; r_rs = a.rsign[co];
+    r_t1 = a.ct1[co]; r_t2 = a.ct2[co]; r_dc = a.cdc[co]; r_b0 = a.cb0[co];
+  } else if (tid < 32) {
+    const int co = 32 * grp + tid;
+    const float* src[9] = {a.alpha, a.A, a.B, a.slope, a.rsign, a.ct1, a.ct2, a.cdc, a.cb0};
+#pragma unroll
+    for (int k = 0; k < 9; ++k) fpar[k * 32 + tid] = src[k][co];
+  }
+  // parameter k of group g for the lane's own channel, and for channel c
+  // of the group (the same in every lane)
+  auto fp_own = [&](int k, int g) __attribute__((always_inline)) -> float {
+    if constexpr (G == 1) {
+      const float rv[9] = {r_al, r_A, r_B, r_sl, r_rs, r_t1, r_t2, r_dc, r_b0};
+      return rv[k];
+    } else {
+      return fpar[k * 32 + 16 * g + fc];
+    }
+  };
+  auto fp_ch = [&](int k, int g, int c) __attribute__((always_inline)) -> float {
+    if constexpr (G == 1) {
+      const float rv[9] = {r_al, r_A, r_B, r_sl, r_rs, r_t1, r_t2, r_dc, r_b0};
+      return f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(rv[k]), c));  // lane c holds channel c
+    } else {
+      return fpar[k * 32 + 16 * g + c];
+    }
+  };
   // 2^-24 (1 + 2^-9 + 2^-19) times the weighted window sum: the 2^-9 covers
   // the round-to-nearest steps of A and Q, the 2^-19 those of E and the room
   // for rounding v -+ E to nearest (with the |v| 2^-22 term below)
   const float cA = 0x1p-24f * (1.0f + 0x1p-9f + 0x1p-19f);
   const int cwo = (a.cout + 31) >> 5;
-  const bool whole_word = (grp & 1) == 0 && grp == ng - 1;
+  const bool whole_word = G == 2 || ((grp & 1) == 0 && grp == ng - 1);
   // the partials of pixels fpx0 (even segment) and fpx0 + 1 (odd, 256 floats
   // on) in a wave's partial: segment row group wv, register fq
   const int i0 = part_idx(0, wv, fc) + fq;
@@ -339,11 +379,12 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   // rolling state, indexed by row mod 3: acc[r % 3] the partial of output
   // row r, ab[y % 3] / qr[y % 3] the window sums and Q of input row y.  The
   // row loop is unrolled by three so that every index is a constant.
-  cert_f32x4 acc[3][2];
+  cert_f32x4 acc[G][3][2];
   float ab[3][2], qr[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    acc[k][0] = acc[k][1] = (cert_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g][k][0] = acc[g][k][1] = (cert_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     ab[k][0] = ab[k][1] = 0.0f;
     qr[k] = 0.0f;
   }
@@ -372,7 +413,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       // channel (0 in the other lanes)
       float hx[8];
       if constexpr (HALO) {
-        const float* hrow = hal + (size_t)(yi % kCertRing) * (kHaloSlot / 4);
+        const float* hrow = hal + (size_t)(yi % kHS) * (kHaloSlot / 4);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float2 v = *reinterpret_cast<const float2*>(&hrow[2 * (cpw * wv + 4 * j + gq)]);
@@ -431,15 +472,18 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
           hl[i] = d.y;
         }
       }
-      // digit sums per ky (taps ky * 3 + kx), kx = 1 first
-      cert_f32x4 zh[3][2], zl[3][2];
+      // digit sums per ky (taps ky * 3 + kx), kx = 1 first, one group at a
+      // time
       const cert_f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+      cert_f32x4 zh[3][2], zl[3][2];
 #pragma unroll
       for (int ky = 0; ky < 3; ++ky)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[s]), Bw[ky * 3 + 1], z4, 0, 0, 0);
-          zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[s]), Bw[ky * 3 + 1], z4, 0, 0, 0);
+          zh[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[s]), Bw[g][ky * 3 + 1], z4, 0, 0, 0);
+          zl[ky][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[s]), Bw[g][ky * 3 + 1], z4, 0, 0, 0);
         }
       {
         // kx = 0: even pixels take the odd segment one lane down, odd pixels
@@ -454,10 +498,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         }
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
-          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dh), Bw[ky * 3], zh[ky][0], 0, 0, 0);
-          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dl), Bw[ky * 3], zl[ky][0], 0, 0, 0);
-          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[0]), Bw[ky * 3], zh[ky][1], 0, 0, 0);
-          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[0]), Bw[ky * 3], zl[ky][1], 0, 0, 0);
+          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dh), Bw[g][ky * 3], zh[ky][0], 0, 0, 0);
+          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(dl), Bw[g][ky * 3], zl[ky][0], 0, 0, 0);
+          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[0]), Bw[g][ky * 3], zh[ky][1], 0, 0, 0);
+          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[0]), Bw[g][ky * 3], zl[ky][1], 0, 0, 0);
         }
       }
       {
@@ -473,10 +517,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         }
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
-          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[1]), Bw[ky * 3 + 2], zh[ky][0], 0, 0, 0);
-          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[1]), Bw[ky * 3 + 2], zl[ky][0], 0, 0, 0);
-          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(uh), Bw[ky * 3 + 2], zh[ky][1], 0, 0, 0);
-          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ul), Bw[ky * 3 + 2], zl[ky][1], 0, 0, 0);
+          zh[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(hi[1]), Bw[g][ky * 3 + 2], zh[ky][0], 0, 0, 0);
+          zl[ky][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(lo[1]), Bw[g][ky * 3 + 2], zl[ky][0], 0, 0, 0);
+          zh[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(uh), Bw[g][ky * 3 + 2], zh[ky][1], 0, 0, 0);
+          zl[ky][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ul), Bw[g][ky * 3 + 2], zl[ky][1], 0, 0, 0);
         }
       }
       // input row yi feeds output rows yi + 1 (ky 0), yi (ky 1), yi - 1 (ky 2)
@@ -484,25 +528,29 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          acc[cn][s][r] = __fmul_rn(__fmaf_rn(zh[0][s][r], 2048.0f, zl[0][s][r]), sb);
-          acc[c0][s][r] = __fmaf_rn(__fmaf_rn(zh[1][s][r], 2048.0f, zl[1][s][r]), sb, acc[c0][s][r]);
-          acc[cp][s][r] = __fmaf_rn(__fmaf_rn(zh[2][s][r], 2048.0f, zl[2][s][r]), sb, acc[cp][s][r]);
+          acc[g][cn][s][r] = __fmul_rn(__fmaf_rn(zh[0][s][r], 2048.0f, zl[0][s][r]), sb);
+          acc[g][c0][s][r] = __fmaf_rn(__fmaf_rn(zh[1][s][r], 2048.0f, zl[1][s][r]), sb, acc[g][c0][s][r]);
+          acc[g][cp][s][r] = __fmaf_rn(__fmaf_rn(zh[2][s][r], 2048.0f, zl[2][s][r]), sb, acc[g][cp][s][r]);
         }
+      }
     }
     ab[c0][0] = abn[0];
     ab[c0][1] = abn[1];
     qr[c0] = qn;
 
     if (yi >= 1) {
-      // output row r = yi - 1 is complete in acc[cp]: each wave leaves its
-      // partial, its window sum of |x| (rows yi - 2, yi - 1, yi) and its
+      // output row r = yi - 1 is complete in acc[g][cp]: each wave leaves its
+      // partials, its window sum of |x| (rows yi - 2, yi - 1, yi) and its
       // quantisation bound in LDS
       const int r = yi - 1;
-      float* mine = opart + wv * 512;
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-        *reinterpret_cast<float4*>(&mine[part_idx(s, gq, p)]) =
-            make_float4(acc[cp][s][0], acc[cp][s][1], acc[cp][s][2], acc[cp][s][3]);
+      for (int g = 0; g < G; ++g) {
+        float* mine = opart + (g * 4 + wv) * 512;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          *reinterpret_cast<float4*>(&mine[part_idx(s, gq, p)]) =
+              make_float4(acc[g][cp][s][0], acc[g][cp][s][1], acc[g][cp][s][2], acc[g][cp][s][3]);
+      }
       if (gq == 0)
         *reinterpret_cast<float2*>(&absw[wv * 32 + 2 * p]) =
             make_float2(__fadd_rn(__fadd_rn(ab[cn][0], ab[cp][0]), ab[c0][0]),
@@ -512,35 +560,53 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       block_barrier();
 
       // finalize: the four partials in wave order
-      float v[2] = {0.0f, 0.0f}, Aw[2] = {0.0f, 0.0f};
+      float v[G][2], Aw[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float t0 = opart[w * 512 + i0], t1 = opart[w * 512 + i0 + 256];
         const float2 u = *reinterpret_cast<const float2*>(&absw[w * 32 + fpx0]);
-        v[0] = __fadd_rn(v[0], t0);
-        v[1] = __fadd_rn(v[1], t1);
         Aw[0] = __fadd_rn(Aw[0], u.x);
         Aw[1] = __fadd_rn(Aw[1], u.y);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        v[g][0] = v[g][1] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float t0 = opart[(g * 4 + w) * 512 + i0], t1 = opart[(g * 4 + w) * 512 + i0 + 256];
+          v[g][0] = __fadd_rn(v[g][0], t0);
+          v[g][1] = __fadd_rn(v[g][1], t1);
+        }
       }
       const float4 qq = *reinterpret_cast<const float4*>(qw);
       const float Qs = __fadd_rn(__fadd_rn(qq.x, qq.y), __fadd_rn(qq.z, qq.w));
       // the row's quantisation part of E with its margins, and 2^-109 for
       // underflow
       const float Qc = __fadd_rn(__fmul_rn(Qs, 1.0f + 0x1p-9f + 0x1p-19f), 0x1p-109f);
-      bool bit[2], unc[2];
+      uint64_t bm[G][2], um[G][2];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        // E with room for rounding v -+ E to nearest
-        const float Ev = __fmaf_rn(fabsf(v[k]), 0x1p-22f, __fmaf_rn(cA, Aw[k], Qc));
-        const float lo = __fsub_rn(v[k], Ev), hi = __fadd_rn(v[k], Ev);
-        const bool c1 = lo >= f_t1, c2 = lo >= f_t2;
-        const bool ok = f_thr && (hi >= f_t1) == c1 && (hi >= f_t2) == c2 && lo >= -f_dc && hi <= f_dc;
-        bit[k] = (f_b0 ^ c1 ^ c2) && chan;
-        unc[k] = !ok && chan && fpx0 + k < vhi;
+      for (int g = 0; g < G; ++g) {
+        bool bit[2], unc[2];
+        const float t1 = fp_own(5, g), t2 = fp_own(6, g), dc = fp_own(7, g), b0 = fp_own(8, g);
+        const bool chan = 16 * (grp * G + g) + fc < a.cout, thr = b0 >= 0.0f, one = b0 > 0.5f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          // E with room for rounding v -+ E to nearest
+          const float Ev = __fmaf_rn(fabsf(v[g][k]), 0x1p-22f, __fmaf_rn(cA, Aw[k], Qc));
+          const float lo = __fsub_rn(v[g][k], Ev), hi = __fadd_rn(v[g][k], Ev);
+          const bool c1 = lo >= t1, c2 = lo >= t2;
+          const bool ok = thr && (hi >= t1) == c1 && (hi >= t2) == c2 && lo >= -dc && hi <= dc;
+          bit[k] = (one ^ c1 ^ c2) && chan;
+          unc[k] = !ok && chan && fpx0 + k < vhi;
+        }
+        bm[g][0] = __ballot(bit[0]);
+        bm[g][1] = __ballot(bit[1]);
+        um[g][0] = __ballot(unc[0]);
+        um[g][1] = __ballot(unc[1]);
       }
-      uint64_t bm[2] = {__ballot(bit[0]), __ballot(bit[1])};
-      uint64_t um[2] = {__ballot(unc[0]), __ballot(unc[1])};
-      if (um[0] | um[1]) {
+      uint64_t uany = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) uany |= um[g][0] | um[g][1];
+      if (uany) {
         // A is NaN exactly when the window holds a NaN (its terms are |x|
         // times positive weights; such an output is never certified): the
         // reference's sum is then NaN and the fold's bit 0 for any
@@ -548,18 +614,25 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const uint64_t nm = __ballot(Aw[k] != Aw[k]);
-          um[k] &= ~nm;
-          bm[k] &= ~nm;
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            um[g][k] &= ~nm;
+            bm[g][k] &= ~nm;
+          }
         }
-        nund += (uint32_t)(__builtin_popcountll(um[0]) + __builtin_popcountll(um[1]));
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          nund += (uint32_t)(__builtin_popcountll(um[g][0]) + __builtin_popcountll(um[g][1]));
       }
 
       // uncertain outputs: the reference's order, lane t < 9 summing tap t
       // over the channels from the LDS rows r - 1 .. r + 1
-      while (um[0] | um[1]) {
-        const int which = um[0] ? 0 : 1;
-        const int li = __builtin_ctzll(um[which]);
-        um[which] &= um[which] - 1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+      while (um[g][0] | um[g][1]) {
+        const int which = um[g][0] ? 0 : 1;
+        const int li = __builtin_ctzll(um[g][which]);
+        um[g][which] &= um[g][which] - 1;
         const int upx = 8 * wv + 2 * (li >> 4) + which;
         float st = 0.0f;
         const int ky = lane / 3, kx = lane - 3 * (lane / 3);
@@ -573,14 +646,23 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
           // at least cin channels and 11 KiB of partials follow the ring),
           // and adds +0 for them, which leaves a sum that started at +0
           // unchanged.  HALO: a column outside the window (-1 or 32) reads
-          // the row's halo, [channel][side], instead.
-          const uint4 m4 = *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4]);
+          // the row's halo, [channel][side] (G = 1), or global memory
+          // (G = 2), instead.
+          const uint4 m4 = G == 1 ? *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4])
+                                  : *reinterpret_cast<const uint4*>(
+                                        &a.cws[(((size_t)(grp * G + g) * 16 + (li & 15)) * 9 + lane) * 4]);
           const bool hcol = HALO && (ix < 0 || ix > 31);
           const int ixr = hcol ? 0 : ix;
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
           const float* ch0 = rowp + (row_off(0, ixr) >> 2);       // channels 4 m, 4 m + 3
           const float* ch1 = rowp + (row_off(1, ixr) >> 2) - 32;  // channels 4 m + 1, 4 m + 2
-          const float* hp = hal + (size_t)(iy % kCertRing) * (kHaloSlot / 4) + (ix < 0 ? 0 : 1);
+          const float* hp = hal + (size_t)(iy % kHS) * (kHaloSlot / 4) + (ix < 0 ? 0 : 1);
+          // (G = 2: the column in global memory by buffer loads, byte offset
+          // goff + channel * cs4; outside the input, past the buffer: 0)
+          const uint32_t goff = iy < ig.ylim && wx0 + ix < ig.xlim
+                                    ? (uint32_t)(ig.base + (size_t)iy * ig.rstride + (wx0 + ix)) * 4u
+                                    : kCertFar;
+          const uint32_t cs4 = (uint32_t)ig.cstride * 4u;
           for (int cb = 0; cb < cin; cb += 32) {
             float xb[32];
 #pragma unroll
@@ -592,8 +674,15 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
               xb[j + 3] = ch0[c4 * 32 + 96];
             }
             if (hcol) {
+              if constexpr (G == 1) {
 #pragma unroll
-              for (int j = 0; j < 32; ++j) xb[j] = hp[2 * (cb + j)];
+                for (int j = 0; j < 32; ++j) xb[j] = hp[2 * (cb + j)];
+              } else {
+                // (channels past cin are added as +0 below whatever is read)
+                const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, xbytes);
+#pragma unroll
+                for (int j = 0; j < 32; ++j) xb[j] = ld_f32(rs, goff + (uint32_t)(cb + j) * cs4, 0u);
+              }
             }
             // -x for a clear mask bit: bit j of the inverted word moved to
             // the sign position
@@ -614,29 +703,39 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
         float tot = 0.0f;
 #pragma unroll
         for (int t = 0; t < 9; ++t) tot = __fadd_rn(tot, f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(st), t)));
-        // the channel's fold parameters from lane li, which holds them
-        auto from_li = [&](float f) __attribute__((always_inline)) {
-          return f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(f), li));
-        };
+        // the fold parameters of lane li's channel
+        const int lc = li & 15;
         float zz;
-        const bool ub = fold_bit(tot, from_li(f_al), from_li(f_A), from_li(f_B), from_li(f_sl), from_li(f_rs), zz);
-        bm[which] = ub ? (bm[which] | (1ull << li)) : (bm[which] & ~(1ull << li));
+        const bool ub = fold_bit(tot, fp_ch(0, g, lc), fp_ch(1, g, lc), fp_ch(2, g, lc), fp_ch(3, g, lc), fp_ch(4, g, lc), zz);
+        bm[g][which] = ub ? (bm[g][which] | (1ull << li)) : (bm[g][which] & ~(1ull << li));
+      }
       }
 
-      // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k
+      // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k: its
+      // 16 bits of the group (G = 1), or the whole word of both groups
       if (fc < 2 && fpx0 + fc < vhi) {
-        const uint32_t word = (uint32_t)((fc ? bm[1] : bm[0]) >> (16 * fq)) & 0xFFFFu;
         const int HW = H * W;
-        uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ((size_t)n * HW + (size_t)r * W + wx0 + fpx0 + fc) * cwo) + grp * 2;
-        if (whole_word) *reinterpret_cast<uint32_t*>(dst) = word;
-        else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+        const size_t pix = (size_t)n * HW + (size_t)r * W + wx0 + fpx0 + fc;
+        if constexpr (G == 2) {
+          const uint32_t w0 = (uint32_t)((fc ? bm[0][1] : bm[0][0]) >> (16 * fq)) & 0xFFFFu;
+          const uint32_t w1 = (uint32_t)((fc ? bm[1][1] : bm[1][0]) >> (16 * fq)) & 0xFFFFu;
+          a.out[pix * cwo + grp] = w0 | (w1 << 16);
+        } else {
+          const uint32_t word = (uint32_t)((fc ? bm[0][1] : bm[0][0]) >> (16 * fq)) & 0xFFFFu;
+          uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + pix * cwo) + grp * 2;
+          if (whole_word) *reinterpret_cast<uint32_t*>(dst) = word;
+          else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+        }
       }
     }
     // next step: output rows yi + 1 and yi, input rows yi - 1 and yi
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      acc[cp][s] = acc[c0][s];
-      acc[c0][s] = acc[cn][s];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        acc[g][cp][s] = acc[g][c0][s];
+        acc[g][c0][s] = acc[g][cn][s];
+      }
       ab[cn][s] = ab[cp][s];
       ab[cp][s] = ab[c0][s];
     }
@@ -657,35 +756,35 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if (xbytes >= kCertFar) return hipErrorInvalidValue;
   const int nld = (a.cin + 7) / 8;
   const bool guard = a.cin / 4 < 28, halo = a.W > 32;
-  const size_t lds = (size_t)kCertRing * nld * 1024 + (4 * 512 + 4 * 32 + 4 + 16 * 36) * 4 + (halo ? kCertRing * kHaloSlot : 0);
-  const void* fn = guard ? (halo ? (const void*)k_real_cert<true, true> : (const void*)k_real_cert<true, false>)
-                         : (halo ? (const void*)k_real_cert<false, true> : (const void*)k_real_cert<false, false>);
-  const int var = (guard ? 1 : 0) + (halo ? 2 : 0);
+  // 17 to 32 output channels: both 16-channel groups in one block
+  const int G = a.cout > 16 && a.cout <= 32 ? 2 : 1;
+  const size_t lds = (size_t)kCertRing * nld * 1024 + (G * 4 * 512 + 4 * 32 + 4 + (G == 1 ? 16 * 36 : 0)) * 4 +
+                     (halo ? (G == 1 ? kCertRing : 2) * kHaloSlot : 0) + (G == 2 ? 9 * 32 * 4 : 0);
+  // the variant's entry and its index (guard, halo, G = 2 bits)
+  using Fn = void (*)(const RealArgs, uint32_t, int, uint32_t);
+  static const Fn fns[8] = {k_real_cert<false, false, 1>, k_real_cert<true, false, 1>, k_real_cert<false, true, 1>,
+                            k_real_cert<true, true, 1>,   k_real_cert<false, false, 2>, k_real_cert<true, false, 2>,
+                            k_real_cert<false, true, 2>,  k_real_cert<true, true, 2>};
+  const int var = (guard ? 1 : 0) + (halo ? 2 : 0) + (G == 2 ? 4 : 0);
   // the kernel asks for more than 64 KiB of LDS: allow it once per variant
   // and device (bit d of the variant's mask for device d)
-  static std::atomic<uint64_t> attr[4];
+  static std::atomic<uint64_t> attr[8];
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
   if (!(attr[var].load(std::memory_order_acquire) & bit)) {
-    if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); e != hipSuccess)
+    if (hipError_t e = hipFuncSetAttribute((const void*)fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        e != hipSuccess)
       return e;
     attr[var].fetch_or(bit, std::memory_order_acq_rel);
   }
   const long ntile = halo ? (a.W + 31) / 32 : 1;
-  const long nitems = (long)a.N * ntile * ((a.cout + 15) / 16);
+  const long nitems = (long)a.N * ntile * ((a.cout + 16 * G - 1) / (16 * G));
   if (nitems >= 0x7FFFFFF0) return hipErrorInvalidValue;
   // a multiple of 8 blocks (one per XCD in turn); the padding ones exit
   const bool xorder = ntile > 1 || a.cout > 16;
   const dim3 grid((unsigned)(xorder ? (nitems + 7) / 8 * 8 : nitems));
-  const uint32_t xb = (uint32_t)xbytes, ni = (uint32_t)nitems;
-  if (guard) {
-    if (halo) hipLaunchKernelGGL((k_real_cert<true, true>), grid, dim3(256), lds, s, a, xb, nld, ni);
-    else hipLaunchKernelGGL((k_real_cert<true, false>), grid, dim3(256), lds, s, a, xb, nld, ni);
-  } else {
-    if (halo) hipLaunchKernelGGL((k_real_cert<false, true>), grid, dim3(256), lds, s, a, xb, nld, ni);
-    else hipLaunchKernelGGL((k_real_cert<false, false>), grid, dim3(256), lds, s, a, xb, nld, ni);
-  }
+  hipLaunchKernelGGL(fns[var], grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
   return hipGetLastError();
 }
 

@@ -61,9 +61,13 @@ def _check(eng, model, x):
         assert _bits_equal(plain[n], want), ("plain logits", n)
 
 
-@pytest.mark.parametrize("H,W", [(32, 32), (24, 76), (24, 96)])
-def test_cert_threshold_ties(tmp_path, orc, H, W):
-    b = synth.make_blob(seed=41)
+@pytest.mark.parametrize("H,W,base", [(32, 32, 16), (24, 76, 16), (24, 96, 16), (32, 32, 32), (24, 76, 32),
+                                       (24, 40, 24)])
+def test_cert_threshold_ties(tmp_path, orc, H, W, base):
+    """Ties on the fold's threshold, so that many outputs are undecided and
+    recomputed; bases 24 and 32 run both 16-channel groups in one block,
+    whose recompute reads sign masks and halo columns from global memory."""
+    b = synth.make_blob(seed=41, base=base)
     rng = np.random.default_rng(42)
     N = 2
     x = rng.choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, H, W))
@@ -75,7 +79,7 @@ def test_cert_threshold_ties(tmp_path, orc, H, W):
     Bv = act.B.copy()
     rs = act.rsign.copy()
     for c in range(conv.shape[0]):
-        o0 = conv[c, 5 + c, 3 + c]  # one of the patch's own outputs
+        o0 = conv[c, 5 + c % 16, 3 + c % 16]  # one of the patch's own outputs
         Bv[c] = np.float32(-(A[c] * o0))
         rs[c] = np.float32(0.0) if c % 2 == 0 else np.float32(1e-30)
     act.B = Bv.astype(np.float32)
@@ -106,11 +110,12 @@ def test_cert_wide_range_and_nonfinite(tmp_path, orc):
     eng.close()
 
 
-def test_cert_wide_edges_nonfinite(tmp_path, orc):
+@pytest.mark.parametrize("base", [16, 32])
+def test_cert_wide_edges_nonfinite(tmp_path, orc, base):
     """Rows of 72 (tiles 0-31, 32-63, 64-71): an infinity, a NaN, a zero
     column and large values in the columns either side of each tile edge,
     which the edge outputs read through the halo."""
-    b = synth.make_blob(seed=47)
+    b = synth.make_blob(seed=47, base=base)
     rng = np.random.default_rng(48)
     x = rng.standard_normal((3, 120, 20, 72), dtype=np.float32)
     x[0, 5, 4, 31] = np.inf
