@@ -32,7 +32,7 @@ namespace {
 // padded to 128 bytes mod 256, so the 16 lanes of a group (16 pixels of one
 // row) read distinct banks.  Two buffers: chunk c + 1 is expanded and stored
 // while chunk c is consumed, and its words are loaded from HBM one chunk
-// earlier.  A comes straight from the weight table, one K step ahead.
+// earlier.  A comes straight from the weight table, two K steps ahead.
 //
 // One K step (64) is one tap of one chunk: lane group q = lane / 16 takes
 // word q / 2 of the chunk, channels 16 * (q % 2) .. +15 of it, in A and B
@@ -223,8 +223,10 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
   advance();
   if (lok) stage_load(lit, lc);
   uint32_t abase = a_base(it);
-  i32x4v Aa[4];
+  i32x4v Aa[4], A1[4];
   loadA(abase, 0, Aa);
+  if (T.nch * 9 > 1) loadA(abase, 1, A1);
+  else loadA(a_base(item_of(li + nslot)), 0, A1);
   __syncthreads();
   int buf = 0;
 #pragma unroll 1
@@ -232,14 +234,15 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 #pragma unroll 1
     for (int c = 0; c < T.nch; ++c) {
       const bool last = c + 1 == T.nch;
-      const uint32_t nbase = last ? a_base(item_of(li + nslot)) : abase;  // past the last item: unused
       const uint32_t bo = (uint32_t)buf * bufb;
 #pragma unroll
       for (int t = 0; t < 9; ++t) {
         const int ky = t / 3, kx = t % 3;
+        // the K step two ahead: this item's, or the next item's first two
         i32x4v An[4];
-        if (t < 8) loadA(abase, c * 9 + t + 1, An);
-        else loadA(nbase, last ? 0 : c * 9 + 9, An);
+        const int s2 = c * 9 + t + 2;
+        if (s2 < T.nch * 9) loadA(abase, s2, An);
+        else loadA(a_base(item_of(li + nslot)), s2 - T.nch * 9, An);
         const uint32_t dt = bo + (uint32_t)((ky - 1) * T.rs + (kx - 1) * kSlot);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -248,7 +251,10 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
           for (int m = 0; m < 4; ++m) acc[m][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aa[m], B, acc[m][g], 0, 0, 0);
         }
 #pragma unroll
-        for (int m = 0; m < 4; ++m) Aa[m] = An[m];
+        for (int m = 0; m < 4; ++m) {
+          Aa[m] = A1[m];
+          A1[m] = An[m];
+        }
       }
       // the next chunk into the other buffer, the one after it from HBM
       if (lok) {
