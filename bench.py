@@ -830,7 +830,7 @@ def main() -> int:
             "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
                      "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
                      "kernels": cfg4_kern,
-                     "int8_mfma_rule": "binary convs with >= 4 chunks of 64 input channels and 8 <= W <= 64"},
+                     "int8_mfma_rule": "fold convs of 32-wide rows with >= 4 chunks of 64 input channels (dec4.c1, dec4.c2 here)"},
             "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
                                 "past the scene), benchmark config 3",
                       "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),

@@ -408,8 +408,17 @@ bool cert_mode() {
   return !(e && !strcmp(e, "0"));
 }
 
+// The int8 matrix-core conv by default only where whole forwards measure
+// it faster than the popcount kernel: fold layers of 32-wide rows (tiles of
+// eight whole rows) with at least 4 input chunks of 64 channels.  In
+// config 4 (256 x 256, base 32) that is dec4.c1 and dec4.c2: forward
+// 2.767-2.772 ms against 2.780-2.786 with the popcount kernel everywhere
+// and 2.800-2.809 when every fold or pool layer of 4+ chunks took it
+// (dec3.c1 at 64-wide rows 9% slower, the pool layers and the 16 x 16
+// bottleneck 3-5% slower).  BNN_BCONV_MFMA=2 takes it wherever it fits.
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
-  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || mfma_nchunk(L.cw0, L.cw1) >= 4);
+  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) &&
+         (L.mfma == 2 || (mfma_nchunk(L.cw0, L.cw1) >= 4 && W == 32 && epi == EPI_FOLD));
 }
 
 struct Workspace {

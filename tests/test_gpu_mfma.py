@@ -77,17 +77,18 @@ def test_forced_mfma_stages_vs_checker(tmp_path, orc, monkeypatch, seed, base, N
 
 
 def test_default_rule_picks_wide_layers(tmp_path, orc, monkeypatch):
-    """Default: the matrix cores for 8 <= W <= 64 and >= 4 input chunks."""
+    """Default: the matrix cores for fold layers of 32-wide rows with >= 4
+    input chunks of 64 channels."""
     monkeypatch.delenv("BNN_BCONV_MFMA", raising=False)
     b = synth.make_blob(seed=26, base=32)
     p = tmp_path / "m.blob"
     p.write_bytes(B.to_bytes(b))
     eng = E.Engine(str(p))
-    x = synth.make_input(126, 1, 120, 64, 64)
+    x = synth.make_input(126, 1, 120, 128, 128)
     ops = _ops(eng, x)
-    # base 32 at 64x64: enc4 256 ch at 8x8, bottleneck 512 at 4x4, dec4 reads
-    # 256 + 512 at 8x8, dec3 128 + 256 at 16x16
-    want = {"enc4.c2", "dec4.c1", "dec4.c2", "dec3.c1"}
+    # base 32 at 128x128: level 2 is 32 wide; dec3.c1 reads 128 + 256
+    # channels there (6 chunks), dec3.c2 128 (2 chunks), enc3.c2 pools
+    want = {"dec3.c1"}
     got = {lab for lab, op in ops.items() if op.endswith("_mfma")}
     assert got == want, (got, ops)
     _check_stages(eng, orc.parse(B.to_bytes(b)), x)
