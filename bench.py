@@ -1,6 +1,7 @@
 """Benchmark: full v1 Bi-Real binary UNet forward, 32x32x120 patches, batch 1024.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024] [--no-cpu]
+                    [--headline-only | --cfg4-only]
 
 One step = one batched forward of `--batch` synthetic patches (seeded blob at
 base 16, x ~ N(0,1)) with the input already resident in HBM; K steps are
@@ -320,6 +321,65 @@ def cert_adversarial(torch, np, engine, blob, synth, td, sp, N, H, W):
     return res
 
 
+def bench_cfg4(sp, stream, td, reps4=5):
+    """Benchmark config 4: large tiles, 256 x 256 x 120, batch 64, base 32
+    (wide layers, 512 channels at the bottleneck): the forward's time per
+    step and every kernel's time by events."""
+    import torch
+
+    from bnns_to_c_amd import blob, engine, synth
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the int8 matrix-core conv takes the fold convs of 32-wide rows with at
+    # least 4 chunks of 64 input channels, the popcount kernel the rest
+    b4 = synth.make_blob(seed=0, base=32)
+    p4 = os.path.join(td, "bench_cfg4.blob")
+    blob.write(b4, p4)
+    eng4 = engine.Engine(p4)
+    N4, S4 = 64, 256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    x4 = torch.randn((N4, b4.n_bands, S4, S4), generator=gen, device="cuda", dtype=torch.float32)
+    y4 = torch.empty((N4, b4.n_classes, S4, S4), dtype=torch.float32, device="cuda")
+    settle(lambda: eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp), torch)
+    for _ in range(2):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps4):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    cfg4_ms = e0.elapsed_time(e1) / reps4
+    engine.prof_reset()
+    engine.prof_enable(True)
+    for _ in range(reps4):
+        eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
+    torch.cuda.synchronize()
+    engine.prof_enable(False)
+    agg4 = {}
+    for lab, op, ms, work in engine.prof_records():
+        a4 = agg4.setdefault(lab, [op, 0.0, 0, work])
+        a4[1] += ms
+        a4[2] += 1
+    cfg4_kern = []
+    for lab, (op, tot, cnt, work) in agg4.items():
+        us = tot / cnt * 1e3
+        k4 = {"label": lab, "op": op, "us": round(us, 2)}
+        if op.endswith("_mfma"):
+            k4["mac_s"] = round(work / (us / 1e6), 1)  # bit-MACs = int8 MACs
+            k4["frac_int8_peak"] = round(work / (us / 1e6) / PEAK_INT8_MACS, 4)
+        cfg4_kern.append(k4)
+    log(f"cfg4 256x256x120 b{N4} base 32: {cfg4_ms:.3f} ms/step, {N4 / cfg4_ms * 1e3:,.0f} patches/s")
+    for k4 in cfg4_kern:
+        extra = f"  {k4['frac_int8_peak']:.3f} of int8 peak" if "mac_s" in k4 else ""
+        log(f"  {k4['label']:10s} {k4['op']:16s} {k4['us']:9.1f} us{extra}")
+    eng4.close()
+    del x4, y4
+
+    return cfg4_ms, cfg4_kern, N4, p4, S4
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +392,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="the headline forward and its per-kernel pass only (for profiler runs)")
+    ap.add_argument("--cfg4-only", action="store_true",
+                    help="benchmark config 4 only, --steps timed forwards and as many with per-kernel events "
+                         "(for profiler runs); prints its own JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -343,6 +406,15 @@ def main() -> int:
     import torch
 
     from bnns_to_c_amd import blob, engine, synth
+
+    if args.cfg4_only:
+        stream = torch.cuda.Stream()
+        torch.cuda.set_stream(stream)
+        cfg4_ms, cfg4_kern, N4, _, _ = bench_cfg4(stream.cuda_stream, stream, tempfile.mkdtemp(), reps4=args.steps)
+        print(json.dumps({"config": "benchmark config 4: 256x256x120, batch 64, base 32", "ms_per_step": round(cfg4_ms, 4),
+                          "patches_s": round(N4 / cfg4_ms * 1e3, 1), "steps": args.steps, "kernels": cfg4_kern}),
+              flush=True)
+        return 0
 
     N, H, W = args.batch, 32, 32
     b = synth.make_blob(seed=0, base=16)
@@ -422,55 +494,7 @@ def main() -> int:
             f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
         L.close()
 
-        # benchmark config 4: large tiles, 256 x 256 x 120, batch 64, base 32
-        # (wide layers, 512 channels at the bottleneck); the int8 matrix-core
-        # conv takes the binary convs with at least 4 chunks of 64 input
-        # channels, the popcount kernel the rest
-        b4 = synth.make_blob(seed=0, base=32)
-        p4 = os.path.join(td, "bench_cfg4.blob")
-        blob.write(b4, p4)
-        eng4 = engine.Engine(p4)
-        N4, S4 = 64, 256
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(4)
-        x4 = torch.randn((N4, b4.n_bands, S4, S4), generator=gen, device="cuda", dtype=torch.float32)
-        y4 = torch.empty((N4, b4.n_classes, S4, S4), dtype=torch.float32, device="cuda")
-        settle(lambda: eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp), torch)
-        for _ in range(2):
-            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-        torch.cuda.synchronize()
-        reps4 = 5
-        e0.record(stream)
-        for _ in range(reps4):
-            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        cfg4_ms = e0.elapsed_time(e1) / reps4
-        engine.prof_reset()
-        engine.prof_enable(True)
-        for _ in range(reps4):
-            eng4.forward_device(x4.data_ptr(), N4, S4, S4, y4.data_ptr(), sp)
-        torch.cuda.synchronize()
-        engine.prof_enable(False)
-        agg4 = {}
-        for lab, op, ms, work in engine.prof_records():
-            a4 = agg4.setdefault(lab, [op, 0.0, 0, work])
-            a4[1] += ms
-            a4[2] += 1
-        cfg4_kern = []
-        for lab, (op, tot, cnt, work) in agg4.items():
-            us = tot / cnt * 1e3
-            k4 = {"label": lab, "op": op, "us": round(us, 2)}
-            if op.endswith("_mfma"):
-                k4["mac_s"] = round(work / (us / 1e6), 1)  # bit-MACs = int8 MACs
-                k4["frac_int8_peak"] = round(work / (us / 1e6) / PEAK_INT8_MACS, 4)
-            cfg4_kern.append(k4)
-        log(f"cfg4 256x256x120 b{N4} base 32: {cfg4_ms:.3f} ms/step, {N4 / cfg4_ms * 1e3:,.0f} patches/s")
-        for k4 in cfg4_kern:
-            extra = f"  {k4['frac_int8_peak']:.3f} of int8 peak" if "mac_s" in k4 else ""
-            log(f"  {k4['label']:10s} {k4['op']:16s} {k4['us']:9.1f} us{extra}")
-        eng4.close()
-        del x4, y4
+        cfg4_ms, cfg4_kern, N4, p4, S4 = bench_cfg4(sp, stream, td)
 
         # benchmark config 3: a 956 x 684 x 120 scene (N(0,1) plus a per-band
         # offset U(-0.5, 0.5)) cut into 32 x 32 patches, 30 x 22 = 660 with the
