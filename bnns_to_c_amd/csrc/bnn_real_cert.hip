@@ -163,19 +163,16 @@ __device__ __forceinline__ float rows_sum(float x) {
   return __fadd_rn(f32_of(r32[0]), f32_of(r32[1]));
 }
 // the largest of the lanes' non-negative floats, as bits (which order as
-// unsigned integers), in every lane: across the halves and the 16-lane rows
-// by two permlane swaps, then within each row by rotation (DPP moves that
-// fold into the max), all in vector registers
+// unsigned integers): within each 16-lane row by rotation, then the four
+// rows through scalar registers
 __device__ __forceinline__ uint32_t wave_max_bits(float m) {
   uint32_t mb = bits_of(m);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(mb, mb, false, false);
-  mb = max((uint32_t)r32[0], (uint32_t)r32[1]);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-  mb = max((uint32_t)r16[0], (uint32_t)r16[1]);
-  mb = max(mb, dmov<0x128>(mb));  // row_ror:8
-  mb = max(mb, dmov<0x124>(mb));  // row_ror:4
-  mb = max(mb, dmov<0x122>(mb));  // row_ror:2
-  return max(mb, dmov<kRor1>(mb));
+  mb = max(mb, dpp<0x128, false>(mb, mb));  // row_ror:8
+  mb = max(mb, dpp<0x124, false>(mb, mb));  // row_ror:4
+  mb = max(mb, dpp<0x122, false>(mb, mb));  // row_ror:2
+  mb = max(mb, dpp<kRor1, false>(mb, mb));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)mb, 0), (uint32_t)__builtin_amdgcn_readlane((int)mb, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)mb, 32), (uint32_t)__builtin_amdgcn_readlane((int)mb, 48)));
 }
 // per-pixel value (pixel 2p + s in v[s]) plus its left and right neighbours
 // (HALO: lane 0's left and lane 15's right neighbour is h, the halo's)
@@ -379,9 +376,9 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
 
   issue(0);
 
-  // rolling state: acc[g][c] the partials of output rows yi (c0), yi + 1
-  // (cn) and yi - 1 (cp), ab / qr the window sums and Q of input rows yi,
-  // yi - 2 and yi - 1 in the same slots, moved down one slot per row step
+  // rolling state, indexed by row mod 3: acc[r % 3] the partial of output
+  // row r, ab[y % 3] / qr[y % 3] the window sums and Q of input row y.  The
+  // row loop is unrolled by three so that every index is a constant.
   cert_f32x4 acc[G][3][2];
   float ab[3][2], qr[3];
 #pragma unroll
@@ -392,25 +389,6 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     qr[k] = 0.0f;
   }
 
-  // an output row's bits are stored one row step late, after the next row's
-  // loads are issued: the wait for a row's loads at the top of a step (the
-  // vector memory counter also counts stores) then finds the store long
-  // done instead of waiting for the store just issued
-  bool pst = false;  // this lane has a word pending
-  uint32_t pw = 0;
-  size_t ppix = 0;
-  auto flush = [&]() __attribute__((always_inline)) {
-    if (pst) {
-      if constexpr (G == 2) {
-        a.out[ppix * cwo + grp] = pw;
-      } else {
-        uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + ppix * cwo) + grp * 2;
-        if (whole_word) *reinterpret_cast<uint32_t*>(dst) = pw;
-        else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)pw;
-      }
-    }
-  };
-
   uint32_t nund = 0;  // outputs this wave recomputed
   for (int yi = 0; yi <= H; ++yi) {
     constexpr int c0 = 0, cn = 1, cp = 2;  // yi % 3, (yi + 1) % 3, (yi - 1) % 3 after rotation
@@ -418,13 +396,10 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     // row yi landed, this wave's LDS traffic done, then every wave's
     wait_vm_lgkm<0>();
     block_barrier();
+    if (yi + 1 < H) issue(yi + 1);
 
     float abn[2] = {0.0f, 0.0f}, qn = 0.0f;
     if (has) {
-      // (the next row's loads, and the previous row's store, are issued
-      // after this row's reads: a wave waits at its loads while the CU's
-      // vector memory unit takes the block's other loads, and that wait now
-      // overlaps its reads' latency)
       const float* row = cert_lds + (size_t)(yi % kCertRing) * rb / 4;
       float xv[2][8];
 #pragma unroll
@@ -446,8 +421,6 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
           hx[j] = ok ? (p == 0 ? v.x : v.y) : 0.0f;
         }
       }
-      if (yi + 1 < H) issue(yi + 1);
-      flush();
       // the wave's largest |x| (max ignores a NaN, which reaches v' and A as
       // NaN)
       float m = 0.0f, as[2] = {0.0f, 0.0f}, ash = 0.0f;
@@ -565,7 +538,6 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     ab[c0][1] = abn[1];
     qr[c0] = qn;
 
-    if (!has) flush();
     if (yi >= 1) {
       // output row r = yi - 1 is complete in acc[g][cp]: each wave leaves its
       // partials, its window sum of |x| (rows yi - 2, yi - 1, yi) and its
@@ -587,23 +559,22 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
       block_barrier();
 
-      // finalize: the four partials in wave order (the sums start from wave
-      // 0's term; only the sign of a zero v' can differ from starting at +0,
-      // and no comparison below sees it)
-      float v[G][2], Aw[2];
+      // finalize: the four partials in wave order
+      float v[G][2], Aw[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const float2 u = *reinterpret_cast<const float2*>(&absw[w * 32 + fpx0]);
-        Aw[0] = w ? __fadd_rn(Aw[0], u.x) : u.x;
-        Aw[1] = w ? __fadd_rn(Aw[1], u.y) : u.y;
+        Aw[0] = __fadd_rn(Aw[0], u.x);
+        Aw[1] = __fadd_rn(Aw[1], u.y);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
+        v[g][0] = v[g][1] = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const float t0 = opart[(g * 4 + w) * 512 + i0], t1 = opart[(g * 4 + w) * 512 + i0 + 256];
-          v[g][0] = w ? __fadd_rn(v[g][0], t0) : t0;
-          v[g][1] = w ? __fadd_rn(v[g][1], t1) : t1;
+          v[g][0] = __fadd_rn(v[g][0], t0);
+          v[g][1] = __fadd_rn(v[g][1], t1);
         }
       }
       const float4 qq = *reinterpret_cast<const float4*>(qw);
@@ -740,19 +711,24 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       }
       }
 
-      // lane (channel k, row group fq), k < 2, holds pixel fpx0 + k for the
-      // next step's store: its 16 bits of the group (G = 1), or the whole
-      // word of both groups
-      pst = fc < 2 && fpx0 + fc < vhi;
-      if (pst) {
-        ppix = (size_t)n * H * W + (size_t)r * W + wx0 + fpx0 + fc;
-        const uint32_t w0 = (uint32_t)((fc ? bm[0][1] : bm[0][0]) >> (16 * fq)) & 0xFFFFu;
-        pw = G == 2 ? w0 | (((uint32_t)((fc ? bm[G - 1][1] : bm[G - 1][0]) >> (16 * fq)) & 0xFFFFu) << 16) : w0;
+      // lane (channel k, row group fq), k < 2, stores pixel fpx0 + k: its
+      // 16 bits of the group (G = 1), or the whole word of both groups
+      if (fc < 2 && fpx0 + fc < vhi) {
+        const int HW = H * W;
+        const size_t pix = (size_t)n * HW + (size_t)r * W + wx0 + fpx0 + fc;
+        if constexpr (G == 2) {
+          const uint32_t w0 = (uint32_t)((fc ? bm[0][1] : bm[0][0]) >> (16 * fq)) & 0xFFFFu;
+          const uint32_t w1 = (uint32_t)((fc ? bm[1][1] : bm[1][0]) >> (16 * fq)) & 0xFFFFu;
+          a.out[pix * cwo + grp] = w0 | (w1 << 16);
+        } else {
+          const uint32_t word = (uint32_t)((fc ? bm[0][1] : bm[0][0]) >> (16 * fq)) & 0xFFFFu;
+          uint8_t* dst = reinterpret_cast<uint8_t*>(a.out + pix * cwo) + grp * 2;
+          if (whole_word) *reinterpret_cast<uint32_t*>(dst) = word;
+          else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)word;
+        }
       }
     }
-    // next step: output rows yi + 1 and yi, input rows yi - 1 and yi (the
-    // moves cost less than a loop unrolled by three, whose code outgrows the
-    // instruction cache)
+    // next step: output rows yi + 1 and yi, input rows yi - 1 and yi
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -766,7 +742,6 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     qr[cn] = qr[cp];
     qr[cp] = qr[c0];
   }
-  flush();
   if (a.ucnt && nund && lane == 0) atomicAdd(a.ucnt, (unsigned long long)nund);
 }
 
