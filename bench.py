@@ -490,8 +490,13 @@ def main() -> int:
         pool_ms = e0.elapsed_time(e1) / reps
         pool_bitmacs = N * C * H * W * C * 9
         pool_rate = 2 * pool_bitmacs / (pool_ms / 1e3)
-        log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, "
-            f"frac {pool_rate / valu_binop_peak():.3f} of VALU popcount peak")
+        # this shape (cout 128, 32-wide rows) is inside the int8 matrix-core
+        # rule unless BNN_BCONV_MFMA=0 keeps the popcount kernel; the
+        # fraction is of the path's own peak
+        pool_mfma = os.environ.get("BNN_BCONV_MFMA") != "0"
+        pool_frac = pool_bitmacs / (pool_ms / 1e3) / PEAK_INT8_MACS if pool_mfma else pool_rate / valu_binop_peak()
+        pool_peak = "int8 matrix peak" if pool_mfma else "VALU popcount peak"
+        log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, frac {pool_frac:.3f} of {pool_peak}")
         L.close()
 
         cfg4_ms, cfg4_kern, N4, p4, S4 = bench_cfg4(sp, stream, td)
@@ -850,11 +855,13 @@ def main() -> int:
                      "hbm_frac": round(c1_bytes / (c1_ms / 1e3) / PEAK_HBM, 4)},
             "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
                            "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
-                           "frac": round(pool_rate / valu_binop_peak(), 4)},
+                           "kernel": "k_bconv_mfma (int8 matrix cores)" if pool_mfma else "k_bconv (VALU popcount)",
+                           "frac": round(pool_frac, 4), "frac_of": pool_peak},
             "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
                      "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
                      "kernels": cfg4_kern,
-                     "int8_mfma_rule": "fold convs of 32-wide rows with >= 4 chunks of 64 input channels (dec4.c1, dec4.c2 here)"},
+                     "int8_mfma_rule": "fold and pool convs with cout % 64 == 0 and rows 16 to 64 wide "
+                                       "(enc3.c1 .. dec3.c2 here)"},
             "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
                                 "past the scene), benchmark config 3",
                       "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),

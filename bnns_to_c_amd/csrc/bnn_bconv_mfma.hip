@@ -7,6 +7,7 @@
 // (-mllvm -amdgpu-mfma-vgpr-form): with AGPR accumulators the compiler
 // copies the 64 accumulator registers through VGPRs on every K step.
 #include <algorithm>
+#include <atomic>
 
 #include "bnn_device.h"
 #include "bnn_kernels.h"
@@ -32,7 +33,14 @@ namespace {
 // padded to 128 bytes mod 256, so the 16 lanes of a group (16 pixels of one
 // row) read distinct banks.  Two buffers: chunk c + 1 is expanded and stored
 // while chunk c is consumed, and its words are loaded from HBM one chunk
-// earlier.  A comes straight from the weight table, two K steps ahead.
+// earlier.  A (the same for the block's four waves) goes through LDS too:
+// each K step's 64 channels x 64 bytes are loaded once per block (16 bytes
+// a thread, two steps ahead of their use) into a ring of three slots, one
+// barrier per K step, and each wave reads the next step's A from its slot
+// while the current step's matrix ops run.  (Read straight from the weight
+// table by every wave, A was the layer's bottleneck: the four waves'
+// identical 4 KB per K step through the vector L1 held the matrix cores
+// near a fifth of their rate.)
 //
 // One K step (64) is one tap of one chunk: lane group q = lane / 16 takes
 // word q / 2 of the chunk, channels 16 * (q % 2) .. +15 of it, in A and B
@@ -68,6 +76,11 @@ __device__ __forceinline__ int32_t max_pair(int32_t x) {
 
 constexpr int kSlot = 80;     // LDS bytes per staged pixel
 constexpr int kStageMax = 2;  // staged pixels per thread and chunk
+// A ring: 3 slots of 64 channels x 80 bytes (64 of weights, 16 of padding,
+// so a read's 16 lanes of one 16-byte column hit distinct banks)
+constexpr int kArow = 80;
+constexpr uint32_t kAslot = 64 * kArow;
+constexpr uint32_t kAring = 3 * kAslot;
 
 struct MfmaTile {
   int lw, ltr, lti;     // log2 of W, of rows per patch in a tile (min(TR, H)), of patches per tile
@@ -172,16 +185,25 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
     }
   };
 
-  // ---- A: weight bytes of channel co0 + j (+16 m), pair 2 * st + q / 2, half h
-  auto a_base = [&](uint32_t it) {
-    return (uint32_t)((((int)(it % (uint32_t)ncot) * 64 + j) * T.npair + (q >> 1)) * 32 + 16 * h);
+  // ---- A: each thread stages 16 bytes of a K step's 64 x 64 weight
+  // bytes: channel ac = tid / 4 of the item's group, bytes 16 * (tid % 4);
+  // the table row of channel co, K step st is 64 bytes at (co * npair + 2 st) * 32
+  const int ac = tid >> 2, ap = tid & 3;
+  auto a_piece = [&](uint32_t itm, int st) {
+    return (uint32_t)((((int)(itm % (uint32_t)ncot) * 64 + ac) * T.npair + 2 * st) * 32 + 16 * ap);
   };
-  const uint32_t mstride = (uint32_t)T.npair * 512u;
-  auto loadA = [&](uint32_t base, int st, i32x4v (&A)[4]) {
+  auto a_load = [&](uint32_t itm, int st) {
+    return __builtin_bit_cast(i32x4v, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)a_piece(itm, st), 0, 0));
+  };
+  const uint32_t aring = 2 * bufb;  // the ring after the two staging buffers
+  auto a_store = [&](uint32_t slot, const i32x4v& v) {
+    *reinterpret_cast<i32x4v*>(smem + aring + slot * kAslot + (uint32_t)(ac * kArow + 16 * ap)) = v;
+  };
+  // the wave's operand A[m] (channel 16 m + j, K bytes 16 q ..) from a slot
+  auto a_read = [&](uint32_t slot, i32x4v (&A)[4]) {
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-      A[m] = __builtin_bit_cast(i32x4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rw, (int)(base + (uint32_t)m * mstride + (uint32_t)st * 64u), 0, 0));
+      A[m] = *reinterpret_cast<const i32x4v*>(smem + aring + slot * kAslot + (uint32_t)((16 * m + j) * kArow + 16 * q));
   };
 
   i32x4v acc[4][4];
@@ -222,50 +244,55 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
   };
   advance();
   if (lok) stage_load(lit, lc);
-  uint32_t abase = a_base(it);
-  i32x4v Aa[4], A1[4];
-  loadA(abase, 0, Aa);
-  if (T.nch * 9 > 1) loadA(abase, 1, A1);
-  else loadA(a_base(item_of(li + nslot)), 0, A1);
+  // the K steps of the block's items run as one sequence: step S (item
+  // steps st = c * 9 + t) takes A from slot S % 3; at its start (a barrier)
+  // A of step S + 1 is visible and slot (S + 2) % 3 is free
+  const int nst = T.nch * 9;  // K steps per item
+  auto a_load_ahead = [&](int st) {  // A of in-item step st, or of the next item past its end
+    return st < nst ? a_load(it, st) : a_load(item_of(li + nslot), st - nst);
+  };
+  a_store(0, a_load(it, 0));
+  a_store(1, a_load_ahead(1));
+  i32x4v ag = a_load_ahead(2);  // A of step S + 2, stored during step S
   __syncthreads();
+  i32x4v Ar[4];
+  a_read(0, Ar);
+  uint32_t S = 0;
   int buf = 0;
 #pragma unroll 1
   for (;;) {
 #pragma unroll 1
     for (int c = 0; c < T.nch; ++c) {
-      const bool last = c + 1 == T.nch;
       const uint32_t bo = (uint32_t)buf * bufb;
 #pragma unroll
       for (int t = 0; t < 9; ++t) {
         const int ky = t / 3, kx = t % 3;
-        // the K step two ahead: this item's, or the next item's first two
+        __syncthreads();
+        const uint32_t s0 = S % 3u, s1 = s0 == 2u ? 0u : s0 + 1u, s2 = s1 == 2u ? 0u : s1 + 1u;
         i32x4v An[4];
-        const int s2 = c * 9 + t + 2;
-        if (s2 < T.nch * 9) loadA(abase, s2, An);
-        else loadA(a_base(item_of(li + nslot)), s2 - T.nch * 9, An);
+        a_read(s1, An);
         const uint32_t dt = bo + (uint32_t)((ky - 1) * T.rs + (kx - 1) * kSlot);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const i32x4v B = *reinterpret_cast<const i32x4v*>(smem + lb[g] + dt);
 #pragma unroll
-          for (int m = 0; m < 4; ++m) acc[m][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aa[m], B, acc[m][g], 0, 0, 0);
+          for (int m = 0; m < 4; ++m) acc[m][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Ar[m], B, acc[m][g], 0, 0, 0);
         }
+        // A of step S + 2 into its slot, the load of step S + 3
+        a_store(s2, ag);
+        ag = a_load_ahead(c * 9 + t + 3);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          Aa[m] = A1[m];
-          A1[m] = An[m];
-        }
+        for (int m = 0; m < 4; ++m) Ar[m] = An[m];
+        ++S;
       }
-      // the next chunk into the other buffer, the one after it from HBM
+      // the next chunk into the other buffer (visible after the next step's
+      // barrier), the one after it from HBM
       if (lok) {
         stage_store(buf ^ 1);
         advance();
         if (lok) stage_load(lit, lc);
       }
-      if (!last) {
-        __syncthreads();
-        buf ^= 1;
-      }
+      buf ^= 1;
     }
     // ---------------------------------------------------------- epilogue --
     // one group of 16 channels at a time: P, the rule, and the gather into
@@ -347,9 +374,6 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int g = 0; g < 4; ++g) acc[m][g] = i32x4v{0, 0, 0, 0};
-    abase = a_base(it);
-    __syncthreads();
-    buf ^= 1;
   }
 }
 
@@ -357,7 +381,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 
 // The tile of a (H, W) layer: TR = 256 / W rows of a patch, or 256 / (H W)
 // whole patches; false when the shape has no such tile or its two staging
-// buffers exceed 64 KB of LDS.
+// buffers exceed 64 KB of LDS (with the A ring, under 80 KB: two blocks a CU).
 static bool mfma_tile(int H, int W, int epi, MfmaTile* T) {
   if (W < 8 || W > 64 || (W & (W - 1)) || H <= 0) return false;
   if (epi == EPI_POOL && (H & 1)) return false;
@@ -422,26 +446,33 @@ hipError_t launch_bconv_mfma(const BconvArgs& a, const MfmaConv& mc, int epi, bo
   T.ntiles = (uint32_t)ntiles;
   const uint32_t b0 = (uint32_t)(npix * a.cw0 * 4);
   const uint32_t b1 = a.in1 ? (uint32_t)((size_t)a.N * a.h1 * a.w1 * a.cw1 * 4) : 0u;
-  const size_t lds = (size_t)2 * ((size_t)T.ps << T.lti);
+  const size_t lds = (size_t)2 * ((size_t)T.ps << T.lti) + kAring;
+  // more than 64 KB of LDS: allowed once per variant and device (bit d of
+  // the variant's mask for device d)
+  using Fn = void (*)(const BconvArgs, const int8_t*, const int32_t*, const MfmaTile, uint32_t, uint32_t);
+  static const Fn fns[4] = {k_bconv_mfma<EPI_FOLD, false>, k_bconv_mfma<EPI_FOLD, true>, k_bconv_mfma<EPI_POOL, false>,
+                            k_bconv_mfma<EPI_POOL, true>};
+  static std::atomic<uint64_t> attr[4];
+  const int var = (epi == EPI_POOL ? 2 : 0) + (dump ? 1 : 0);
   // as many blocks as fit on the chip at once (LDS, and three waves per
   // SIMD by registers), each walking items blockIdx.x, + gridDim.x, ...
   int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr[var].load(std::memory_order_acquire) & bit)) {
+    if (hipError_t e = hipFuncSetAttribute((const void*)fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        e != hipSuccess)
+      return e;
+    attr[var].fetch_or(bit, std::memory_order_acq_rel);
+  }
   const size_t per_cu = std::min<size_t>(3, (160 * 1024) / lds);
   const size_t items = ntiles * (size_t)(a.cout / 64);
   if (items >= 0xFFFFFFFFull) return hipErrorInvalidValue;
   // (a multiple of 8 blocks for the XCD-aware item order; blocks without
   // an item exit)
   const dim3 grid((unsigned)((std::min<size_t>(items, per_cu * cus) + 7) / 8 * 8));
-  if (epi == EPI_POOL) {
-    if (dump) hipLaunchKernelGGL((k_bconv_mfma<EPI_POOL, true>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
-    else hipLaunchKernelGGL((k_bconv_mfma<EPI_POOL, false>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
-  } else {
-    if (dump) hipLaunchKernelGGL((k_bconv_mfma<EPI_FOLD, true>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
-    else hipLaunchKernelGGL((k_bconv_mfma<EPI_FOLD, false>), grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
-  }
+  hipLaunchKernelGGL(fns[var], grid, dim3(256), lds, s, a, mc.w, mc.s, T, b0, b1);
   return hipGetLastError();
 }
 

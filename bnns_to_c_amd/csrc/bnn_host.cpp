@@ -346,13 +346,11 @@ FoldHost canon_fold(const Act& a, int coutp) {
 }
 
 // Which binary convs run on the int8 matrix cores (same results as the
-// popcount kernel either way).  By default a fold or pool conv with
-// cout % 64 == 0, an image tile that fits (mfma_conv_fits) and at least 4
-// chunks of 64 input channels: measured per layer in whole forwards, the
-// matrix-core kernel is 6-20 % faster there and slower with fewer chunks,
-// where its per-tile staging and epilogue dominate.  BNN_BCONV_MFMA=0 keeps
-// every conv on the popcount kernel, =2 takes the matrix cores wherever
-// they fit (both read when a model or layer is created).
+// popcount kernel either way): by default a fold or pool conv with
+// cout % 64 == 0, an image tile that fits (mfma_conv_fits) and rows at least
+// 16 wide (use_mfma).  BNN_BCONV_MFMA=0 keeps every conv on the popcount
+// kernel, =2 takes the matrix cores wherever they fit (both read when a
+// model or layer is created).
 int mfma_conv_mode() {
   const char* e = getenv("BNN_BCONV_MFMA");
   if (e && !strcmp(e, "0")) return 0;
@@ -408,17 +406,18 @@ bool cert_mode() {
   return !(e && !strcmp(e, "0"));
 }
 
-// The int8 matrix-core conv by default only where whole forwards measure
-// it faster than the popcount kernel: fold layers of 32-wide rows (tiles of
-// eight whole rows) with at least 4 input chunks of 64 channels.  In
-// config 4 (256 x 256, base 32) that is dec4.c1 and dec4.c2: forward
-// 2.767-2.772 ms against 2.780-2.786 with the popcount kernel everywhere
-// and 2.800-2.809 when every fold or pool layer of 4+ chunks took it
-// (dec3.c1 at 64-wide rows 9% slower, the pool layers and the 16 x 16
-// bottleneck 3-5% slower).  BNN_BCONV_MFMA=2 takes it wherever it fits.
+// The int8 matrix-core conv by default where whole forwards measure it
+// faster than the popcount kernel: every fold or pool layer that fits with
+// rows of 16 to 64 pixels.  Config 4 (256 x 256, base 32: ten such layers
+// at 64, 32 and 16 wide) 2.44 ms against 2.79 with the popcount kernel
+// everywhere (dec4.c1 119 against 223 us); the isolated 128 -> 128 pool
+// layer at 32 x 32 (benchmark config 2) 210 against 288 us.  At 8 x 8 (the
+// headline's level 2 when its layers run one by one) a tile's staging and
+// epilogue outweigh its one to three input chunks: enc3.c1 15 against 8 us,
+// forward 0.342 against 0.320 ms.  BNN_BCONV_MFMA=2 takes it wherever it
+// fits.
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
-  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) &&
-         (L.mfma == 2 || (mfma_nchunk(L.cw0, L.cw1) >= 4 && W == 32 && epi == EPI_FOLD));
+  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || W >= 16);
 }
 
 struct Workspace {

@@ -77,8 +77,8 @@ def test_forced_mfma_stages_vs_checker(tmp_path, orc, monkeypatch, seed, base, N
 
 
 def test_default_rule_picks_wide_layers(tmp_path, orc, monkeypatch):
-    """Default: the matrix cores for fold layers of 32-wide rows with >= 4
-    input chunks of 64 channels."""
+    """Default: the matrix cores for fold and pool layers with cout % 64 == 0
+    and rows 16 to 64 wide."""
     monkeypatch.delenv("BNN_BCONV_MFMA", raising=False)
     b = synth.make_blob(seed=26, base=32)
     p = tmp_path / "m.blob"
@@ -86,9 +86,10 @@ def test_default_rule_picks_wide_layers(tmp_path, orc, monkeypatch):
     eng = E.Engine(str(p))
     x = synth.make_input(126, 1, 120, 128, 128)
     ops = _ops(eng, x)
-    # base 32 at 128x128: level 2 is 32 wide; dec3.c1 reads 128 + 256
-    # channels there (6 chunks), dec3.c2 128 (2 chunks), enc3.c2 pools
-    want = {"dec3.c1"}
+    # base 32 at 128x128: levels 1, 2, 3 are 64, 32 and 16 wide with 64,
+    # 128 and 256 channels; level 0 (128 wide, 32 channels) and the 8 x 8
+    # bottleneck stay on the popcount kernel
+    want = {f"{lv}.c{k}" for lv in ("enc2", "enc3", "enc4", "dec4", "dec3", "dec2") for k in (1, 2)}
     got = {lab for lab, op in ops.items() if op.endswith("_mfma")}
     assert got == want, (got, ops)
     _check_stages(eng, orc.parse(B.to_bytes(b)), x)
