@@ -860,8 +860,8 @@ def main() -> int:
             "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
                      "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
                      "kernels": cfg4_kern,
-                     "int8_mfma_rule": "fold and pool convs with cout % 64 == 0 and rows 16 to 64 wide "
-                                       "(enc3.c1 .. dec3.c2 here)"},
+                     "int8_mfma_rule": "fold and pool convs with cout % 64 == 0, rows at least 16 wide and "
+                                       "64+ input channels (enc2.c2 .. dec2.c2 here)"},
             "scene": {"config": f"{SH}x{SW}x{b.n_bands} cube, {PS}x{PS} patches ({npatch}, edge patches zero "
                                 "past the scene), benchmark config 3",
                       "device_ms": round(scene_dev_ms, 4), "device_patches_s": round(npatch / scene_dev_ms * 1e3, 1),

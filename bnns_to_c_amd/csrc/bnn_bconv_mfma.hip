@@ -22,8 +22,9 @@ namespace {
 // the A operand: int8 +-1 weights) x one tile of 256 output pixels (each
 // wave 4 groups of 16, the B operand: activation bits as 0/1 bytes) with
 // v_mfma_i32_16x16x64_i8; P = 2*D - S[border class][co] (bnn_kernels.h).
-// A tile is TR whole rows of one patch (a patch of TR rows or more) or TI
-// whole patches (smaller patches), TR * W = 256 with W a power of two.
+// A tile is TR rows of TW columns of one patch (a patch of TR rows or more)
+// or TI whole patches (smaller patches), TR * TW = 256: TW = W for rows up
+// to 64 wide (whole rows), 32 for wider ones (W a power of two).
 //
 // B comes from LDS: for each chunk of two activation words the block stages
 // the tile's rows with a one-pixel halo, (TR + 2) x (W + 2) pixels per patch,
@@ -83,8 +84,9 @@ constexpr uint32_t kAslot = 64 * kArow;
 constexpr uint32_t kAring = 3 * kAslot;
 
 struct MfmaTile {
-  int lw, ltr, lti;     // log2 of W, of rows per patch in a tile (min(TR, H)), of patches per tile
-  int hpt;              // tiles per patch (H / TR), 1 for multi-patch tiles
+  int lw, ltr, lti;     // log2 of TW, of rows per patch in a tile (min(TR, H)), of patches per tile
+  int lcw;              // log2 of tiles across a row (W / TW)
+  int hpt;              // tiles per patch (H / TR * W / TW), 1 for multi-patch tiles
   int rs, ps;           // LDS bytes per staged row, per staged patch
   FastDiv dps, drow;    // staged pixels per patch, per row
   int ns;               // staged pixels per chunk buffer
@@ -114,12 +116,12 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
     if (EPI == EPI_POOL) {
       // block 8 * (group pair) + j / 2 of the wave's 16, row g % 2 of it
       const int blk = 16 * wave + 8 * (g >> 1) + (j >> 1);
-      const int bx = blk & ((W >> 1) - 1), br = blk >> (T.lw - 1);  // block row within the tile
+      const int bx = blk & ((1 << (T.lw - 1)) - 1), br = blk >> (T.lw - 1);  // block row within the tile
       l = ((2 * br + (g & 1)) << T.lw) + 2 * bx + (j & 1);
     } else {
       l = 64 * wave + 16 * g + j;
     }
-    px[g] = l & (W - 1);
+    px[g] = l & ((1 << T.lw) - 1);
     const int r = l >> T.lw;
     py[g] = r & ((1 << T.ltr) - 1);
     pi[g] = r >> T.ltr;
@@ -136,14 +138,18 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
   const __amdgpu_buffer_rsrc_t r1 = make_rsrc(a.in1 ? a.in1 : a.in0, bytes1);
   const uint32_t cw0b = (uint32_t)a.cw0 * 4u, cw1b = (uint32_t)a.cw1 * 4u;
   // item it: tile it / ncot (patches n0 .. n0 + 2^lti - 1, rows y0 ..
-  // y0 + 2^ltr - 1), output channels 64 * (it % ncot) ..
+  // y0 + 2^ltr - 1
+  // (columns x0 .. x0 + TW - 1), output channels 64 * (it % ncot) ..
   auto tile_n0 = [&](uint32_t it) { return (int)((it / (uint32_t)ncot) / (uint32_t)T.hpt) << T.lti; };
-  auto tile_y0 = [&](uint32_t it) { return (int)((it / (uint32_t)ncot) % (uint32_t)T.hpt) << T.ltr; };
+  auto tile_y0 = [&](uint32_t it) { return (int)(((it / (uint32_t)ncot) % (uint32_t)T.hpt) >> T.lcw) << T.ltr; };
+  auto tile_x0 = [&](uint32_t it) {
+    return (int)(((it / (uint32_t)ncot) % (uint32_t)T.hpt) & ((1u << T.lcw) - 1u)) << T.lw;
+  };
 
   // ---- staging: the two words of chunk c of item it for this thread's staged pixels
   uint32_t sw[kStageMax][2];
   auto stage_load = [&](uint32_t it, int c) {
-    const int n0 = tile_n0(it), y0 = tile_y0(it);
+    const int n0 = tile_n0(it), y0 = tile_y0(it), x0 = tile_x0(it);
     const bool s1 = c >= T.nc0;
     const int wd = 2 * (s1 ? c - T.nc0 : c);
     const bool two = wd + 1 < (s1 ? a.cw1 : a.cw0);
@@ -151,7 +157,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
     for (int k = 0; k < kStageMax; ++k) {
       const uint32_t i = (uint32_t)(tid + 256 * k);
       const uint32_t ip = fdiv(i, T.dps), ir = i - ip * T.dps.d, rr = fdiv(ir, T.drow), cc = ir - rr * T.drow.d;
-      const int n = n0 + (int)ip, y = y0 + (int)rr - 1, x = (int)cc - 1;
+      const int n = n0 + (int)ip, y = y0 + (int)rr - 1, x = x0 + (int)cc - 1;
       bool ok = i < (uint32_t)T.ns && n < a.N && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
       uint32_t off;
       if (!s1) {
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
     // one group of 16 channels at a time: P, the rule, and the gather into
     // 16-bit halves of the output words; then the word stores
     {
-      const int n0 = tile_n0(it), y0 = tile_y0(it);
+      const int n0 = tile_n0(it), y0 = tile_y0(it), x0 = tile_x0(it);
       const int co0 = (int)(it % (uint32_t)ncot) * 64;
       const int HW = H * W;
       const int Hh = H >> 1, Wh = W >> 1;
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
       size_t pix[4];  // global pixel index
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int y = y0 + py[g], x = px[g];
+        const int y = y0 + py[g], x = x0 + px[g];
         pv[g] = n0 + pi[g] < a.N;
         cls[g] = ((y == 0 ? 1 : 0) | (y == H - 1 ? 2 : 0)) * 4 + ((x == 0 ? 1 : 0) | (x == W - 1 ? 2 : 0));
         pix[g] = ((size_t)(n0 + pi[g]) * H + y) * W + x;
@@ -327,7 +333,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
           for (int r = 0; r < 4; ++r) {
             P[g][r] = 2 * acc[m][g][r] - sv[r];
             nib |= ((uint32_t)P[g][r] - (uint32_t)lo1[r] < (uint32_t)wd1[r] ? 1u : 0u) << r;
-            if (DUMP && pv[g]) a.P[((size_t)(n0 + pi[g]) * a.cout + cb + r) * HW + (size_t)(y0 + py[g]) * W + px[g]] = P[g][r];
+            if (DUMP && pv[g]) a.P[((size_t)(n0 + pi[g]) * a.cout + cb + r) * HW + (size_t)(y0 + py[g]) * W + x0 + px[g]] = P[g][r];
           }
           half[m][g] = or_groups(nib << (4 * q));
         }
@@ -343,7 +349,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
               nib2 |= ((uint32_t)pm - (uint32_t)lo2[r] < (uint32_t)wd2[r] ? 1u : 0u) << r;
               if (DUMP && pv[2 * p] && (j & 1) == 0)
                 a.P2[((size_t)(n0 + pi[2 * p]) * a.cout + cb + r) * Hh * Wh + (size_t)((y0 + py[2 * p]) >> 1) * Wh +
-                     (px[2 * p] >> 1)] = pm;
+                     ((x0 + px[2 * p]) >> 1)] = pm;
             }
             half2[m][p] = or_groups(nib2 << (4 * q));
           }
@@ -361,7 +367,7 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
         for (int p = 0; p < 2; ++p) {
           if (pv[2 * p] && (j & 1) == 0 && q < 2) {
             const uint32_t word = q == 0 ? (half2[0][p] | half2[1][p] << 16) : (half2[2][p] | half2[3][p] << 16);
-            const size_t dp = ((size_t)(n0 + pi[2 * p]) * Hh + ((y0 + py[2 * p]) >> 1)) * Wh + (px[2 * p] >> 1);
+            const size_t dp = ((size_t)(n0 + pi[2 * p]) * Hh + ((y0 + py[2 * p]) >> 1)) * Wh + ((x0 + px[2 * p]) >> 1);
             a.out2[dp * a.cwo + (co0 >> 5) + q] = word;
           }
         }
@@ -379,26 +385,29 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 
 }  // namespace
 
-// The tile of a (H, W) layer: TR = 256 / W rows of a patch, or 256 / (H W)
-// whole patches; false when the shape has no such tile or its two staging
-// buffers exceed 64 KB of LDS (with the A ring, under 80 KB: two blocks a CU).
+// The tile of a (H, W) layer: TR = 256 / TW rows of TW columns of a patch
+// (TW = W up to 64 wide, else 32), or 256 / (H W) whole patches; false when
+// the shape has no such tile or its two staging buffers exceed 64 KB of LDS
+// (with the A ring, under 80 KB: two blocks a CU).
 static bool mfma_tile(int H, int W, int epi, MfmaTile* T) {
-  if (W < 8 || W > 64 || (W & (W - 1)) || H <= 0) return false;
+  if (W < 8 || (W & (W - 1)) || W > (1 << 20) || H <= 0) return false;
   if (epi == EPI_POOL && (H & 1)) return false;
-  const int TR = 256 / W;
-  int ltr = 0, lti = 0, hpt = 1;
+  const int TW = W > 64 ? 32 : W;
+  const int TR = 256 / TW;
+  int ltr = 0, lti = 0, hpt = 1, lcw = 0;
+  while ((TW << lcw) < W) ++lcw;
   if (H >= TR) {
     if (H % TR) return false;
-    hpt = H / TR;
+    hpt = (H / TR) << lcw;
     while ((1 << ltr) < TR) ++ltr;
   } else {
-    if (TR % H || (H & (H - 1))) return false;
+    if (TW != W || TR % H || (H & (H - 1))) return false;
     while ((1 << ltr) < H) ++ltr;
     while ((1 << lti) < TR / H) ++lti;
   }
   int lw = 0;
-  while ((1 << lw) < W) ++lw;
-  const int rows = (1 << ltr) + 2, cols = W + 2;
+  while ((1 << lw) < TW) ++lw;
+  const int rows = (1 << ltr) + 2, cols = TW + 2;
   int rs = cols * kSlot;
   rs += (128 - rs % 256 + 256) % 256;  // rows 128 bytes apart mod 256
   int ps = rows * rs;
@@ -410,7 +419,7 @@ static bool mfma_tile(int H, int W, int epi, MfmaTile* T) {
   const int ns = (rows * cols) << lti;
   if (ns > 256 * kStageMax) return false;
   if (T) {
-    T->lw = lw; T->ltr = ltr; T->lti = lti; T->hpt = hpt;
+    T->lw = lw; T->ltr = ltr; T->lti = lti; T->lcw = lcw; T->hpt = hpt;
     T->rs = rs; T->ps = ps;
     T->dps = make_fastdiv((uint32_t)(rows * cols));
     T->drow = make_fastdiv((uint32_t)cols);

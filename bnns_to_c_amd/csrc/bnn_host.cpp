@@ -347,8 +347,8 @@ FoldHost canon_fold(const Act& a, int coutp) {
 
 // Which binary convs run on the int8 matrix cores (same results as the
 // popcount kernel either way): by default a fold or pool conv with
-// cout % 64 == 0, an image tile that fits (mfma_conv_fits) and rows at least
-// 16 wide (use_mfma).  BNN_BCONV_MFMA=0 keeps every conv on the popcount
+// cout % 64 == 0, an image tile that fits (mfma_conv_fits), rows at least 16
+// wide and 64 or more input channels (use_mfma).  BNN_BCONV_MFMA=0 keeps every conv on the popcount
 // kernel, =2 takes the matrix cores wherever they fit (both read when a
 // model or layer is created).
 int mfma_conv_mode() {
@@ -408,16 +408,18 @@ bool cert_mode() {
 
 // The int8 matrix-core conv by default where whole forwards measure it
 // faster than the popcount kernel: every fold or pool layer that fits with
-// rows of 16 to 64 pixels.  Config 4 (256 x 256, base 32: ten such layers
-// at 64, 32 and 16 wide) 2.44 ms against 2.79 with the popcount kernel
-// everywhere (dec4.c1 119 against 223 us); the isolated 128 -> 128 pool
-// layer at 32 x 32 (benchmark config 2) 210 against 288 us.  At 8 x 8 (the
-// headline's level 2 when its layers run one by one) a tile's staging and
-// epilogue outweigh its one to three input chunks: enc3.c1 15 against 8 us,
-// forward 0.342 against 0.320 ms.  BNN_BCONV_MFMA=2 takes it wherever it
-// fits.
+// rows at least 16 pixels wide and at least two input words (a 64-channel
+// K chunk filled).  Config 4 (256 x 256, base 32: thirteen such layers at
+// 128, 64, 32 and 16 wide) 2.34 ms against 2.79 with the popcount kernel
+// everywhere (dec4.c1 116 against 223 us, dec2.c1 130 against 190); the
+// isolated 128 -> 128 pool layer at 32 x 32 (benchmark config 2) 210
+// against 288 us.  A 32-channel input fills half a chunk (config 4's
+// enc2.c1: 61 against 46 us), and at 8 x 8 (the headline's level 2 when its
+// layers run one by one) a tile's staging and epilogue outweigh its one to
+// three chunks (enc3.c1 15 against 8 us, forward 0.342 against 0.320 ms).
+// BNN_BCONV_MFMA=2 takes it wherever it fits.
 bool use_mfma(const DevBconv& L, int epi, int H, int W) {
-  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || W >= 16);
+  return L.mc.w && mfma_conv_fits(L.cout, H, W, epi) && (L.mfma == 2 || (W >= 16 && L.cw0 + L.cw1 >= 2));
 }
 
 struct Workspace {

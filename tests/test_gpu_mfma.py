@@ -54,13 +54,17 @@ def _check_stages(eng, model, x):
 
 # (seed, base, N, H, W): patches of several tiles (64x64, 96x64 and its
 # 48x32 level), whole-patch tiles with a partial last tile (8x8 levels, N
-# odd), an odd number of input words (base 24: 96 -> 192 channels at 8x8)
+# odd), an odd number of input words (base 24: 96 -> 192 channels at 8x8),
+# rows wider than 64 in tiles of 32 columns (base 64 at 64x256: levels 256
+# and 128 wide, with pools and concats, and a 4x16 bottleneck in tiles of
+# four whole patches)
 @pytest.mark.parametrize("seed,base,N,H,W", [
     (21, 32, 2, 64, 64),
     (22, 32, 3, 32, 32),
     (23, 16, 3, 32, 32),
     (24, 24, 1, 64, 64),
     (25, 32, 1, 96, 64),
+    (26, 64, 1, 64, 256),
 ])
 def test_forced_mfma_stages_vs_checker(tmp_path, orc, monkeypatch, seed, base, N, H, W):
     monkeypatch.setenv("BNN_BCONV_MFMA", "2")
@@ -77,8 +81,8 @@ def test_forced_mfma_stages_vs_checker(tmp_path, orc, monkeypatch, seed, base, N
 
 
 def test_default_rule_picks_wide_layers(tmp_path, orc, monkeypatch):
-    """Default: the matrix cores for fold and pool layers with cout % 64 == 0
-    and rows 16 to 64 wide."""
+    """Default: the matrix cores for fold and pool layers with cout % 64 == 0,
+    rows at least 16 wide and at least 64 input channels."""
     monkeypatch.delenv("BNN_BCONV_MFMA", raising=False)
     b = synth.make_blob(seed=26, base=32)
     p = tmp_path / "m.blob"
@@ -87,16 +91,17 @@ def test_default_rule_picks_wide_layers(tmp_path, orc, monkeypatch):
     x = synth.make_input(126, 1, 120, 128, 128)
     ops = _ops(eng, x)
     # base 32 at 128x128: levels 1, 2, 3 are 64, 32 and 16 wide with 64,
-    # 128 and 256 channels; level 0 (128 wide, 32 channels) and the 8 x 8
-    # bottleneck stay on the popcount kernel
-    want = {f"{lv}.c{k}" for lv in ("enc2", "enc3", "enc4", "dec4", "dec3", "dec2") for k in (1, 2)}
+    # 128 and 256 channels; level 0 (128 wide, 32 channels), enc2.c1 (32
+    # input channels) and the 8 x 8 bottleneck stay on the popcount kernel
+    want = {f"{lv}.c{k}" for lv in ("enc2", "enc3", "enc4", "dec4", "dec3", "dec2") for k in (1, 2)} - {"enc2.c1"}
     got = {lab for lab, op in ops.items() if op.endswith("_mfma")}
     assert got == want, (got, ops)
     _check_stages(eng, orc.parse(B.to_bytes(b)), x)
     eng.close()
 
 
-@pytest.mark.parametrize("N,H,W,c", [(1024, 32, 32, 128), (5, 8, 8, 64), (3, 16, 16, 256), (2, 64, 64, 64)])
+@pytest.mark.parametrize("N,H,W,c", [(1024, 32, 32, 128), (5, 8, 8, 64), (3, 16, 16, 256), (2, 64, 64, 64),
+                                     (2, 32, 128, 64), (1, 16, 256, 128)])
 def test_layer_fold_pool_matches_popcount(monkeypatch, N, H, W, c):
     import torch
     a = synth.make_bits(40 + c, N, H, W, c)
