@@ -413,12 +413,20 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
       // channel (0 in the other lanes)
       float hx[8];
       if constexpr (HALO) {
+        // every lane reads (the slot holds 128 channels, so every address
+        // is inside it), then selects: left to itself the compiler moves
+        // each read under its lane condition, eight branches that each wait
+        // for their read
         const float* hrow = hal + (size_t)(yi % kHS) * (kHaloSlot / 4);
+        float2 hv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = *reinterpret_cast<const float2*>(&hrow[2 * (cpw * wv + 4 * j + gq)]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(hv[j].x), "+v"(hv[j].y));
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float2 v = *reinterpret_cast<const float2*>(&hrow[2 * (cpw * wv + 4 * j + gq)]);
           const bool ok = ((GUARD || j == 7) ? ((jvalid >> j) & 1u) != 0 : true) && (p == 0 || p == 15);
-          hx[j] = ok ? (p == 0 ? v.x : v.y) : 0.0f;
+          hx[j] = ok ? (p == 0 ? hv[j].x : hv[j].y) : 0.0f;
         }
       }
       // the wave's largest |x| (max ignores a NaN, which reaches v' and A as
