@@ -1306,17 +1306,17 @@ template <int MT, int COG, int EPI, bool DUMP>
 __global__ __launch_bounds__(kBlock) void k_bconv(const BconvArgs a, uint32_t bytes0, uint32_t bytes1) {
   constexpr int NP = MT + 2;
   // Block order.  Plain: group g of tile block t is block g * ntb + t.
-  // XCD-aware (a.xorder, for outputs of two or more words per pixel):
+  // XCD-aware (a.xorder, for outputs in two or more channel groups):
   // consecutive blocks go to the 8 XCDs in turn, so block b runs on XCD
   // b % 8, and its index j = b / 8 there walks (tile block, channel group)
   // with the group fastest, tile block (j / ngroups) * 8 + b % 8.  Every
   // group of a tile block then runs on one XCD, one after the other, and
   // the pieces of a pixel's output words they write merge in that XCD's L2:
   // in the plain order they left L2 as separate partial writes, 8x the
-  // output bytes for 128 channels in groups of 16.  (Tile blocks are padded
-  // to a multiple of 8; a tile past the end is inactive.)  With one output
-  // word per pixel the plain order is kept: there the groups' byte stores
-  // to the same words at the same moment measured slower.
+  // output bytes for 128 channels in groups of 16, and 2x for one word per
+  // pixel in two groups (config 4's enc1.c2: the same time in either order,
+  // as are the v1 and v3 forwards).  (Tile blocks are padded to a multiple
+  // of 8; a tile past the end is inactive.)
   const uint32_t ngroups = (uint32_t)(a.cout + COG - 1) / COG;
   uint32_t gidx, tile;
   if (a.xorder) {
@@ -2145,7 +2145,7 @@ hipError_t go_bconv(BconvArgs a, hipStream_t s) {
   const uint32_t b1 = a.in1 ? (uint32_t)((size_t)(nrel * a.h1 * a.w1 + (a.padoff != 0x80000000u ? 1 : 0)) *
                                          a.cw1 * 4)
                             : 0u;
-  a.xorder = (a.cwo >= 2 && groups > 1 && EPI != EPI_P) ? 1 : 0;
+  a.xorder = (groups > 1 && EPI != EPI_P) ? 1 : 0;
   const uint64_t nblocks = (uint64_t)(a.xorder ? (blocks_for((long)ntiles) + 7) & ~7u : blocks_for((long)ntiles)) *
                            groups;
   if (nblocks >= 0x80000000ull) return hipErrorInvalidValue;
