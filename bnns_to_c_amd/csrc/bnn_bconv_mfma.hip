@@ -36,7 +36,8 @@ namespace {
 // while chunk c is consumed, and its words are loaded from HBM one chunk
 // earlier.  A (the same for the block's four waves) goes through LDS too:
 // each K step's 64 channels x 64 bytes are loaded once per block (16 bytes
-// a thread, two steps ahead of their use) into a ring of three slots, one
+// a thread, four steps ahead of their use and two ahead of their store;
+// one step ahead of the store measured 1-3% slower) into a ring of three slots, one
 // barrier per K step, and each wave reads the next step's A from its slot
 // while the current step's matrix ops run.  (Read straight from the weight
 // table by every wave, A was the layer's bottleneck: the four waves'
@@ -259,7 +260,8 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
   };
   a_store(0, a_load(it, 0));
   a_store(1, a_load_ahead(1));
-  i32x4v ag = a_load_ahead(2);  // A of step S + 2, stored during step S
+  i32x4v ag = a_load_ahead(2);   // A of step S + 2, stored during step S
+  i32x4v ag2 = a_load_ahead(3);  // A of step S + 3
   __syncthreads();
   i32x4v Ar[4];
   a_read(0, Ar);
@@ -284,9 +286,10 @@ __global__ __launch_bounds__(256) void k_bconv_mfma(const BconvArgs a, const int
 #pragma unroll
           for (int m = 0; m < 4; ++m) acc[m][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Ar[m], B, acc[m][g], 0, 0, 0);
         }
-        // A of step S + 2 into its slot, the load of step S + 3
+        // A of step S + 2 into its slot, the load of step S + 4
         a_store(s2, ag);
-        ag = a_load_ahead(c * 9 + t + 3);
+        ag = ag2;
+        ag2 = a_load_ahead(c * 9 + t + 4);
 #pragma unroll
         for (int m = 0; m < 4; ++m) Ar[m] = An[m];
         ++S;
