@@ -276,7 +276,9 @@ def cert_adversarial(torch, np, engine, blob, synth, td, sp, N, H, W):
             exactly on one integer sum, so csrc/bnn_fold.c:62-77 sits on
             z = 0 for about one output in a hundred;
       nan   a quarter of the patches all NaN, the others with a NaN block in
-            every band (NaN windows are decided without a recompute)."""
+            every band (NaN windows are decided without a recompute);
+      inf   one +inf per patch (band 7, pixel (16, 16)): its wave-row's bound
+            is infinite, so every output of those rows is recomputed."""
     res = {}
 
     def run(tag, b, x):
@@ -301,6 +303,9 @@ def cert_adversarial(torch, np, engine, blob, synth, td, sp, N, H, W):
     xn[: N // 4] = np.nan
     xn[N // 4:, :, 8:16, 10:22] = np.nan
     run("nan", b, xn)
+    xi = synth.make_input(1, N, 120, H, W)
+    xi[:, 7, H // 2, W // 2] = np.inf
+    run("inf", b, xi)
     # ties: the fold's B from one of patch 0's own conv outputs per channel
     bt = synth.make_blob(seed=41)
     xt = np.random.default_rng(42).choice(np.array([-1.0, 1.0], np.float32), size=(N, 120, H, W))
@@ -869,9 +874,9 @@ def main() -> int:
                       "host_note": "host cube in, host map out: strips through pinned buffers over PCIe",
                       "kernels": scene_kern},
             "cert_adversarial": {"config": f"the headline batch ({N} patches 32x32x120): the certified first conv "
-                                           "on N(0,1) patches, on patches with NaNs, and on +-1 bands with each "
-                                           "channel's fold placed on an integer tap sum (about 1% of outputs on "
-                                           "the fold's switch point)",
+                                           "on N(0,1) patches, on patches with NaNs, on patches with one +inf "
+                                           "each, and on +-1 bands with each channel's fold placed on an integer "
+                                           "tap sum (about 1% of outputs on the fold's switch point)",
                                  **adversarial},
             "v2_stem": {"config": "v2 spectral-stem model, 16-channel 1x1 stem, base 16, 32x32x120, batch 1024",
                         "ms_per_step": round(v2_ms, 5), "patches_s": round(N / v2_ms * 1e3, 1),

@@ -119,6 +119,10 @@ __device__ __forceinline__ void lane_up_h(const cert_u32x4& a, const cert_u32x4&
 
 __device__ __forceinline__ float f32_of(uint32_t b) { return __builtin_bit_cast(float, b); }
 __device__ __forceinline__ uint32_t bits_of(float f) { return __builtin_bit_cast(uint32_t, f); }
+// the number of set bits of m below this lane
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 
 // the reference's real fold of tap sum v (csrc/bnn_fold.c:62-77, A * o + B
 // fused as the reference build does); z is the value before the PReLU branch
@@ -633,32 +637,56 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
           nund += (uint32_t)(__builtin_popcountll(um[g][0]) + __builtin_popcountll(um[g][1]));
       }
 
-      // uncertain outputs: the reference's order, lane t < 9 summing tap t
-      // over the channels from the LDS rows r - 1 .. r + 1
+      // uncertain outputs: the reference's order, up to seven at a time,
+      // lane t < 63 summing tap t % 9 of output t / 9 over the channels from
+      // the LDS rows r - 1 .. r + 1 (a row reached by an infinity leaves
+      // all its outputs undecided; seven per pass keep 63 of the 64 lanes
+      // busy)
+      constexpr int kRb = 7;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
       while (um[g][0] | um[g][1]) {
-        const int which = um[g][0] ? 0 : 1;
-        const int li = __builtin_ctzll(um[g][which]);
-        um[g][which] &= um[g][which] - 1;
+        // the batch: the first kRb pending outputs in the order word 0 then
+        // word 1 (lane j holds bit j of each), output k's position li + 64
+        // which sent to lane k by a forward permute (lanes outside the batch
+        // send to lane 63, which no batch reaches)
+        // (the lane index is re-derived here, so that none of the batch's
+        // lane arithmetic is hoisted into registers held across the row loop)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const uint64_t u0 = um[g][0], u1 = um[g][1];
+        const int p0 = __builtin_popcountll(u0);
+        const int nb = min(kRb, p0 + __builtin_popcountll(u1));
+        const int r0 = mbcnt64(u0), r1 = p0 + mbcnt64(u1);
+        const bool t0 = ((u0 >> ln) & 1u) && r0 < kRb;
+        const bool t1 = ((u1 >> ln) & 1u) && r1 < kRb;
+        const int v0 = __builtin_amdgcn_ds_permute((t0 ? r0 : 63) << 2, ln);
+        const int v1 = __builtin_amdgcn_ds_permute((t1 ? r1 : 63) << 2, ln + 64);
+        const uint64_t c0 = __ballot(t0), c1 = __ballot(t1);
+        um[g][0] = u0 & ~c0;
+        um[g][1] = u1 & ~c1;
+        const int ko = ln < p0 ? v0 : v1;  // lane k < nb: output k
+        const int kk = ln / 9, tap = ln - 9 * kk;
+        const int mo = __builtin_amdgcn_ds_bpermute(kk << 2, ko);
+        const int which = mo >> 6, li = mo & 63;
         const int upx = 8 * wv + 2 * (li >> 4) + which;
         float st = 0.0f;
-        const int ky = lane / 3, kx = lane - 3 * (lane / 3);
+        const int ky = tap / 3, kx = tap - 3 * (tap / 3);
         const int iy = r + ky - 1, ix = upx + kx - 1;
-        if (lane < 9 && iy >= 0 && iy < H && wx0 + ix >= 0 && wx0 + ix < W) {
-          // lane t sums tap t: its four sign-mask words, then the channels
-          // in batches of 32 read ahead of their adds (channels 4 m, 4 m + 3
-          // at column offset c0, 4 m + 1, 4 m + 2 at the swapped one, as
-          // row_off lays them out).  A last partial batch reads up to 28
-          // channels past cin, inside the block's LDS (a row buffer holds
-          // at least cin channels and 11 KiB of partials follow the ring),
-          // and adds +0 for them, which leaves a sum that started at +0
-          // unchanged.  HALO: a column outside the window (-1 or 32) reads
-          // the row's halo, [channel][side] (G = 1), or global memory
+        if (kk < nb && iy >= 0 && iy < H && wx0 + ix >= 0 && wx0 + ix < W) {
+          // lane t sums tap t % 9: its four sign-mask words, then the
+          // channels in batches of 32 read ahead of their adds (channels
+          // 4 m, 4 m + 3 at column offset c0, 4 m + 1, 4 m + 2 at the
+          // swapped one, as row_off lays them out).  A last partial batch
+          // reads up to 28 channels past cin, inside the block's LDS (a row
+          // buffer holds at least cin channels and 11 KiB of partials follow
+          // the ring), and adds +0 for them, which leaves a sum that started
+          // at +0 unchanged.  HALO: a column outside the window (-1 or 32)
+          // reads the row's halo, [channel][side] (G = 1), or global memory
           // (G = 2), instead.
-          const uint4 m4 = G == 1 ? *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + lane) * 4])
+          const uint4 m4 = G == 1 ? *reinterpret_cast<const uint4*>(&wsl[((li & 15) * 9 + tap) * 4])
                                   : *reinterpret_cast<const uint4*>(
-                                        &a.cws[(((size_t)(grp * G + g) * 16 + (li & 15)) * 9 + lane) * 4]);
+                                        &a.cws[(((size_t)(grp * G + g) * 16 + (li & 15)) * 9 + tap) * 4]);
           const bool hcol = HALO && (ix < 0 || ix > 31);
           const int ixr = hcol ? 0 : ix;
           const float* rowp = cert_lds + (size_t)(iy % kCertRing) * rb / 4;
@@ -708,14 +736,34 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
             }
           }
         }
+        // lane k < nb: output k's taps in order from lanes 9 k .. 9 k + 8,
+        // folded with its channel's parameters, the bit then pulled back by
+        // the lane of its position
+        const int lc = ko & 15;
         float tot = 0.0f;
+        const int tb = ln < kRb ? 36 * ln : 0;  // lane 9 k's byte address, k < kRb
 #pragma unroll
-        for (int t = 0; t < 9; ++t) tot = __fadd_rn(tot, f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(st), t)));
-        // the fold parameters of lane li's channel
-        const int lc = li & 15;
+        for (int t = 0; t < 9; ++t)
+          tot = __fadd_rn(tot, f32_of((uint32_t)__builtin_amdgcn_ds_bpermute(tb + 4 * t, (int)bits_of(st))));
+        float pv[5];
+#pragma unroll
+        for (int q = 0; q < 5; ++q) {
+          if constexpr (G == 1) {
+            const float rv[5] = {r_al, r_A, r_B, r_sl, r_rs};
+            pv[q] = f32_of((uint32_t)__builtin_amdgcn_ds_bpermute(lc << 2, (int)bits_of(rv[q])));  // lane c holds channel c
+          } else {
+            pv[q] = fpar[q * 32 + 16 * g + lc];
+          }
+        }
         float zz;
-        const bool ub = fold_bit(tot, fp_ch(0, g, lc), fp_ch(1, g, lc), fp_ch(2, g, lc), fp_ch(3, g, lc), fp_ch(4, g, lc), zz);
-        bm[g][which] = ub ? (bm[g][which] | (1ull << li)) : (bm[g][which] & ~(1ull << li));
+        const int ub = ln < nb && fold_bit(tot, pv[0], pv[1], pv[2], pv[3], pv[4], zz) ? 1 : 0;
+        // (every lane runs the permutes: a lane outside EXEC reads as 0)
+        const int b0 = __builtin_amdgcn_ds_bpermute((r0 & 63) << 2, ub);
+        const int b1 = __builtin_amdgcn_ds_bpermute((r1 & 63) << 2, ub);
+        const uint64_t s0 = __ballot(t0 && b0);
+        const uint64_t s1 = __ballot(t1 && b1);
+        bm[g][0] = (bm[g][0] & ~c0) | s0;
+        bm[g][1] = (bm[g][1] & ~c1) | s1;
       }
       }
 

@@ -130,6 +130,26 @@ def test_cert_wide_edges_nonfinite(tmp_path, orc, base):
     eng.close()
 
 
+@pytest.mark.parametrize("base,H,W", [(16, 20, 32), (32, 20, 32), (16, 16, 72), (32, 16, 72)])
+def test_cert_dense_infinities(tmp_path, orc, base, H, W):
+    """Infinities of both signs on a grid (every third row and column in one
+    band, one sample of each sign, one mixed), so that every output row has
+    far more undecided outputs than one recompute batch of seven takes, in
+    both 64-pixel halves of a wave and at the tile edges of wide rows; a
+    window holding both signs sums to NaN."""
+    b = synth.make_blob(seed=49, base=base)
+    rng = np.random.default_rng(50)
+    x = rng.standard_normal((3, 120, H, W), dtype=np.float32)
+    x[0, 11, ::3, ::3] = np.inf
+    x[1, 60, 1::3, ::3] = -np.inf
+    x[2, 2, ::3, ::3] = np.inf
+    x[2, 90, ::3, 1::3] = -np.inf
+    model = orc.parse(B.to_bytes(b))
+    eng = _engine(tmp_path, b)
+    _check(eng, model, x)
+    eng.close()
+
+
 @pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16),
                                        (16, 16, 72), (8, 20, 100), (32, 16, 256), (16, 36, 36)])
 def test_cert_shapes(tmp_path, orc, base, H, W):
