@@ -468,9 +468,10 @@ struct BnnDevice {
   size_t strip_in_cap[2] = {}, strip_out_cap[2] = {};
   hipStream_t copy = nullptr;
   hipEvent_t ev_copied[2] = {}, ev_free[2] = {}, ev_done[2] = {};
-  // the later parts of a large batch run their binary layers on these streams
+  // the parts of a large batch before the last run their binary layers on
+  // these streams, each from the event after its first conv
   hipStream_t side[kSplitMax - 1] = {};
-  hipEvent_t ev_fork = nullptr, ev_join[kSplitMax - 1] = {};
+  hipEvent_t ev_conv[kSplitMax - 1] = {}, ev_join[kSplitMax - 1] = {};
   // this device's copy of `scratch` (bnn_forward_device_noalloc), null if
   // its address could not be looked up (scratch_err says why)
   uint8_t* scratch = nullptr;
@@ -656,8 +657,8 @@ void release(BnnDevice* D) {
     if (D->ev_done[k]) (void)hipEventDestroy(D->ev_done[k]);
   }
   if (D->copy) (void)hipStreamDestroy(D->copy);
-  if (D->ev_fork) (void)hipEventDestroy(D->ev_fork);
   for (int k = 0; k < kSplitMax - 1; ++k) {
+    if (D->ev_conv[k]) (void)hipEventDestroy(D->ev_conv[k]);
     if (D->ev_join[k]) (void)hipEventDestroy(D->ev_join[k]);
     if (D->side[k]) (void)hipStreamDestroy(D->side[k]);
   }
@@ -1039,8 +1040,10 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   static const char* enc_c2[4] = {"enc1.c2", "enc2.c2", "enc3.c2", "enc4.c2"};
   static const char* dec_c1[4] = {"dec4.c1", "dec3.c1", "dec2.c1", "dec1.c1"};
   static const char* dec_c2[4] = {"dec4.c2", "dec3.c2", "dec2.c2", "dec1.c2"};
+  int stage = 3;  // what part() enqueues: 1 the first conv, 2 the binary layers
   auto part = [&]() -> int {
-  if ((rc = first_conv())) return rc;
+  if ((stage & 1) && (rc = first_conv())) return rc;
+  if (!(stage & 2)) return BNN_OK;
   const uint32_t* x = w.a1;
   for (int i = 0; i < (use_ext ? 1 : use_mid ? 2 : 4); ++i) {
     const uint32_t* hin = x;
@@ -1091,12 +1094,20 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   }
   return BNN_OK;
   };
-  // A large plain batch runs as parts on parallel streams: the binary
-  // layers are short and latency bound (launch, ramp and drain are a large
-  // part of each kernel), and independent chains keep each other's gaps
-  // filled; each part's first conv runs on its own stream too, so one part's
-  // binary layers start while the other's first conv drains.  A scene splits
-  // at whole patch rows.  One stream with per-kernel events or debug dumps.
+  // A large plain batch runs as parts: the binary layers are short and
+  // latency bound (launch, ramp and drain are a large part of each kernel),
+  // and independent chains keep each other's gaps filled.  Every part's
+  // first conv runs on the caller's stream, one after the other (each fills
+  // the GPU); a part before the last runs its binary layers on a side stream
+  // from the event after its conv, beside the next part's conv, and the last
+  // part's layers follow on the caller's stream, which then waits for the
+  // side streams.  A forward so begins and ends on the caller's stream, and
+  // the next one's first conv follows its last kernel with no wait across
+  // streams on the way (with the first conv of the last part on a side
+  // stream instead, the wait for it at the end and for the caller's stream
+  // at the start left the GPU idle for 17 us a forward at batch 1024).  A
+  // scene splits at whole patch rows.  One stream with per-kernel events or
+  // debug dumps.
   int parts = 1;
   if (!dump && !evs)
     while (parts < std::min(kSplitMax, max_parts) && N >= kSplitMin * parts * 2) parts *= 2;
@@ -1104,38 +1115,56 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
   const int unit = sc ? sc->pcols : 1;
   if (sc && N / unit < parts) parts = 1;
   if (parts == 1) return part();
-  if (!D->ev_fork) {
+  if (!D->ev_conv[0]) {
     // all or nothing: a failure leaves no half-made set behind
     hipStream_t side[kSplitMax - 1] = {};
-    hipEvent_t fork = nullptr, join[kSplitMax - 1] = {};
-    bool ok = hipEventCreateWithFlags(&fork, hipEventDisableTiming) == hipSuccess;
+    hipEvent_t conv[kSplitMax - 1] = {}, join[kSplitMax - 1] = {};
+    // (the conv event orders two streams of this GPU only: the consumer
+    // kernels see the conv's output through its own device-scope release,
+    // so the event skips the system-scope fence, which cost the caller's
+    // stream about 2 us a forward; the join event keeps it, since the
+    // caller may read the side streams' logits from the host)
+    bool ok = true;
     for (int k = 0; ok && k < kSplitMax - 1; ++k)
       ok = hipStreamCreateWithFlags(&side[k], hipStreamNonBlocking) == hipSuccess &&
+           hipEventCreateWithFlags(&conv[k], hipEventDisableTiming | hipEventDisableSystemFence) == hipSuccess &&
            hipEventCreateWithFlags(&join[k], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
-      if (fork) (void)hipEventDestroy(fork);
       for (int k = 0; k < kSplitMax - 1; ++k) {
+        if (conv[k]) (void)hipEventDestroy(conv[k]);
         if (join[k]) (void)hipEventDestroy(join[k]);
         if (side[k]) (void)hipStreamDestroy(side[k]);
       }
       return set_err(BNN_EHIP, "cannot create the streams of a split batch");
     }
-    D->ev_fork = fork;
-    for (int k = 0; k < kSplitMax - 1; ++k) { D->side[k] = side[k]; D->ev_join[k] = join[k]; }
+    for (int k = 0; k < kSplitMax - 1; ++k) {
+      D->side[k] = side[k];
+      D->ev_conv[k] = conv[k];
+      D->ev_join[k] = join[k];
+    }
   }
-  HIP_TRY(hipEventRecord(D->ev_fork, s));
-  for (int k = 1; k < parts; ++k) HIP_TRY(hipStreamWaitEvent(D->side[k - 1], D->ev_fork, 0));
+  const int rows = N / unit;
   for (int k = 0; k < parts; ++k) {
-    const int rows = N / unit;
     nb = (int)((long)rows * k / parts) * unit;
     cnt = (k + 1 == parts ? N : (int)((long)rows * (k + 1) / parts) * unit) - nb;
-    st = k ? D->side[k - 1] : s;
     use_ext = ext_ok && k + 1 == parts && cnt >= kMidExtMin;
+    st = s;
+    if (k + 1 == parts) {
+      stage = 3;
+      if ((rc = part())) return rc;
+      break;
+    }
+    stage = 1;
+    if ((rc = part())) return rc;
+    HIP_TRY(hipEventRecord(D->ev_conv[k], s));
+    HIP_TRY(hipStreamWaitEvent(D->side[k], D->ev_conv[k], 0));
+    st = D->side[k];
+    stage = 2;
     if ((rc = part())) return rc;
   }
-  for (int k = 1; k < parts; ++k) {
-    HIP_TRY(hipEventRecord(D->ev_join[k - 1], D->side[k - 1]));
-    HIP_TRY(hipStreamWaitEvent(s, D->ev_join[k - 1], 0));
+  for (int k = 0; k + 1 < parts; ++k) {
+    HIP_TRY(hipEventRecord(D->ev_join[k], D->side[k]));
+    HIP_TRY(hipStreamWaitEvent(s, D->ev_join[k], 0));
   }
   return BNN_OK;
 }
