@@ -496,7 +496,9 @@ int enqueue_forward(const ModelR* m, BnnReactDevice* D, RWorkspace& w, const flo
   auto mark = [&](const char* label, const char* optype, double oe, double taps) -> int {
     if (!evs) return BNN_OK;
     hipEvent_t e;
-    HIP_TRY(hipEventCreate(&e));
+    // a timing-only event: no system-scope fence (which would add its own
+    // cache writeback to the interval between two kernels)
+    HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     HIP_TRY(hipEventRecord(e, s));
     evs->push_back(e);
     if (label) ops->push_back({label, optype, oe, taps});
