@@ -41,7 +41,10 @@ before each other configuration.  Prints ONE JSON line on stdout:
                 64x64, batch 256, int32 P out: binary-op/s against the
                 VALU-popcount roofline and the HBM rate of its bytes
   fused_pool    the isolated fused bconv+fold+maxpool kernel at 128->128,
-                32x32, batch 1024 (the benchmark's fused-kernel config)
+                32x32, batch 1024 (the benchmark's fused-kernel config):
+                the kernel the default rule takes (the int8 matrix cores)
+                against the int8 peak, and the bit-packed popcount kernel
+                (BNN_BCONV_MFMA=0) against the VALU-popcount peak
   cfg4          benchmark config 4: 256x256x120 patches, batch 64, base 32;
                 per-kernel times, the int8 matrix-core convs against the
                 dense int8 peak
@@ -544,6 +547,35 @@ def main() -> int:
         pool_peak = "int8 matrix peak" if pool_mfma else "VALU popcount peak"
         log(f"fused bconv+fold+pool 128->128 32x32 b{N}: {pool_ms * 1e3:.1f} us, frac {pool_frac:.3f} of {pool_peak}")
         L.close()
+        pool_pc = None
+        if pool_mfma:
+            # the same layer on the bit-packed popcount kernel (the mode is
+            # read when a layer is made), against the VALU-popcount peak
+            old = os.environ.get("BNN_BCONV_MFMA")
+            os.environ["BNN_BCONV_MFMA"] = "0"
+            try:
+                Lp = engine.ConvLayer(blob.pack_kidx(w), C, C, synth.make_thresholds(32, C, 288),
+                                      synth.make_thresholds(33, C, 288))
+            finally:
+                if old is None:
+                    os.environ.pop("BNN_BCONV_MFMA", None)
+                else:
+                    os.environ["BNN_BCONV_MFMA"] = old
+            settle(lambda: Lp.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp), torch)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(reps):
+                Lp.fold_pool_device(act.data_ptr(), N, H, W, skip.data_ptr(), down.data_ptr(), sp)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            pc_ms = e0.elapsed_time(e1) / reps
+            pc_rate = 2 * pool_bitmacs / (pc_ms / 1e3)
+            pool_pc = {"kernel": "k_bconv (VALU popcount, BNN_BCONV_MFMA=0)", "us": round(pc_ms * 1e3, 2),
+                       "binary_op_s": round(pc_rate, 1), "frac": round(pc_rate / valu_binop_peak(), 4),
+                       "frac_of": "VALU popcount peak"}
+            log(f"  the same on the popcount kernel: {pc_ms * 1e3:.1f} us, frac {pc_rate / valu_binop_peak():.3f} "
+                f"of the VALU popcount peak")
+            Lp.close()
 
         cfg4_ms, cfg4_kern, N4, p4, S4 = bench_cfg4(sp, stream, td)
 
@@ -904,7 +936,8 @@ def main() -> int:
             "fused_pool": {"config": "bconv 128->128 + fold + 2x2 maxpool + fold, 32x32, batch 1024",
                            "us": round(pool_ms * 1e3, 2), "binary_op_s": round(pool_rate, 1),
                            "kernel": "k_bconv_mfma (int8 matrix cores)" if pool_mfma else "k_bconv (VALU popcount)",
-                           "frac": round(pool_frac, 4), "frac_of": pool_peak},
+                           "frac": round(pool_frac, 4), "frac_of": pool_peak,
+                           **({"popcount": pool_pc} if pool_pc else {})},
             "cfg4": {"config": "large tiles: 256x256x120, batch 64, base 32 (512 channels at the bottleneck)",
                      "ms_per_step": round(cfg4_ms, 4), "patches_s": round(N4 / cfg4_ms * 1e3, 1),
                      "kernels": cfg4_kern,
