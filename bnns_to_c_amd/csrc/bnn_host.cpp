@@ -1146,9 +1146,22 @@ int enqueue_forward(const Model* m, BnnDevice* D, Workspace& w, const float* d_i
     }
   }
   const int rows = N / unit;
+  // Where two parts meet: at half the batch, or, when the certified first
+  // conv runs and the batch is at most one and a half of its rounds (the
+  // patches whose blocks it holds at once), after one whole round, so that
+  // the second part's conv, at most half a round, splits its patches' rows
+  // over two or four blocks and takes a fraction of a round's time
+  // (launch_real_cert; config 3's 660 patches as 506 + 154 instead of two
+  // half-full rounds of 330)
+  long cut = rows / 2;
+  if (parts == 2 && !D->stem && D->cert && real_cert_fits(D->rcin, W, sc ? sc->sW : W) &&
+      (uintptr_t)d_in % 16 == 0) {
+    const long round = real_cert_round(D->rcin, D->rcout, W) / unit;
+    if (round > 0 && rows > round && 2 * (rows - round) <= round) cut = round;
+  }
   for (int k = 0; k < parts; ++k) {
-    nb = (int)((long)rows * k / parts) * unit;
-    cnt = (k + 1 == parts ? N : (int)((long)rows * (k + 1) / parts) * unit) - nb;
+    nb = parts == 2 ? (int)(k ? cut : 0) * unit : (int)((long)rows * k / parts) * unit;
+    cnt = (k + 1 == parts ? N : parts == 2 ? (int)cut * unit : (int)((long)rows * (k + 1) / parts) * unit) - nb;
     use_ext = ext_ok && k + 1 == parts && cnt >= kMidExtMin;
     st = s;
     if (k + 1 == parts) {

@@ -137,6 +137,8 @@ struct RealArgs {
   float* hout;          // h planes [cout][N*H*W]; of ntot patches when ntot > 0 (a batch part)
   int ntot;
   float* f32b;          // projection output [N][cout][H][W]; may be null
+  // certified kernel: row parts per patch (launch_real_cert sets it)
+  int rsplit;
 };
 
 // Real-conv work split: output channels per lane group and output rows per
@@ -561,6 +563,9 @@ hipError_t launch_mid(const MidArgs& a, bool dump, hipStream_t s);
 
 // the certified first conv (bits only; RealArgs with cwb, cws, out, no f32)
 hipError_t launch_real_cert(const RealArgs& a, hipStream_t s);
+// how many patches of this shape one round of the certified kernel holds
+// (its blocks resident on the device at once), 0 if it cannot tell
+long real_cert_round(int cin, int cout, int W);
 
 // The 1x1 head as its own kernel (heads over more than 32 channels, which
 // one epilogue group cannot hold): input the head layer's packed bits

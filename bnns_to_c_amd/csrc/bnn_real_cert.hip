@@ -224,11 +224,18 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   // XCD's L2
   // (one block per patch keeps the plain order)
   const int ng = (a.cout + 16 * G - 1) / (16 * G);  // blocks per tile
-  const bool xorder = ng > 1 || ntile > 1 || G > 1;
+  // a launch of fewer patches than a round of the device holds splits each
+  // patch's rows into S parts, one block each (launch_real_cert)
+  const int S = a.rsplit > 1 ? a.rsplit : 1;
+  const bool xorder = ng > 1 || ntile > 1 || G > 1 || S > 1;
   const uint32_t item = xorder ? (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   if (item >= nitems) return;
-  const int grp = (int)(item % (uint32_t)ng), tt = (int)(item / (uint32_t)ng);
+  const uint32_t q = item / (uint32_t)ng;
+  const int grp = (int)(item - q * (uint32_t)ng), rp = (int)(q % (uint32_t)S), tt = (int)(q / (uint32_t)S);
   const int n = tt / ntile, tile = tt - n * ntile;
+  // output rows [y0, y1) of the patch, from input rows ys = y0 - 1 (or 0)
+  // to y1 (or H - 1)
+  const int rh = (H + S - 1) / S, y0 = rp * rh, y1 = min(H, y0 + rh), ys = max(0, y0 - 1);
   const int wx0 = HALO ? 32 * tile : 0;  // image column of window column 0
   const int vhi = HALO ? min(32, W - wx0) : W;  // output window columns 0 .. vhi - 1
   const uint32_t rb = (uint32_t)nld * 1024u;  // bytes per row buffer
@@ -350,22 +357,13 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
 #pragma unroll
     for (int k = 0; k < 9; ++k) fpar[k * 32 + tid] = src[k][co];
   }
-  // parameter k of group g for the lane's own channel, and for channel c
-  // of the group (the same in every lane)
+  // parameter k of group g for the lane's own channel
   auto fp_own = [&](int k, int g) __attribute__((always_inline)) -> float {
     if constexpr (G == 1) {
       const float rv[9] = {r_al, r_A, r_B, r_sl, r_rs, r_t1, r_t2, r_dc, r_b0};
       return rv[k];
     } else {
       return fpar[k * 32 + 16 * g + fc];
-    }
-  };
-  auto fp_ch = [&](int k, int g, int c) __attribute__((always_inline)) -> float {
-    if constexpr (G == 1) {
-      const float rv[9] = {r_al, r_A, r_B, r_sl, r_rs, r_t1, r_t2, r_dc, r_b0};
-      return f32_of((uint32_t)__builtin_amdgcn_readlane((int)bits_of(rv[k]), c));  // lane c holds channel c
-    } else {
-      return fpar[k * 32 + 16 * g + c];
     }
   };
   // 2^-24 (1 + 2^-9 + 2^-19) times the weighted window sum: the 2^-9 covers
@@ -378,11 +376,11 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   // on) in a wave's partial: segment row group wv, register fq
   const int i0 = part_idx(0, wv, fc) + fq;
 
-  issue(0);
+  issue(ys);
 
-  // rolling state, indexed by row mod 3: acc[r % 3] the partial of output
-  // row r, ab[y % 3] / qr[y % 3] the window sums and Q of input row y.  The
-  // row loop is unrolled by three so that every index is a constant.
+  // rolling state, rotated at the end of every step: at step yi, acc[g][c0]
+  // holds the partial of output row yi, [cn] of yi + 1 and [cp] of yi - 1;
+  // ab / qr the window sums and Q of input rows yi, yi + 1 and yi - 1 alike
   cert_f32x4 acc[G][3][2];
   float ab[3][2], qr[3];
 #pragma unroll
@@ -394,13 +392,13 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
   }
 
   uint32_t nund = 0;  // outputs this wave recomputed
-  for (int yi = 0; yi <= H; ++yi) {
+  for (int yi = ys; yi <= y1; ++yi) {
     constexpr int c0 = 0, cn = 1, cp = 2;  // yi % 3, (yi + 1) % 3, (yi - 1) % 3 after rotation
     const bool has = yi < H;
     // row yi landed, this wave's LDS traffic done, then every wave's
     wait_vm_lgkm<0>();
     block_barrier();
-    if (yi + 1 < H) issue(yi + 1);
+    if (yi + 1 < H && yi + 1 <= y1) issue(yi + 1);
 
     float abn[2] = {0.0f, 0.0f}, qn = 0.0f;
     if (has) {
@@ -550,7 +548,7 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
     ab[c0][1] = abn[1];
     qr[c0] = qn;
 
-    if (yi >= 1) {
+    if (yi > y0) {
       // output row r = yi - 1 is complete in acc[g][cp]: each wave leaves its
       // partials, its window sum of |x| (rows yi - 2, yi - 1, yi) and its
       // quantisation bound in LDS
@@ -803,6 +801,76 @@ void k_real_cert(const RealArgs a, uint32_t xbytes, int nld, uint32_t nitems) {
 
 }  // namespace
 
+namespace {
+
+using CertFn = void (*)(const RealArgs, uint32_t, int, uint32_t);
+const CertFn kCertFns[8] = {k_real_cert<false, false, 1>, k_real_cert<true, false, 1>, k_real_cert<false, true, 1>,
+                            k_real_cert<true, true, 1>,   k_real_cert<false, false, 2>, k_real_cert<true, false, 2>,
+                            k_real_cert<false, true, 2>,  k_real_cert<true, true, 2>};
+
+// A launch's shape: the variant (guard, halo, G = 2 bits), its LDS bytes and
+// work items (blocks of a whole patch) per patch.
+struct CertShape {
+  int var, nld, G;
+  size_t lds;
+  long per_patch;
+};
+CertShape cert_shape(int cin, int cout, int W) {
+  CertShape c{};
+  c.nld = (cin + 7) / 8;
+  const bool guard = cin / 4 < 28, halo = W > 32;
+  // 17 to 32 output channels: both 16-channel groups in one block
+  c.G = cout > 16 && cout <= 32 ? 2 : 1;
+  c.lds = (size_t)kCertRing * c.nld * 1024 + (c.G * 4 * 512 + 4 * 32 + 4 + (c.G == 1 ? 16 * 36 : 0)) * 4 +
+          (halo ? (c.G == 1 ? kCertRing : 2) * kHaloSlot : 0) + (c.G == 2 ? 9 * 32 * 4 : 0);
+  c.var = (guard ? 1 : 0) + (halo ? 2 : 0) + (c.G == 2 ? 4 : 0);
+  c.per_patch = (halo ? (W + 31) / 32 : 1) * (long)((cout + 16 * c.G - 1) / (16 * c.G));
+  return c;
+}
+
+// The kernel asks for more than 64 KiB of LDS: allow it once per variant and
+// device (bit d of the variant's mask for device d).
+hipError_t cert_attr(int var) {
+  static std::atomic<uint64_t> attr[8];
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr[var].load(std::memory_order_acquire) & bit)) {
+    if (hipError_t e =
+            hipFuncSetAttribute((const void*)kCertFns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        e != hipSuccess)
+      return e;
+    attr[var].fetch_or(bit, std::memory_order_acq_rel);
+  }
+  return hipSuccess;
+}
+
+// Blocks of the variant resident on the current device at once (its CUs
+// times the blocks one CU holds at these LDS bytes), cached per variant and
+// row-buffer count (the devices of one process are alike); 0 if unknown.
+long cert_slots(const CertShape& c) {
+  static std::atomic<long> cache[8][17];
+  if (c.nld < 1 || c.nld > 16) return 0;
+  long v = cache[c.var][c.nld].load(std::memory_order_acquire);
+  if (v) return v;
+  int dev = 0, ncu = 0, per_cu = 0;
+  if (cert_attr(c.var) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kCertFns[c.var], 256, c.lds) != hipSuccess)
+    return 0;
+  v = (long)ncu * per_cu;
+  cache[c.var][c.nld].store(v, std::memory_order_release);
+  return v;
+}
+
+}  // namespace
+
+long real_cert_round(int cin, int cout, int W) {
+  const CertShape c = cert_shape(cin, cout, W);
+  const long slots = cert_slots(c);
+  return slots > 0 ? slots / c.per_patch : 0;
+}
+
 hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if ((long)a.N * a.H * a.W <= 0) return hipSuccess;
   if (!a.cwb || !a.cws || !a.ct1 || !a.ct2 || !a.cb0 || !a.cdc || !a.out || a.f32 || a.hout) return hipErrorInvalidValue;
@@ -810,37 +878,26 @@ hipError_t launch_real_cert(const RealArgs& a, hipStream_t s) {
   if (!real_cert_fits(a.cin, a.W, rowlen) || (uintptr_t)a.x % 16) return hipErrorInvalidValue;
   const size_t xbytes = a.pcols > 0 ? (size_t)a.cin * a.sH * a.sW * 4 : (size_t)a.N * a.cin * a.H * a.W * 4;
   if (xbytes >= kCertFar) return hipErrorInvalidValue;
-  const int nld = (a.cin + 7) / 8;
-  const bool guard = a.cin / 4 < 28, halo = a.W > 32;
-  // 17 to 32 output channels: both 16-channel groups in one block
-  const int G = a.cout > 16 && a.cout <= 32 ? 2 : 1;
-  const size_t lds = (size_t)kCertRing * nld * 1024 + (G * 4 * 512 + 4 * 32 + 4 + (G == 1 ? 16 * 36 : 0)) * 4 +
-                     (halo ? (G == 1 ? kCertRing : 2) * kHaloSlot : 0) + (G == 2 ? 9 * 32 * 4 : 0);
-  // the variant's entry and its index (guard, halo, G = 2 bits)
-  using Fn = void (*)(const RealArgs, uint32_t, int, uint32_t);
-  static const Fn fns[8] = {k_real_cert<false, false, 1>, k_real_cert<true, false, 1>, k_real_cert<false, true, 1>,
-                            k_real_cert<true, true, 1>,   k_real_cert<false, false, 2>, k_real_cert<true, false, 2>,
-                            k_real_cert<false, true, 2>,  k_real_cert<true, true, 2>};
-  const int var = (guard ? 1 : 0) + (halo ? 2 : 0) + (G == 2 ? 4 : 0);
-  // the kernel asks for more than 64 KiB of LDS: allow it once per variant
-  // and device (bit d of the variant's mask for device d)
-  static std::atomic<uint64_t> attr[8];
-  int dev = 0;
-  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-  const uint64_t bit = 1ull << (dev & 63);
-  if (!(attr[var].load(std::memory_order_acquire) & bit)) {
-    if (hipError_t e = hipFuncSetAttribute((const void*)fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        e != hipSuccess)
-      return e;
-    attr[var].fetch_or(bit, std::memory_order_acq_rel);
-  }
-  const long ntile = halo ? (a.W + 31) / 32 : 1;
-  const long nitems = (long)a.N * ntile * ((a.cout + 16 * G - 1) / (16 * G));
+  const CertShape c = cert_shape(a.cin, a.cout, a.W);
+  if (hipError_t e = cert_attr(c.var); e != hipSuccess) return e;
+  const long npatch_items = (long)a.N * c.per_patch;
+  // Row parts: a block's time is its row steps (the kernel is latency-bound,
+  // a block alone on its CU takes about as long as two), so a launch that
+  // leaves slots of the round empty splits each patch's rows over S = 2 or 4
+  // blocks while S times the blocks still fit in one round, each part at
+  // least 8 rows (a part re-reads the input row above it: 17 row steps
+  // for half of 32 rows against 33 for all of them)
+  const long slots = cert_slots(c);
+  int S = 1;
+  while (S < 4 && slots > 0 && npatch_items * S * 2 <= slots && a.H / (S * 2) >= 8) S *= 2;
+  const long nitems = npatch_items * S;
   if (nitems >= 0x7FFFFFF0) return hipErrorInvalidValue;
+  RealArgs b = a;
+  b.rsplit = S;
   // a multiple of 8 blocks (one per XCD in turn); the padding ones exit
-  const bool xorder = ntile > 1 || a.cout > 16;
+  const bool xorder = c.per_patch > 1 || a.cout > 16 || S > 1;
   const dim3 grid((unsigned)(xorder ? (nitems + 7) / 8 * 8 : nitems));
-  hipLaunchKernelGGL(fns[var], grid, dim3(256), lds, s, a, (uint32_t)xbytes, nld, (uint32_t)nitems);
+  hipLaunchKernelGGL(kCertFns[c.var], grid, dim3(256), c.lds, s, b, (uint32_t)xbytes, c.nld, (uint32_t)nitems);
   return hipGetLastError();
 }
 

@@ -150,6 +150,28 @@ def test_cert_dense_infinities(tmp_path, orc, base, H, W):
     eng.close()
 
 
+@pytest.mark.parametrize("N,H,W,base", [(100, 33, 32, 16), (200, 32, 32, 16), (250, 20, 32, 16), (60, 47, 44, 16),
+                                         (40, 32, 64, 32), (3, 17, 36, 32)])
+def test_cert_row_parts(tmp_path, orc, N, H, W, base):
+    """A launch of fewer patches than a round of the GPU holds splits each
+    patch's rows over two or four blocks, each starting one input row above
+    its first output row: 100 patches of 33 rows in parts of 9, 9, 9 and 6;
+    200 of 32 in halves; 250 of 20 in halves; tiled rows of 44 and 64 (both
+    16-channel groups in one block at base 32), 17 rows in parts of 9 and 8.
+    Logits of the whole batch bitwise against the order-exact kernel, act1
+    bits and logits of three patches against the checker."""
+    b = synth.make_blob(seed=70 + H, base=base)
+    x = synth.make_input(71 + W, N, 120, H, W)
+    x[N // 2, 40, H // 2, :] = np.inf  # an undecided row in a middle part
+    fast = _engine(tmp_path, b, "a.blob", cert=True)
+    exact = _engine(tmp_path, b, "b.blob", cert=False)
+    assert _bits_equal(fast.forward_batch(x), exact.forward_batch(x))
+    model = orc.parse(B.to_bytes(b))
+    _check(fast, model, x[[0, N // 2, N - 1]])
+    fast.close()
+    exact.close()
+
+
 @pytest.mark.parametrize("base,H,W", [(16, 32, 32), (32, 32, 32), (8, 16, 16), (16, 20, 28), (24, 32, 16),
                                        (16, 16, 72), (8, 20, 100), (32, 16, 256), (16, 36, 36)])
 def test_cert_shapes(tmp_path, orc, base, H, W):
