@@ -447,8 +447,8 @@ def main() -> int:
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: the patch batch shards with no exchange "
-              "(see DESIGN.md), and this build runs on one GPU; use --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: the patch batch would shard across GPUs with no exchange "
+              "between them, and this build runs on one GPU; use --gpus 1", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -725,8 +725,8 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     # an event between consecutive steps on the forward's stream: per-step
-    # times, of which the median is the step time (N / wall time
-    # of one batched forward, median of reps; csrc/main.c:55-61); timing-only
+    # times, of which the median is the step time (the reference's figure: N /
+    # wall time of one batched forward, median of reps; csrc/main.c:55-61); timing-only
     # events with no cache fence of their own (StepEvents)
     evs = StepEvents(args.steps + 1)
     t0 = time.perf_counter()
