@@ -329,6 +329,39 @@ def test_default_stream_is_ordered(tmp_path):
     eng.close()
 
 
+def test_split_forward_graph_capture(tmp_path):
+    """bnn_forward_device of a split batch (600 patches: a full round of the
+    certified conv, then 88 patches in row quarters, the first part's binary
+    layers on the model's side stream) captured in a HIP graph after one
+    eager call, replayed on new inputs with eager work between the replays:
+    every replay bit-identical to the eager forward of the same input."""
+    import torch
+    eng, _ = _engine(tmp_path, synth.make_blob(seed=12))
+    N, H, W = 600, 32, 32
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    x = torch.randn((N, 120, H, W), device="cuda", generator=gen)
+    y = torch.empty((N, 3, H, W), dtype=torch.float32, device="cuda")
+    want = torch.empty_like(y)
+    s = torch.cuda.Stream()
+    eng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        eng.forward_device(x.data_ptr(), N, H, W, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    for r in range(3):
+        print(f"graph replay {r}", flush=True)
+        x.copy_(torch.randn((N, 120, H, W), device="cuda", generator=gen))
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eng.forward_device(x.data_ptr(), N, H, W, want.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32)), r
+    del graph
+    eng.close()
+
+
 def test_batch_past_launch_limit(tmp_path):
     """4400 patches, 2.16 GB of input: more than the 2 GiB one launch
     addresses, so the batch runs as two launches (4369 + 31 patches), from
