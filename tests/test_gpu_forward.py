@@ -246,10 +246,12 @@ def test_cli_matches_reference_cli(tmp_path, golden):
     assert r.returncode == 1 and "cannot open" in r.stderr
 
 
-@pytest.mark.parametrize("N", [256, 300, 1031])
+@pytest.mark.parametrize("N", [256, 300, 513, 768, 769, 1031])
 def test_batch_size_independent(tmp_path, N):
     """Any batch size, including ones that fill the last block partially,
-    gives the same bits for every patch as batches of 64."""
+    gives the same bits for every patch as batches of 64: halves in row
+    parts (256, 300), one full round of the first conv and the rest in row
+    quarters or halves (513, 768), halves in whole rows (769, 1031)."""
     import torch
     b = synth.make_blob(seed=11)
     eng, _ = _engine(tmp_path, b)
