@@ -269,7 +269,14 @@ class StepEvents:
     def __init__(self, n: int):
         import ctypes
         self.C = ctypes
-        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip = None
+        for name in ("libamdhip64.so.7", "libamdhip64.so", "libamdhip64.so.6"):
+            try:
+                self.hip = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        assert self.hip is not None, "the HIP runtime (libamdhip64) is not loadable"
         self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
